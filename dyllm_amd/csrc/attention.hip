@@ -1,0 +1,327 @@
+// Varlen non-causal attention for head_dim 128 on gfx950 MFMA, in three modes:
+//
+//   Dense      -- softmax(Q K^T * scale) V for every query row (the full / refresh step,
+//                 the flash_attn_varlen_func call at attention.py:41-52).
+//   RowSparse  -- the same for a compact list of salient query rows (q_rows) against the
+//                 full cached K/V; output is compact (attention.py:76-87).
+//   ColSparse  -- O = C + softmax(Q K^T / sqrt(D)) dV with PV only on key blocks that hold
+//                 salient rows, plus the saliency statistics of every row; salient rows take
+//                 o_sal instead (attention_ops_kernels_sm80.cu:44-483 together with
+//                 attention_aux_kernels.cu:22-72).
+//
+// Numerics follow the reference: log2-domain online softmax over 64-key blocks, running max
+// initialised to -FLT_MAX, P rounded to bf16 before the PV product while the row sum stays
+// fp32, 1/rowsum as a correctly rounded reciprocal, new = C + (acc * inv) without contraction,
+// statistics from the unrounded fp32 new values (bf16 o_sal for salient rows).
+//
+// MI355X layout: one workgroup = 4 wavefronts = 128 query rows of one (sequence, head); each
+// wavefront owns 32 query rows. The score tile is computed transposed, S^T = K Q^T, with
+// v_mfma_f32_32x32x16_bf16 so that lane l holds query row l%32: row max / row sum / rescale
+// are lane-local (plus one cross-half swap), and the P^T accumulator feeds the PV MFMA
+// (O^T = V^T P^T) as its B operand without any data movement. K is staged row-major and V
+// transposed in LDS (padded rows, no bank-conflicting strides). Workgroups are remapped so
+// that all query tiles of one (sequence, kv-head) land on the same XCD and share its L2.
+#include "kernels.h"
+
+#include <float.h>
+
+namespace dyllm {
+
+constexpr int kD = 128;
+constexpr int kBQ = 128;       // query rows per workgroup
+constexpr int kBK = 64;        // keys per block (reference block width)
+constexpr int kKStride = kD + 8;     // K tile row stride (elements)
+constexpr int kVStride = kBK + 8;    // V^T tile row stride (elements)
+
+union Pack8 {
+  bf16x8_t v;
+  uint32_t u[4];
+  uint4 q;
+};
+union Pack4 {
+  bf16x4_t v;
+  uint32_t u[2];
+};
+
+template <AttnMode MODE>
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
+
+  // ---- workgroup -> (seq, head, tile), XCD-aware ------------------------------------
+  const int nwg = gridDim.x;
+  int wg = blockIdx.x;
+  if ((nwg & 7) == 0) wg = (wg & 7) * (nwg >> 3) + (wg >> 3);
+  const int tile = wg % a.tiles_per_seq;
+  const int head = (wg / a.tiles_per_seq) % a.H;
+  const int b = wg / (a.tiles_per_seq * a.H);
+  const int kvh = head / (a.H / a.Hkv);
+
+  const int row_beg = a.cu_rows[b], row_end = a.cu_rows[b + 1];
+  if (row_beg + tile * kBQ >= row_end) return;
+  const int k_beg = a.cu_k[b], Lk = a.cu_k[b + 1] - k_beg;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int ql = lane & 31, half = lane >> 5;
+  const int row = row_beg + tile * kBQ + w * 32 + ql;  // compact row of this lane
+  const bool row_ok = row < row_end;
+  int64_t qrow = row;
+  if constexpr (MODE == AttnMode::RowSparse) qrow = row_ok ? a.q_rows[row] : 0;
+
+  const int ldq = a.H * kD, ldkv = a.Hkv * kD;
+
+  // ---- Q fragments (B operand of S^T = K Q^T), held for the whole key loop ----------
+  bf16x8_t qf[8];
+  {
+    const uint16_t* qp = a.Q + qrow * ldq + head * kD + half * 8;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      Pack8 p;
+      p.q = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+      qf[s] = p.v;
+    }
+  }
+
+  f32x16_t o_acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
+  float m_run = -FLT_MAX, l_run = 0.f;
+  const float c2 = a.scale_log2;
+
+  const uint16_t* Kb = a.K + int64_t(k_beg) * ldkv + kvh * kD;
+  const uint16_t* Vb = a.V + int64_t(k_beg) * ldkv + kvh * kD;
+  const int nkb = (Lk + kBK - 1) / kBK;
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int key0 = kb * kBK;
+    uint64_t bmask = ~0ull;
+    if constexpr (MODE == AttnMode::ColSparse) bmask = a.kmask[int64_t(b) * a.nblk + kb];
+
+    // ---- stage K (row-major) and V (transposed) into LDS ----------------------------
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int c = tid + 256 * it;
+      const int key = c >> 4, dc = c & 15;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (key0 + key < Lk) v = *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8);
+      *reinterpret_cast<uint4*>(&k_lds[key * kKStride + dc * 8]) = v;
+    }
+    if (bmask != 0) {
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const int c = tid + 256 * it;
+        const int kp = c & 31, dc = c >> 5;
+        const int k0 = 2 * kp;
+        uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
+        if (key0 + k0 < Lk) v0 = *reinterpret_cast<const uint4*>(Vb + int64_t(key0 + k0) * ldkv + dc * 8);
+        if (key0 + k0 + 1 < Lk) v1 = *reinterpret_cast<const uint4*>(Vb + int64_t(key0 + k0 + 1) * ldkv + dc * 8);
+        const uint32_t x0[4] = {v0.x, v0.y, v0.z, v0.w}, x1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t lo = (x0[j] & 0xffffu) | (x1[j] << 16);
+          const uint32_t hi = (x0[j] >> 16) | (x1[j] & 0xffff0000u);
+          *reinterpret_cast<uint32_t*>(&vt_lds[(dc * 8 + 2 * j) * kVStride + k0]) = lo;
+          *reinterpret_cast<uint32_t*>(&vt_lds[(dc * 8 + 2 * j + 1) * kVStride + k0]) = hi;
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- S^T = K Q^T for two 32-key tiles --------------------------------------------
+    f32x16_t s_acc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s_acc[t][r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(&k_lds[(t * 32 + ql) * kKStride + 16 * s + half * 8]);
+        s_acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], s_acc[t], 0, 0, 0);
+      }
+    }
+
+    // ---- online softmax (lane = query row) ----------------------------------------------
+    float bm = -FLT_MAX;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+        if (key >= Lk) s_acc[t][r] = -FLT_MAX;
+        bm = fmaxf(bm, s_acc[t][r]);
+      }
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float m_new = fmaxf(m_run, bm);
+    const float rescale = exp2f((m_run - m_new) * c2);
+    const float m2 = m_new * c2;
+    m_run = m_new;
+    float psum = 0.f;
+    bf16x8_t pf[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        Pack8 p;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e0 = exp2f(fmaf(s_acc[t][8 * u + 2 * j], c2, -m2));
+          const float e1 = exp2f(fmaf(s_acc[t][8 * u + 2 * j + 1], c2, -m2));
+          psum += e0 + e1;
+          p.u[j] = pack_bf16x2(e0, e1);
+        }
+        pf[t][u] = p.v;
+      }
+    l_run = l_run * rescale + psum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o_acc[i][r] *= rescale;
+
+    // ---- O^T += V^T P^T on the 16-key groups that carry salient rows -----------------
+    if (bmask != 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if (((bmask >> (t * 32 + u * 16)) & 0xffffull) == 0) continue;
+          const int kofs = t * 32 + u * 16 + half * 4;
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const uint16_t* vr = &vt_lds[(dt * 32 + ql) * kVStride + kofs];
+            Pack4 lo, hi;
+            lo.v = *reinterpret_cast<const bf16x4_t*>(vr);
+            hi.v = *reinterpret_cast<const bf16x4_t*>(vr + 8);
+            Pack8 va;
+            va.u[0] = lo.u[0];
+            va.u[1] = lo.u[1];
+            va.u[2] = hi.u[0];
+            va.u[3] = hi.u[1];
+            o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, pf[t][u], o_acc[dt], 0, 0, 0);
+          }
+        }
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue ---------------------------------------------------------------------------
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = 1.0f / l_tot;
+  if constexpr (MODE != AttnMode::ColSparse) {
+    if (!row_ok) return;
+    uint16_t* op = a.O + int64_t(row) * ldq + head * kD + half * 4;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        uint2 st;
+        st.x = pack_bf16x2(o_acc[dt][4 * g] * inv, o_acc[dt][4 * g + 1] * inv);
+        st.y = pack_bf16x2(o_acc[dt][4 * g + 2] * inv, o_acc[dt][4 * g + 3] * inv);
+        *reinterpret_cast<uint2*>(op + dt * 32 + g * 8) = st;
+      }
+  } else {
+    float dot = 0.f, nn = 0.f, oo = 0.f;
+    if (row_ok) {
+      const int slot = a.sal_slot[row];
+      const uint16_t* cp = a.C + int64_t(row) * ldq + head * kD + half * 4;
+      uint16_t* op = a.O + int64_t(row) * ldq + head * kD + half * 4;
+      const uint16_t* sp = slot >= 0 ? a.o_sal + int64_t(slot) * ldq + head * kD + half * 4 : nullptr;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int off = dt * 32 + g * 8;
+          const uint2 cv = *reinterpret_cast<const uint2*>(cp + off);
+          const float old[4] = {__uint_as_float(cv.x << 16), __uint_as_float(cv.x & 0xffff0000u),
+                                __uint_as_float(cv.y << 16), __uint_as_float(cv.y & 0xffff0000u)};
+          float nw[4];
+          uint2 st;
+          if (sp) {
+            st = *reinterpret_cast<const uint2*>(sp + off);
+            nw[0] = __uint_as_float(st.x << 16);
+            nw[1] = __uint_as_float(st.x & 0xffff0000u);
+            nw[2] = __uint_as_float(st.y << 16);
+            nw[3] = __uint_as_float(st.y & 0xffff0000u);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) nw[j] = __fadd_rn(old[j], __fmul_rn(o_acc[dt][4 * g + j], inv));
+            st.x = pack_bf16x2(nw[0], nw[1]);
+            st.y = pack_bf16x2(nw[2], nw[3]);
+          }
+          *reinterpret_cast<uint2*>(op + off) = st;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            dot += nw[j] * old[j];
+            nn += nw[j] * nw[j];
+            oo += old[j] * old[j];
+          }
+        }
+    }
+    dot += __shfl_xor(dot, 32, 64);
+    nn += __shfl_xor(nn, 32, 64);
+    oo += __shfl_xor(oo, 32, 64);
+    if (row_ok && half == 0) {
+      a.part[(int64_t(head) * 3 + 0) * a.Tq + row] = dot;
+      a.part[(int64_t(head) * 3 + 1) * a.Tq + row] = nn;
+      a.part[(int64_t(head) * 3 + 2) * a.Tq + row] = oo;
+    }
+  }
+}
+
+// ---- column-sparse preparation: slot map + per-block salient key bits ------------------
+__global__ __launch_bounds__(256) void colsparse_fill_kernel(int32_t* __restrict__ slot, int64_t Tq,
+                                                             uint64_t* __restrict__ kmask, int64_t nmask) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < Tq) slot[i] = -1;
+  if (i < nmask) kmask[i] = 0;
+}
+
+__global__ __launch_bounds__(256) void colsparse_scatter_kernel(const int32_t* __restrict__ idx_q,
+                                                                const int32_t* __restrict__ idx_k, int n_sal,
+                                                                const int32_t* __restrict__ cu_k, int B, int nblk,
+                                                                int32_t* __restrict__ slot,
+                                                                unsigned long long* __restrict__ kmask) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= n_sal) return;
+  slot[idx_q[j]] = j;
+  const int64_t k = idx_k[j];
+  const int b = find_segment(cu_k, B + 1, k);
+  if (b >= B || k >= cu_k[b + 1]) return;
+  const int off = int(k - cu_k[b]);
+  atomicOr(&kmask[int64_t(b) * nblk + off / kBK], 1ull << (off % kBK));
+}
+
+int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s) {
+  DYLLM_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.H % a.Hkv == 0, "bad head counts");
+  DYLLM_REQUIRE(max_rows_per_seq >= 0, "bad row bound");
+  if (max_rows_per_seq == 0) return 0;
+  AttnArgs g = a;
+  g.tiles_per_seq = int(cdiv(max_rows_per_seq, kBQ));
+  const int64_t nwg = int64_t(g.tiles_per_seq) * a.H * a.B;
+  DYLLM_REQUIRE(nwg < (int64_t(1) << 31), "grid too large");
+  switch (mode) {
+    case AttnMode::Dense: attention_kernel<AttnMode::Dense><<<unsigned(nwg), 256, 0, s>>>(g); break;
+    case AttnMode::RowSparse: attention_kernel<AttnMode::RowSparse><<<unsigned(nwg), 256, 0, s>>>(g); break;
+    case AttnMode::ColSparse: attention_kernel<AttnMode::ColSparse><<<unsigned(nwg), 256, 0, s>>>(g); break;
+  }
+  return check_launch("attention_kernel");
+}
+
+int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal, const int32_t* cu_k, int B,
+                          int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, hipStream_t s) {
+  const int64_t nmask = int64_t(B) * nblk;
+  const int64_t n = Tq > nmask ? Tq : nmask;
+  if (n > 0) {
+    colsparse_fill_kernel<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(slot, Tq, kmask, nmask);
+    if (int rc = check_launch("colsparse_fill_kernel")) return rc;
+  }
+  if (n_sal > 0) {
+    colsparse_scatter_kernel<<<unsigned(cdiv(n_sal, 256)), 256, 0, s>>>(
+        idx_q, idx_k, n_sal, cu_k, B, nblk, slot, reinterpret_cast<unsigned long long*>(kmask));
+    return check_launch("colsparse_scatter_kernel");
+  }
+  return 0;
+}
+
+}  // namespace dyllm

@@ -1,0 +1,422 @@
+// extern "C" entry points of libdyllm_hip.so: argument validation, workspace carving and
+// kernel launches. No host synchronisation and no device allocation happens here.
+#include "../../include/dyllm_hip.h"
+#include "kernels.h"
+
+#include <string>
+
+namespace dyllm {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+int fail(const std::string& msg) {
+  g_last_error = msg;
+  return 1;
+}
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return 0;
+  return fail(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+static const float kLog2e = 1.4426950408889634f;
+constexpr int kMoeBlock = 128;
+
+}  // namespace dyllm
+
+using namespace dyllm;
+
+#define DYLLM_STREAM(s) reinterpret_cast<hipStream_t>(s)
+#define DYLLM_NONNULL(p) DYLLM_REQUIRE((p) != nullptr, #p " must not be NULL")
+
+extern "C" {
+
+const char* dyllm_last_error(void) { return g_last_error.c_str(); }
+int dyllm_abi_version(void) { return 1; }
+
+// ---------------------------------------------------------------------------------------
+size_t dyllm_attention_sparse_workspace_bytes(int batch, int num_heads, int64_t total_q, int max_seqlen_k) {
+  const int64_t nblk = cdiv(max_seqlen_k > 0 ? max_seqlen_k : 1, 64);
+  return align256(size_t(total_q) * 4) + align256(size_t(batch) * nblk * 8) +
+         align256(size_t(num_heads) * 3 * size_t(total_q) * 4);
+}
+
+int dyllm_attention_sparse_varlen(const void* q, const void* k, const void* v_delta, const void* c,
+                                  const void* o_sal, void* o, int batch, int num_heads, int num_kv_heads,
+                                  int head_dim, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int max_seqlen_q, int max_seqlen_k, int64_t total_q, int num_salient,
+                                  const int32_t* cu_salientlens, const int32_t* idx_salient_q,
+                                  const int32_t* idx_salient_k, float* cosine_stats, uint8_t* cosine_out,
+                                  float threshold, void* workspace, size_t workspace_bytes, void* stream) {
+  DYLLM_NONNULL(q);
+  DYLLM_NONNULL(k);
+  DYLLM_NONNULL(v_delta);
+  DYLLM_NONNULL(c);
+  DYLLM_NONNULL(o);
+  DYLLM_NONNULL(cu_seqlens_q);
+  DYLLM_NONNULL(cu_seqlens_k);
+  DYLLM_NONNULL(cosine_stats);
+  DYLLM_NONNULL(cosine_out);
+  DYLLM_REQUIRE(head_dim == 128, "supported head dimension is 128, got " + std::to_string(head_dim));
+  DYLLM_REQUIRE(batch >= 1, "batch must be >= 1");
+  DYLLM_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
+                "query heads must be a positive multiple of KV heads; got " + std::to_string(num_heads) + " and " +
+                    std::to_string(num_kv_heads));
+  DYLLM_REQUIRE(total_q > 0, "Q and K/V token dimensions must be non-empty");
+  DYLLM_REQUIRE(max_seqlen_q > 0 && max_seqlen_q <= total_q && max_seqlen_k > 0,
+                "maximum sequence lengths must be positive and fit their packed token dimensions");
+  DYLLM_REQUIRE(num_salient >= 0 && num_salient <= total_q, "salient Q index count cannot exceed Q.size(0)");
+  DYLLM_REQUIRE(num_salient == 0 || (o_sal && idx_salient_q), "o_sal and idx_salient_q are required");
+  const size_t need = dyllm_attention_sparse_workspace_bytes(batch, num_heads, total_q, max_seqlen_k);
+  DYLLM_REQUIRE(workspace && workspace_bytes >= need,
+                "workspace too small: need " + std::to_string(need) + " bytes");
+  const hipStream_t s = DYLLM_STREAM(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int nblk = int(cdiv(max_seqlen_k, 64));
+  int32_t* slot = reinterpret_cast<int32_t*>(ws);
+  ws += align256(size_t(total_q) * 4);
+  uint64_t* kmask = reinterpret_cast<uint64_t*>(ws);
+  ws += align256(size_t(batch) * nblk * 8);
+  float* part = reinterpret_cast<float*>(ws);
+  if (int rc = launch_colsparse_prep(idx_salient_q, idx_salient_k ? idx_salient_k : idx_salient_q, num_salient,
+                                     cu_seqlens_k, batch, nblk, slot, total_q, kmask, s))
+    return rc;
+  AttnArgs a{};
+  a.Q = static_cast<const uint16_t*>(q);
+  a.K = static_cast<const uint16_t*>(k);
+  a.V = static_cast<const uint16_t*>(v_delta);
+  a.C = static_cast<const uint16_t*>(c);
+  a.o_sal = static_cast<const uint16_t*>(o_sal);
+  a.O = static_cast<uint16_t*>(o);
+  a.cu_rows = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.sal_slot = slot;
+  a.kmask = kmask;
+  a.part = part;
+  a.B = batch;
+  a.H = num_heads;
+  a.Hkv = num_kv_heads;
+  a.nblk = nblk;
+  a.Tq = total_q;
+  // the reference uses rsqrt(head_dim) here, not the layer's scale (sm80.cu:166-168)
+  a.scale_log2 = (1.0f / sqrtf(float(head_dim))) * kLog2e;
+  if (int rc = launch_attention(AttnMode::ColSparse, a, max_seqlen_q, s)) return rc;
+  return launch_saliency_reduce(part, cosine_stats, cosine_out, total_q, num_heads, threshold, s);
+}
+
+int dyllm_flash_attn_varlen(const void* q, const void* k, const void* v, void* o, int batch, int num_heads,
+                            int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
+                            const int32_t* cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, float softmax_scale,
+                            const int32_t* q_rows, void* stream) {
+  DYLLM_NONNULL(q);
+  DYLLM_NONNULL(k);
+  DYLLM_NONNULL(v);
+  DYLLM_NONNULL(o);
+  DYLLM_NONNULL(cu_seqlens_q);
+  DYLLM_NONNULL(cu_seqlens_k);
+  DYLLM_REQUIRE(head_dim == 128, "supported head dimension is 128, got " + std::to_string(head_dim));
+  DYLLM_REQUIRE(batch >= 1, "batch must be >= 1");
+  DYLLM_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0, "bad head counts");
+  DYLLM_REQUIRE(max_seqlen_q >= 0 && max_seqlen_k > 0, "bad maximum sequence lengths");
+  AttnArgs a{};
+  a.Q = static_cast<const uint16_t*>(q);
+  a.K = static_cast<const uint16_t*>(k);
+  a.V = static_cast<const uint16_t*>(v);
+  a.O = static_cast<uint16_t*>(o);
+  a.cu_rows = cu_seqlens_q;
+  a.cu_k = cu_seqlens_k;
+  a.q_rows = q_rows;
+  a.B = batch;
+  a.H = num_heads;
+  a.Hkv = num_kv_heads;
+  a.scale_log2 = softmax_scale * kLog2e;
+  return launch_attention(q_rows ? AttnMode::RowSparse : AttnMode::Dense, a, max_seqlen_q, DYLLM_STREAM(stream));
+}
+
+// ---------------------------------------------------------------------------------------
+int dyllm_cosine_mask(const float* stats, int64_t rows, float threshold, uint8_t* mask, void* stream) {
+  DYLLM_NONNULL(stats);
+  DYLLM_NONNULL(mask);
+  return launch_cosine_mask(stats, mask, rows, threshold, DYLLM_STREAM(stream));
+}
+
+int dyllm_saliency_stats(const void* c_new, const void* c_old, int64_t rows, int64_t dim, float threshold,
+                         float* stats, uint8_t* mask, void* stream) {
+  DYLLM_NONNULL(c_new);
+  DYLLM_NONNULL(c_old);
+  DYLLM_NONNULL(stats);
+  DYLLM_NONNULL(mask);
+  return launch_saliency_rows(static_cast<const uint16_t*>(c_new), static_cast<const uint16_t*>(c_old), stats, mask,
+                              rows, dim, threshold, DYLLM_STREAM(stream));
+}
+
+int dyllm_salient_compact(const uint8_t* mask, int64_t rows, const int32_t* cu_seqlens_q, int batch,
+                          const int32_t* cu_promptlens, int64_t* idx64, int32_t* idx32, int64_t* idx_k,
+                          int32_t* cu_salientlens, int32_t* count, void* stream) {
+  DYLLM_REQUIRE(rows == 0 || mask != nullptr, "mask must not be NULL");
+  DYLLM_NONNULL(cu_seqlens_q);
+  DYLLM_NONNULL(idx64);
+  DYLLM_NONNULL(cu_salientlens);
+  DYLLM_NONNULL(count);
+  return launch_compact(mask, rows, cu_seqlens_q, batch, cu_promptlens, idx64, idx32, idx_k, cu_salientlens, count,
+                        DYLLM_STREAM(stream));
+}
+
+int dyllm_fused_offset_launch(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_promptlens,
+                              const int32_t* cu_salientlens, int num_groups, int64_t* out, int64_t max_threads,
+                              void* stream) {
+  DYLLM_NONNULL(idxs);
+  DYLLM_NONNULL(num_idxs);
+  DYLLM_NONNULL(cu_promptlens);
+  DYLLM_NONNULL(cu_salientlens);
+  DYLLM_NONNULL(out);
+  DYLLM_REQUIRE(max_threads >= 0, "max_threads must be non-negative");
+  return launch_fused_offset(idxs, num_idxs, cu_promptlens, cu_salientlens, num_groups, out, max_threads,
+                             DYLLM_STREAM(stream));
+}
+
+// ---------------------------------------------------------------------------------------
+static int row_map(RowMap mode, const void* src, void* dst, int64_t row_bytes, int64_t n_rows,
+                   const int64_t* seq_starts, const int32_t* cu, const int32_t* cu_q, const int64_t* seq_ids,
+                   const int64_t* row_idx, int batch, void* stream) {
+  DYLLM_NONNULL(src);
+  DYLLM_NONNULL(dst);
+  DYLLM_REQUIRE(batch >= 0, "batch must be non-negative");
+  if (n_rows <= 0 || (batch == 0 && mode != RowMap::Gather)) return 0;
+  RowMapArgs a{};
+  a.src = static_cast<const char*>(src);
+  a.dst = static_cast<char*>(dst);
+  a.row_bytes = row_bytes;
+  a.n_rows = n_rows;
+  a.seq_starts = seq_starts;
+  a.cu = cu;
+  a.cu_q = cu_q;
+  a.seq_ids = seq_ids;
+  a.row_idx = row_idx;
+  a.B = batch;
+  return launch_row_map(mode, a, DYLLM_STREAM(stream));
+}
+
+int dyllm_get_seqs(const void* cache, void* out, int64_t row_bytes, const int64_t* seq_starts,
+                   const int32_t* cu_seqlens, const int64_t* seq_ids, int batch, int64_t total_rows, void* stream) {
+  DYLLM_NONNULL(seq_starts);
+  DYLLM_NONNULL(cu_seqlens);
+  DYLLM_NONNULL(seq_ids);
+  return row_map(RowMap::GetSeqs, cache, out, row_bytes, total_rows, seq_starts, cu_seqlens, nullptr, seq_ids,
+                 nullptr, batch, stream);
+}
+int dyllm_get_block(const void* cache, void* out, int64_t row_bytes, const int64_t* seq_starts,
+                    const int32_t* cu_seqlens_k, const int32_t* cu_seqlens_q, const int64_t* seq_ids, int batch,
+                    int64_t total_rows, void* stream) {
+  DYLLM_NONNULL(seq_starts);
+  DYLLM_NONNULL(cu_seqlens_k);
+  DYLLM_NONNULL(cu_seqlens_q);
+  DYLLM_NONNULL(seq_ids);
+  return row_map(RowMap::GetBlock, cache, out, row_bytes, total_rows, seq_starts, cu_seqlens_k, cu_seqlens_q,
+                 seq_ids, nullptr, batch, stream);
+}
+int dyllm_reset_full(void* cache, const void* in, int64_t row_bytes, const int64_t* seq_starts,
+                     const int32_t* cu_seqlens, const int64_t* seq_ids, int batch, int64_t total_rows, void* stream) {
+  DYLLM_NONNULL(seq_starts);
+  DYLLM_NONNULL(cu_seqlens);
+  DYLLM_NONNULL(seq_ids);
+  return row_map(RowMap::ResetFull, in, cache, row_bytes, total_rows, seq_starts, cu_seqlens, nullptr, seq_ids,
+                 nullptr, batch, stream);
+}
+int dyllm_reset_block(void* cache, const void* in, int64_t row_bytes, const int64_t* seq_starts,
+                      const int32_t* cu_seqlens_k, const int32_t* cu_seqlens_q, const int64_t* seq_ids, int batch,
+                      int64_t total_rows, void* stream) {
+  DYLLM_NONNULL(seq_starts);
+  DYLLM_NONNULL(cu_seqlens_k);
+  DYLLM_NONNULL(cu_seqlens_q);
+  DYLLM_NONNULL(seq_ids);
+  return row_map(RowMap::ResetBlock, in, cache, row_bytes, total_rows, seq_starts, cu_seqlens_k, cu_seqlens_q,
+                 seq_ids, nullptr, batch, stream);
+}
+int dyllm_scatter_update(void* cache, const void* new_vals, int64_t row_bytes, const int64_t* row_idx, int64_t rows,
+                         const int32_t* cu_seqlens, const int64_t* seq_starts, const int64_t* seq_ids, int batch,
+                         void* stream) {
+  DYLLM_NONNULL(row_idx);
+  DYLLM_NONNULL(cu_seqlens);
+  DYLLM_NONNULL(seq_starts);
+  DYLLM_NONNULL(seq_ids);
+  return row_map(RowMap::Scatter, new_vals, cache, row_bytes, rows, seq_starts, cu_seqlens, nullptr, seq_ids, row_idx,
+                 batch, stream);
+}
+int dyllm_scatter_dest_rows(const int64_t* row_idx, int64_t rows, const int32_t* cu_seqlens,
+                            const int64_t* seq_starts, const int64_t* seq_ids, int batch, int64_t* dest,
+                            void* stream) {
+  DYLLM_NONNULL(row_idx);
+  DYLLM_NONNULL(cu_seqlens);
+  DYLLM_NONNULL(seq_starts);
+  DYLLM_NONNULL(seq_ids);
+  DYLLM_NONNULL(dest);
+  DYLLM_REQUIRE(batch >= 1, "batch must be >= 1");
+  return launch_scatter_dest_rows(row_idx, rows, cu_seqlens, seq_starts, seq_ids, batch, dest, DYLLM_STREAM(stream));
+}
+int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t* idx, int64_t rows, void* stream) {
+  DYLLM_NONNULL(idx);
+  return row_map(RowMap::Gather, x, out, row_bytes, rows, nullptr, nullptr, nullptr, nullptr, idx, 0, stream);
+}
+
+// ---------------------------------------------------------------------------------------
+size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate) {
+  return align256(size_t(rows > 0 ? rows : 0) * size_t(intermediate) * 2);
+}
+
+// 256x256 tiles when they still give >= one workgroup per CU, else 128x128.
+static int pick_tile(int64_t M, int64_t N) { return (cdiv(M, 256) * cdiv(N, 256) >= 256) ? 256 : 128; }
+
+int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
+                     const void* w_down, int hidden, int intermediate, void* workspace, size_t workspace_bytes,
+                     void* out, const int64_t* out_rows, void* stream) {
+  DYLLM_NONNULL(x);
+  DYLLM_NONNULL(w_gate_up);
+  DYLLM_NONNULL(w_down);
+  DYLLM_NONNULL(out);
+  DYLLM_REQUIRE(hidden > 0 && hidden % 64 == 0, "hidden size must be a positive multiple of 64");
+  DYLLM_REQUIRE(intermediate > 0 && intermediate % 64 == 0, "intermediate size must be a positive multiple of 64");
+  if (rows <= 0) return 0;
+  const size_t need = dyllm_swiglu_ffn_workspace_bytes(rows, intermediate);
+  DYLLM_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need " + std::to_string(need) + " bytes");
+  const hipStream_t s = DYLLM_STREAM(stream);
+  uint16_t* h = static_cast<uint16_t*>(workspace);
+  GemmArgs g{};
+  g.A = static_cast<const uint16_t*>(x);
+  g.lda = ld_x;
+  g.a_ids = rows_idx;
+  g.a_div = 1;
+  g.id_limit = INT64_MAX;
+  g.W = static_cast<const uint16_t*>(w_gate_up);
+  g.ldw = hidden;
+  g.Cout = h;
+  g.ldc = intermediate;
+  g.M = rows;
+  g.N = 2 * intermediate;
+  g.K = hidden;
+  g.half_n = intermediate;
+  const int t1 = (pick_tile(rows, g.N) == 256 && intermediate % 128 == 0) ? 256 : 128;
+  if (int rc = launch_gemm(GemmEpi::SwiGLU, g, rows, t1, s)) return rc;
+  GemmArgs d{};
+  d.A = h;
+  d.lda = intermediate;
+  d.a_div = 1;
+  d.id_limit = INT64_MAX;
+  d.W = static_cast<const uint16_t*>(w_down);
+  d.ldw = intermediate;
+  d.Cout = static_cast<uint16_t*>(out);
+  d.ldc = hidden;
+  d.c_rows = out_rows;
+  d.M = rows;
+  d.N = hidden;
+  d.K = intermediate;
+  return launch_gemm(GemmEpi::Store, d, rows, pick_tile(rows, hidden), s);
+}
+
+// ---------------------------------------------------------------------------------------
+int dyllm_moe_gate(const void* x, const int32_t* rows_idx, int64_t tokens, int hidden, const void* router_w,
+                   int num_experts, int top_k, int renormalize, void* topk_weights, int32_t* topk_ids, void* stream) {
+  DYLLM_NONNULL(x);
+  DYLLM_NONNULL(router_w);
+  DYLLM_NONNULL(topk_weights);
+  DYLLM_NONNULL(topk_ids);
+  return launch_moe_router(static_cast<const uint16_t*>(x), rows_idx, static_cast<const uint16_t*>(router_w), tokens,
+                           hidden, num_experts, top_k, renormalize, static_cast<uint16_t*>(topk_weights), topk_ids,
+                           DYLLM_STREAM(stream));
+}
+
+int dyllm_moe_align_block_size(const int32_t* topk_ids, int64_t slots, int num_experts, int block,
+                               int32_t* sorted_token_ids, int64_t capacity, int32_t* tile_expert,
+                               int32_t* num_post_pad, void* stream) {
+  DYLLM_NONNULL(topk_ids);
+  DYLLM_NONNULL(sorted_token_ids);
+  DYLLM_NONNULL(tile_expert);
+  DYLLM_NONNULL(num_post_pad);
+  return launch_moe_align(topk_ids, slots, num_experts, block, sorted_token_ids, capacity, tile_expert, num_post_pad,
+                          DYLLM_STREAM(stream));
+}
+
+static int64_t moe_capacity(int64_t slots, int E) { return cdiv(slots + int64_t(E) * (kMoeBlock - 1), kMoeBlock) * kMoeBlock; }
+
+size_t dyllm_fused_experts_workspace_bytes(int64_t tokens, int top_k, int num_experts, int hidden, int intermediate) {
+  const int64_t S = tokens * top_k;
+  const int64_t cap = moe_capacity(S, num_experts);
+  return align256(size_t(cap) * 4) + align256(size_t(cap / kMoeBlock) * 4) + align256(4) +
+         align256(size_t(S) * intermediate * 2) + align256(size_t(S) * hidden * 2);
+}
+
+int dyllm_fused_experts(const void* x, const int32_t* rows_idx, int64_t tokens, int hidden, const void* w1,
+                        const void* w2, int num_experts, int intermediate, const void* topk_weights,
+                        const int32_t* topk_ids, int top_k, void* out, const int64_t* out_rows, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  DYLLM_NONNULL(x);
+  DYLLM_NONNULL(w1);
+  DYLLM_NONNULL(w2);
+  DYLLM_NONNULL(topk_weights);
+  DYLLM_NONNULL(topk_ids);
+  DYLLM_NONNULL(out);
+  DYLLM_REQUIRE(rows_idx == nullptr, "fused_experts takes compacted tokens (gather them first)");
+  DYLLM_REQUIRE(hidden % 64 == 0 && intermediate % 64 == 0, "hidden and intermediate must be multiples of 64");
+  if (tokens <= 0) return 0;
+  const size_t need = dyllm_fused_experts_workspace_bytes(tokens, top_k, num_experts, hidden, intermediate);
+  DYLLM_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need " + std::to_string(need) + " bytes");
+  const hipStream_t s = DYLLM_STREAM(stream);
+  const int64_t S = tokens * top_k;
+  const int64_t cap = moe_capacity(S, num_experts);
+  char* ws = static_cast<char*>(workspace);
+  int32_t* sorted = reinterpret_cast<int32_t*>(ws);
+  ws += align256(size_t(cap) * 4);
+  int32_t* tile_e = reinterpret_cast<int32_t*>(ws);
+  ws += align256(size_t(cap / kMoeBlock) * 4);
+  int32_t* npp = reinterpret_cast<int32_t*>(ws);
+  ws += align256(4);
+  uint16_t* inter = reinterpret_cast<uint16_t*>(ws);
+  ws += align256(size_t(S) * intermediate * 2);
+  uint16_t* y = reinterpret_cast<uint16_t*>(ws);
+  if (int rc = launch_moe_align(topk_ids, S, num_experts, kMoeBlock, sorted, cap, tile_e, npp, s)) return rc;
+  // GEMM 1: inter[slot] = silu(x[slot/top_k] W1g^T) * (x W1u^T)
+  GemmArgs g{};
+  g.A = static_cast<const uint16_t*>(x);
+  g.lda = hidden;
+  g.a_ids = sorted;
+  g.a_div = top_k;
+  g.id_limit = S;
+  g.W = static_cast<const uint16_t*>(w1);
+  g.ldw = hidden;
+  g.w_expert_stride = int64_t(2) * intermediate * hidden;
+  g.tile_expert = tile_e;
+  g.num_m_dev = npp;
+  g.Cout = inter;
+  g.ldc = intermediate;
+  g.c_by_id = 1;
+  g.M = cap;
+  g.N = 2 * intermediate;
+  g.K = hidden;
+  g.half_n = intermediate;
+  if (int rc = launch_gemm(GemmEpi::SwiGLU, g, cap, kMoeBlock, s)) return rc;
+  // GEMM 2: y[slot] = (inter[slot] W2^T) * w[slot]
+  GemmArgs d{};
+  d.A = inter;
+  d.lda = intermediate;
+  d.a_ids = sorted;
+  d.a_div = 1;
+  d.id_limit = S;
+  d.W = static_cast<const uint16_t*>(w2);
+  d.ldw = intermediate;
+  d.w_expert_stride = int64_t(hidden) * intermediate;
+  d.tile_expert = tile_e;
+  d.num_m_dev = npp;
+  d.Cout = y;
+  d.ldc = hidden;
+  d.c_by_id = 1;
+  d.row_scale_bf16 = static_cast<const uint16_t*>(topk_weights);
+  d.M = cap;
+  d.N = hidden;
+  d.K = intermediate;
+  if (int rc = launch_gemm(GemmEpi::Store, d, cap, kMoeBlock, s)) return rc;
+  return launch_moe_combine(y, tokens, hidden, top_k, static_cast<uint16_t*>(out), out_rows, s);
+}
+
+}  // extern "C"

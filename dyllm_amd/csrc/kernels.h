@@ -1,0 +1,89 @@
+// Kernel-side argument structs and launchers shared between the kernel translation units
+// and the C-ABI layer (capi.hip).
+#pragma once
+#include "dyllm_common.h"
+
+namespace dyllm {
+
+enum class RowMap : int { GetSeqs = 0, GetBlock = 1, ResetFull = 2, ResetBlock = 3, Scatter = 4, Gather = 5 };
+struct RowMapArgs {
+  const char* src;
+  char* dst;
+  int64_t row_bytes;
+  int64_t n_rows;
+  const int64_t* seq_starts;
+  const int32_t* cu;
+  const int32_t* cu_q;
+  const int64_t* seq_ids;
+  const int64_t* row_idx;
+  int B;
+};
+int launch_row_map(RowMap mode, const RowMapArgs& a, hipStream_t stream);
+int launch_scatter_dest_rows(const int64_t* row_idx, int64_t M, const int32_t* cu, const int64_t* seq_starts,
+                             const int64_t* seq_ids, int B, int64_t* dest, hipStream_t s);
+int launch_cosine_mask(const float* stats, uint8_t* mask, int64_t T, float tau, hipStream_t s);
+int launch_saliency_rows(const uint16_t* c_new, const uint16_t* c_old, float* stats, uint8_t* mask, int64_t T,
+                         int64_t D, float tau, hipStream_t s);
+int launch_saliency_reduce(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
+                           hipStream_t s);
+int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
+                   int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* cu_sal, int32_t* count, hipStream_t s);
+int launch_fused_offset(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_prompt,
+                        const int32_t* cu_sal, int groups, int64_t* out, int64_t cap, hipStream_t s);
+
+enum class AttnMode : int { Dense = 0, RowSparse = 1, ColSparse = 2 };
+struct AttnArgs {
+  const uint16_t* Q;
+  const uint16_t* K;
+  const uint16_t* V;
+  const uint16_t* C;
+  const uint16_t* o_sal;
+  uint16_t* O;
+  const int32_t* cu_rows;
+  const int32_t* cu_k;
+  const int32_t* q_rows;
+  const int32_t* sal_slot;
+  const uint64_t* kmask;
+  float* part;
+  int B, H, Hkv;
+  int tiles_per_seq;
+  int nblk;
+  int64_t Tq;
+  float scale_log2;
+};
+int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s);
+int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal, const int32_t* cu_k, int B,
+                          int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, hipStream_t s);
+
+enum class GemmEpi : int { Store = 0, SwiGLU = 1 };
+struct GemmArgs {
+  const uint16_t* A;
+  int64_t lda;
+  const int32_t* a_ids;
+  int a_div;
+  int64_t id_limit;
+  const uint16_t* W;
+  int64_t ldw;
+  int64_t w_expert_stride;
+  const int32_t* tile_expert;
+  const int32_t* num_m_dev;
+  uint16_t* Cout;
+  int64_t ldc;
+  const int64_t* c_rows;
+  int c_by_id;
+  const float* row_scale_f32;
+  const uint16_t* row_scale_bf16;
+  int64_t M;
+  int N, K;
+  int half_n;
+};
+int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, hipStream_t s);
+
+int launch_moe_router(const uint16_t* x, const int32_t* rows, const uint16_t* wr, int64_t T, int Hd, int E, int top_k,
+                      int renorm, uint16_t* topk_w, int32_t* topk_ids, hipStream_t s);
+int launch_moe_align(const int32_t* ids, int64_t S, int E, int bm, int32_t* sorted_ids, int64_t cap,
+                     int32_t* tile_expert, int32_t* num_post_pad, hipStream_t s);
+int launch_moe_combine(const uint16_t* y, int64_t T, int Hd, int top_k, uint16_t* out, const int64_t* dst_rows,
+                       hipStream_t s);
+
+}  // namespace dyllm

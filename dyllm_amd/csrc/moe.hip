@@ -1,0 +1,201 @@
+// Mixture-of-experts pieces around the grouped GEMM (gemm.hip):
+//
+//   router   -- fp32 logits x . Wr^T, softmax, top-k in descending order, optional
+//               renormalisation; weights emitted in bf16 and ids int32
+//               (moe_gate, dyllm/model_executor/layers/fused_moe.py:375-408).
+//   align    -- stable grouping of the flattened (token, k) slots by expert, each expert
+//               bucket padded to the GEMM tile height with the sentinel T*top_k, plus the
+//               expert of every tile (moe_align_block_size, fused_moe.py:37-85). Runs on the
+//               device: no .item() host sync.
+//   combine  -- sum over the top-k slots of each token (fused_moe.py:335), written in bf16,
+//               optionally straight into the cached FFN rows (MLPcache scatter).
+#include "kernels.h"
+
+#include <float.h>
+
+namespace dyllm {
+
+// ---- router: one wavefront per token, lane e scores expert e ---------------------------
+// E <= 64 experts. x row is read once per lane in 16-byte pieces (L1/L2 broadcast).
+__global__ __launch_bounds__(256) void moe_router_kernel(const uint16_t* __restrict__ x, const int32_t* __restrict__ rows,
+                                                         const uint16_t* __restrict__ wr, int64_t T, int Hd, int E,
+                                                         int top_k, int renorm, uint16_t* __restrict__ topk_w,
+                                                         int32_t* __restrict__ topk_ids) {
+  const int64_t t = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int64_t xr = rows ? rows[t] : t;
+  const uint4* xp = reinterpret_cast<const uint4*>(x + xr * Hd);
+  float logit = -FLT_MAX;
+  if (lane < E) {
+    const uint4* wp = reinterpret_cast<const uint4*>(wr + int64_t(lane) * Hd);
+    float acc = 0.f;
+    for (int i = 0; i < Hd / 8; ++i) {
+      const uint4 a = xp[i], b = wp[i];
+      const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc += __uint_as_float(av[j] << 16) * __uint_as_float(bv[j] << 16);
+        acc += __uint_as_float(av[j] & 0xffff0000u) * __uint_as_float(bv[j] & 0xffff0000u);
+      }
+    }
+    logit = acc;
+  }
+  const float mx = wave_max(logit);
+  const float e = (lane < E) ? expf(logit - mx) : 0.f;
+  const float sum = wave_sum(e);
+  float p = (lane < E) ? e / sum : -1.0f;
+  // top-k: repeated wave argmax, lowest expert index wins ties (torch.topk order is
+  // unspecified for exact ties)
+  float picked_sum = 0.f;
+  float my_w = 0.f;
+  int my_rank = -1;
+  for (int k = 0; k < top_k; ++k) {
+    float best = p;
+    int bi = lane;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(best, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ob > best || (ob == best && oi < bi)) {
+        best = ob;
+        bi = oi;
+      }
+    }
+    if (lane == bi) {
+      my_rank = k;
+      my_w = p;
+      p = -2.0f;
+    }
+    picked_sum += best;
+  }
+  if (my_rank >= 0) {
+    const float wv = renorm ? my_w / picked_sum : my_w;
+    topk_w[t * top_k + my_rank] = f32_to_bf16(wv);
+    topk_ids[t * top_k + my_rank] = lane;
+  }
+}
+
+int launch_moe_router(const uint16_t* x, const int32_t* rows, const uint16_t* wr, int64_t T, int Hd, int E, int top_k,
+                      int renorm, uint16_t* topk_w, int32_t* topk_ids, hipStream_t s) {
+  DYLLM_REQUIRE(E >= 1 && E <= 64, "router supports 1..64 experts");
+  DYLLM_REQUIRE(top_k >= 1 && top_k <= E, "top_k must be in [1, num_experts]");
+  DYLLM_REQUIRE(Hd % 8 == 0, "hidden size must be a multiple of 8");
+  if (T <= 0) return 0;
+  moe_router_kernel<<<unsigned(cdiv(T, 4)), 256, 0, s>>>(x, rows, wr, T, Hd, E, top_k, renorm, topk_w, topk_ids);
+  return check_launch("moe_router_kernel");
+}
+
+// ---- align: one workgroup of 1024 threads -----------------------------------------------
+// Pass 1 counts slots per expert (LDS atomics). Then padded bucket starts. Pass 2 walks
+// the slots in order, 1024 per round; inside a round each wavefront finds the lanes that
+// share its expert with six ballots and ranks them by lane order, and per-(wave, expert)
+// counts are prefix-summed across the 16 wavefronts: the placement is stable.
+__global__ __launch_bounds__(1024) void moe_align_kernel(const int32_t* __restrict__ ids, int64_t S, int E, int bm,
+                                                         int32_t* __restrict__ sorted_ids, int64_t cap,
+                                                         int32_t* __restrict__ tile_expert,
+                                                         int32_t* __restrict__ num_post_pad) {
+  __shared__ int cnt[64];
+  __shared__ int start[64];
+  __shared__ int run[64];
+  __shared__ int wcnt[16][64];
+  __shared__ int total_sh;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  if (tid < 64) cnt[tid] = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < S; i += 1024) atomicAdd(&cnt[ids[i]], 1);
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    for (int e = 0; e < E; ++e) {
+      start[e] = acc;
+      run[e] = 0;
+      acc += (cnt[e] + bm - 1) / bm * bm;
+    }
+    num_post_pad[0] = acc;
+    total_sh = acc;
+  }
+  __syncthreads();
+  const int total = total_sh;
+  // sentinel fill + tile experts
+  for (int64_t i = tid; i < cap; i += 1024) sorted_ids[i] = int32_t(S);
+  for (int e = 0; e < E; ++e) {
+    const int nt = (cnt[e] + bm - 1) / bm;
+    for (int t = tid; t < nt; t += 1024) tile_expert[start[e] / bm + t] = e;
+  }
+  for (int64_t t = total / bm + tid; t < cap / bm; t += 1024) tile_expert[t] = 0;
+  __syncthreads();
+  for (int64_t r0 = 0; r0 < S; r0 += 1024) {
+    const int64_t i = r0 + tid;
+    const bool ok = i < S;
+    const int e = ok ? ids[i] : 63;
+    unsigned long long same = __ballot(ok);
+#pragma unroll
+    for (int bit = 0; bit < 6; ++bit) {
+      const unsigned long long b = __ballot(ok && ((e >> bit) & 1));
+      same &= ((e >> bit) & 1) ? b : ~b;
+    }
+    const int rank = __popcll(same & ((1ull << lane) - 1));
+    for (int x = tid; x < 16 * 64; x += 1024) (&wcnt[0][0])[x] = 0;
+    __syncthreads();
+    if (ok && rank == 0) wcnt[wid][e] = __popcll(same);
+    __syncthreads();
+    if (ok) {
+      int before = 0;
+      for (int ww = 0; ww < wid; ++ww) before += wcnt[ww][e];
+      sorted_ids[start[e] + run[e] + before + rank] = int32_t(i);
+    }
+    __syncthreads();
+    if (tid < E) {
+      int tot = 0;
+      for (int ww = 0; ww < 16; ++ww) tot += wcnt[ww][tid];
+      run[tid] += tot;
+    }
+    __syncthreads();
+  }
+}
+
+int launch_moe_align(const int32_t* ids, int64_t S, int E, int bm, int32_t* sorted_ids, int64_t cap,
+                     int32_t* tile_expert, int32_t* num_post_pad, hipStream_t s) {
+  DYLLM_REQUIRE(E >= 1 && E <= 64, "align supports 1..64 experts");
+  DYLLM_REQUIRE(bm > 0 && cap % bm == 0 && cap >= S + int64_t(E) * (bm - 1), "sorted-id capacity too small");
+  moe_align_kernel<<<1, 1024, 0, s>>>(ids, S, E, bm, sorted_ids, cap, tile_expert, num_post_pad);
+  return check_launch("moe_align_kernel");
+}
+
+// ---- combine: out[dst(t)] = bf16( sum_k y[t*top_k + k] ) ---------------------------------
+__global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __restrict__ y, int64_t T, int Hd, int top_k,
+                                                          uint16_t* __restrict__ out, const int64_t* __restrict__ dst_rows) {
+  const int64_t t = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int64_t d = dst_rows ? dst_rows[t] : t;
+  for (int c = lane; c < Hd / 8; c += 64) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = 0; k < top_k; ++k) {
+      const uint4 v = reinterpret_cast<const uint4*>(y + (t * top_k + k) * Hd)[c];
+      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] += __uint_as_float(vv[j] << 16);
+        acc[2 * j + 1] += __uint_as_float(vv[j] & 0xffff0000u);
+      }
+    }
+    uint4 o;
+    o.x = pack_bf16x2(acc[0], acc[1]);
+    o.y = pack_bf16x2(acc[2], acc[3]);
+    o.z = pack_bf16x2(acc[4], acc[5]);
+    o.w = pack_bf16x2(acc[6], acc[7]);
+    reinterpret_cast<uint4*>(out + d * Hd)[c] = o;
+  }
+}
+
+int launch_moe_combine(const uint16_t* y, int64_t T, int Hd, int top_k, uint16_t* out, const int64_t* dst_rows,
+                       hipStream_t s) {
+  DYLLM_REQUIRE(Hd % 8 == 0, "hidden size must be a multiple of 8");
+  if (T <= 0) return 0;
+  moe_combine_kernel<<<unsigned(cdiv(T, 4)), 256, 0, s>>>(y, T, Hd, top_k, out, dst_rows);
+  return check_launch("moe_combine_kernel");
+}
+
+}  // namespace dyllm

@@ -1,0 +1,381 @@
+"""Torch-facing wrappers of the HIP hot path, with the reference's native op signatures.
+
+Each wrapper validates like the reference's TORCH_CHECKs (raising RuntimeError), allocates
+outputs / workspace with the torch caching allocator, and enqueues the HIP kernels on the
+current torch stream through the C ABI (``_lib``). There is no CPU fallback.
+
+Reference signatures mirrored:
+  attention_sparse_varlen, fused_offset_launch -> dyllm.attention_ops (attention.cpp:197-204)
+  get_seqs_cuda, get_block_cuda, reset_full_cuda, reset_block_cuda, scatter_update_cuda
+                                               -> dyllm.cache (cache.cpp:19-25)
+  flash_attn_varlen_func                       -> flash-attn call sites attention.py:41-52, :76-87
+  tensor_parallel_cosine_mask                  -> parallel_state.py:52-66
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _check(t, name, dtype=None, dim=None, device=None):
+    if t is None:
+        raise RuntimeError(f"{name} must be defined")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor")
+    if device is not None and t.device != device:
+        raise RuntimeError(f"{name} must be on {device}")
+    if dtype is not None and t.dtype != dtype:
+        raise RuntimeError(f"{name} has an invalid dtype ({t.dtype}, expected {dtype})")
+    if dim is not None and t.dim() != dim:
+        raise RuntimeError(f"{name} must be a {dim}D tensor")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _i32(t):
+    return t if t.dtype == torch.int32 and t.is_contiguous() else t.to(torch.int32).contiguous()
+
+
+def _i64(t):
+    return t if t.dtype == torch.int64 and t.is_contiguous() else t.to(torch.int64).contiguous()
+
+
+# ---------------------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------------------
+def attention_sparse_varlen(Q, K, V, C, o_sal, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                            total_seqlen, cu_salientlens, idx_salient_row, cosine_stats, cosine_out,
+                            threshold=0.0, is_q_pruned=False, idx_salient_row_k=None, force_mask_v_rows=-1):
+    """Column-sparse attention + stats + tau test (attention.cpp:64-179). Returns O = C +
+    softmax(QK^T/sqrt(D)) V on non-salient rows and o_sal on salient rows; fills
+    cosine_stats [T,3] and cosine_out [T] (bool). ``force_mask_v_rows`` is accepted for
+    signature compatibility (the HIP kernel always skips salient-free key groups)."""
+    dev = Q.device
+    for t, n in ((Q, "Q"), (K, "K"), (V, "V"), (C, "C"), (o_sal, "o_sal")):
+        _check(t, n, torch.bfloat16, 3, dev)
+    for t, n in ((cu_seqlens_q, "cu_seqlens_q"), (cu_seqlens_k, "cu_seqlens_k"),
+                 (cu_salientlens, "cu_salientlens"), (idx_salient_row, "idx_salient_row")):
+        _check(t, n, torch.int32, 1, dev)
+    _check(cosine_stats, "cosine_stats", torch.float32, 2, dev)
+    _check(cosine_out, "cosine_out", torch.bool, 1, dev)
+    if K.shape != V.shape:
+        raise RuntimeError("K and V must have the same shape")
+    if C.shape != Q.shape:
+        raise RuntimeError("C must have the same shape as Q")
+    if o_sal.shape[0] != idx_salient_row.numel() or o_sal.shape[1:] != Q.shape[1:]:
+        raise RuntimeError("o_sal must be [idx_salient_row.numel(), Q.size(1), Q.size(2)]")
+    if total_seqlen != Q.shape[0]:
+        raise RuntimeError("total_seqlen must equal Q.size(0)")
+    if tuple(cosine_stats.shape) != (Q.shape[0], 3):
+        raise RuntimeError("cosine_stats must be [Q.size(0), 3]")
+    if cosine_out.numel() != Q.shape[0]:
+        raise RuntimeError("cosine_out must contain Q.size(0) elements")
+    if not (cu_seqlens_q.numel() >= 2 and cu_seqlens_q.numel() == cu_seqlens_k.numel() == cu_salientlens.numel()):
+        raise RuntimeError("cu_seqlens_q, cu_seqlens_k, and cu_salientlens must have the same B+1 length")
+    if force_mask_v_rows not in (-1, 0, 1):
+        raise RuntimeError("force_mask_v_rows must be -1, 0, or 1")
+    idx_k = None
+    if is_q_pruned:
+        _check(idx_salient_row_k, "idx_salient_row_k", torch.int32, 1, dev)
+        if idx_salient_row_k.numel() != idx_salient_row.numel():
+            raise RuntimeError("parallel Q/K pruning requires matching salient Q and K index counts")
+        idx_k = idx_salient_row_k
+    B = cu_seqlens_q.numel() - 1
+    H, D = Q.shape[1], Q.shape[2]
+    O = torch.empty_like(Q)
+    ws_bytes = _lib.load().dyllm_attention_sparse_workspace_bytes(B, H, Q.shape[0], int(max_seqlen_k))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    _lib.call("dyllm_attention_sparse_varlen", _ptr(Q), _ptr(K), _ptr(V), _ptr(C), _ptr(o_sal), _ptr(O), B, H,
+              K.shape[1], D, _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), int(max_seqlen_q), int(max_seqlen_k),
+              Q.shape[0], idx_salient_row.numel(), _ptr(cu_salientlens), _ptr(idx_salient_row), _ptr(idx_k),
+              _ptr(cosine_stats), _ptr(cosine_out), float(threshold), _ptr(ws), ws_bytes, _stream())
+    return O
+
+
+def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
+                           softmax_scale=None, causal=False, q_rows=None):
+    """Non-causal varlen attention (the two flash_attn_varlen_func call sites). With
+    ``q_rows`` (int32), compact row j of the output attends with q[q_rows[j]] and
+    cu_seqlens_q is the prefix of the compact rows -- the row-sparse call
+    ``flash_attn_varlen_func(q[idx], ...)`` without materialising q[idx]."""
+    if causal or dropout_p != 0.0:
+        raise RuntimeError("only non-causal attention without dropout is implemented")
+    dev = q.device
+    _check(q, "q", torch.bfloat16, 3, dev)
+    _check(k, "k", torch.bfloat16, 3, dev)
+    _check(v, "v", torch.bfloat16, 3, dev)
+    cu_q, cu_k = _i32(cu_seqlens_q), _i32(cu_seqlens_k)
+    D = q.shape[2]
+    scale = D ** -0.5 if softmax_scale is None else softmax_scale
+    if q_rows is not None:
+        q_rows = _i32(q_rows)
+        n_out = q_rows.numel()
+    else:
+        n_out = q.shape[0]
+    o = torch.empty((n_out, q.shape[1], D), dtype=q.dtype, device=dev)
+    if n_out == 0:
+        return o
+    _lib.call("dyllm_flash_attn_varlen", _ptr(q), _ptr(k), _ptr(v), _ptr(o), cu_q.numel() - 1, q.shape[1],
+              k.shape[1], D, _ptr(cu_q), _ptr(cu_k), int(max_seqlen_q), int(max_seqlen_k), float(scale),
+              _ptr(q_rows), _stream())
+    return o
+
+
+# ---------------------------------------------------------------------------------------
+# saliency / compaction
+# ---------------------------------------------------------------------------------------
+def tensor_parallel_cosine_mask(stats, threshold):
+    """cos < threshold from [T,3] fp32 stats (parallel_state.py:52-66, world size 1)."""
+    _check(stats, "stats", torch.float32, 2)
+    out = torch.empty(stats.shape[0], dtype=torch.bool, device=stats.device)
+    _lib.call("dyllm_cosine_mask", _ptr(stats), stats.shape[0], float(threshold), _ptr(out), _stream())
+    return out
+
+
+def saliency_stats(c_new, c_old, threshold):
+    """Standalone saliency pass over two bf16 row sets: ([T,3] fp32 stats, [T] bool mask)."""
+    _check(c_new, "c_new", torch.bfloat16)
+    _check(c_old, "c_old", torch.bfloat16)
+    if c_new.shape != c_old.shape:
+        raise RuntimeError("c_new and c_old must have the same shape")
+    T = c_new.shape[0]
+    D = c_new.numel() // max(T, 1)
+    stats = torch.empty(T, 3, dtype=torch.float32, device=c_new.device)
+    mask = torch.empty(T, dtype=torch.bool, device=c_new.device)
+    _lib.call("dyllm_saliency_stats", _ptr(c_new), _ptr(c_old), T, D, float(threshold), _ptr(stats), _ptr(mask),
+              _stream())
+    return stats, mask
+
+
+class Compacted:
+    """Device results of one compaction; ``count`` stays on the device until asked for."""
+
+    def __init__(self, idx64, idx32, idx_k, cu_salientlens, count):
+        self.idx64, self.idx32, self.idx_k = idx64, idx32, idx_k
+        self.cu_salientlens, self.count = cu_salientlens, count
+
+    def n(self) -> int:
+        return int(self.count.item())
+
+    def trimmed(self):
+        n = self.n()
+        return (self.idx64[:n], self.idx32[:n], None if self.idx_k is None else self.idx_k[:n],
+                self.cu_salientlens)
+
+
+def salient_compact(mask, cu_seqlens_q, cu_promptlens=None):
+    """torch.nonzero(mask) + searchsorted(idxs, cu_seqlens_q) + fused_offset, on the device
+    (attention.py:147-166). Index buffers are capacity-sized; see ``Compacted``."""
+    dev = mask.device
+    _check(mask, "mask", None, 1, dev)
+    if mask.dtype not in (torch.bool, torch.uint8):
+        raise RuntimeError("mask must be bool or uint8")
+    T = mask.numel()
+    cu_q = _i32(cu_seqlens_q)
+    B = cu_q.numel() - 1
+    idx64 = torch.empty(max(T, 1), dtype=torch.int64, device=dev)
+    idx32 = torch.empty(max(T, 1), dtype=torch.int32, device=dev)
+    idx_k = torch.empty(max(T, 1), dtype=torch.int64, device=dev) if cu_promptlens is not None else None
+    cu_p = _i32(cu_promptlens) if cu_promptlens is not None else None
+    cu_sal = torch.empty(B + 1, dtype=torch.int32, device=dev)
+    count = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.call("dyllm_salient_compact", _ptr(mask), T, _ptr(cu_q), B, _ptr(cu_p), _ptr(idx64), _ptr(idx32),
+              _ptr(idx_k), _ptr(cu_sal), _ptr(count), _stream())
+    return Compacted(idx64, idx32, idx_k, cu_sal, count)
+
+
+def fused_offset_launch(idxs, num_idxs, cu_promptlens, cu_salientlens, out_tensor, max_threads):
+    """attention_aux_kernels.cu:173-200 (same argument checks)."""
+    dev = idxs.device
+    for t, n in ((idxs, "idxs"), (num_idxs, "num_idxs"), (cu_promptlens, "cu_promptlens"),
+                 (cu_salientlens, "cu_salientlens")):
+        _check(t, n, torch.int32, 1, dev)
+    if num_idxs.numel() != 1:
+        raise RuntimeError("num_idxs must contain exactly one element")
+    if cu_promptlens.numel() != cu_salientlens.numel():
+        raise RuntimeError("cu_promptlens and cu_salientlens must have the same length")
+    _check(out_tensor, "out_tensor", torch.int64, 1, dev)
+    if not (0 <= max_threads <= out_tensor.numel()):
+        raise RuntimeError("max_threads must fit out_tensor")
+    if max_threads == 0:
+        return
+    _lib.call("dyllm_fused_offset_launch", _ptr(idxs), _ptr(num_idxs), _ptr(cu_promptlens), _ptr(cu_salientlens),
+              cu_promptlens.numel() - 1, _ptr(out_tensor), int(max_threads), _stream())
+
+
+# ---------------------------------------------------------------------------------------
+# packed row caches (dyllm.cache)
+# ---------------------------------------------------------------------------------------
+def _row_bytes(t):
+    return t.shape[1] * t.element_size()
+
+
+def _check_cache(cache, seq_starts, seq_ids):
+    _check(cache, "cache", None, 2)
+    _check(seq_starts, "seq_starts", torch.int64, 1)
+    _check(seq_ids, "seq_ids", torch.int64, 1)
+    if (cache.shape[1] * cache.element_size()) % 16 != 0:
+        raise RuntimeError("row size must be a multiple of 16 bytes (D % 8 == 0 for bf16)")
+
+
+def get_seqs_cuda(cache, seq_starts, cu_seqlens, seq_ids, total_seqlen):
+    _check_cache(cache, seq_starts, seq_ids)
+    cu = _i32(cu_seqlens)
+    out = torch.empty((int(total_seqlen), cache.shape[1]), dtype=cache.dtype, device=cache.device)
+    _lib.call("dyllm_get_seqs", _ptr(cache), _ptr(out), _row_bytes(cache), _ptr(seq_starts), _ptr(cu),
+              _ptr(seq_ids), seq_ids.numel(), int(total_seqlen), _stream())
+    return out
+
+
+def get_block_cuda(cache, seq_starts, cu_seqlens, cu_seqlens_q, seq_ids, total_seqlen):
+    _check_cache(cache, seq_starts, seq_ids)
+    cu, cq = _i32(cu_seqlens), _i32(cu_seqlens_q)
+    out = torch.empty((int(total_seqlen), cache.shape[1]), dtype=cache.dtype, device=cache.device)
+    _lib.call("dyllm_get_block", _ptr(cache), _ptr(out), _row_bytes(cache), _ptr(seq_starts), _ptr(cu), _ptr(cq),
+              _ptr(seq_ids), seq_ids.numel(), int(total_seqlen), _stream())
+    return out
+
+
+def reset_full_cuda(cache, inp, seq_starts, cu_seqlens, seq_ids, total_seqlen):
+    _check_cache(cache, seq_starts, seq_ids)
+    _check(inp, "in", cache.dtype, 2)
+    cu = _i32(cu_seqlens)
+    _lib.call("dyllm_reset_full", _ptr(cache), _ptr(inp), _row_bytes(cache), _ptr(seq_starts), _ptr(cu),
+              _ptr(seq_ids), seq_ids.numel(), int(total_seqlen), _stream())
+
+
+def reset_block_cuda(cache, inp, seq_starts, cu_seqlens, cu_seqlens_q, seq_ids, total_seqlen):
+    _check_cache(cache, seq_starts, seq_ids)
+    _check(inp, "in", cache.dtype, 2)
+    cu, cq = _i32(cu_seqlens), _i32(cu_seqlens_q)
+    _lib.call("dyllm_reset_block", _ptr(cache), _ptr(inp), _row_bytes(cache), _ptr(seq_starts), _ptr(cu), _ptr(cq),
+              _ptr(seq_ids), seq_ids.numel(), int(total_seqlen), _stream())
+
+
+def scatter_update_cuda(cache, new_vals, row_idx, cu_seqlens, seq_starts, seq_ids):
+    _check_cache(cache, seq_starts, seq_ids)
+    new_vals = new_vals.reshape(new_vals.shape[0], -1).contiguous()
+    _check(new_vals, "new_vals", cache.dtype, 2)
+    if new_vals.shape[1] != cache.shape[1]:
+        raise RuntimeError("new_vals row width must match the cache")
+    ri = _i64(row_idx)
+    if ri.numel() != new_vals.shape[0]:
+        raise RuntimeError("row_idx must have one entry per new row")
+    cu = _i32(cu_seqlens)
+    _lib.call("dyllm_scatter_update", _ptr(cache), _ptr(new_vals), _row_bytes(cache), _ptr(ri), ri.numel(),
+              _ptr(cu), _ptr(seq_starts), _ptr(seq_ids), seq_ids.numel(), _stream())
+
+
+def scatter_dest_rows(row_idx, cu_seqlens, seq_starts, seq_ids):
+    ri = _i64(row_idx)
+    cu = _i32(cu_seqlens)
+    dest = torch.empty_like(ri)
+    if ri.numel():
+        _lib.call("dyllm_scatter_dest_rows", _ptr(ri), ri.numel(), _ptr(cu), _ptr(seq_starts), _ptr(seq_ids),
+                  seq_ids.numel(), _ptr(dest), _stream())
+    return dest
+
+
+def gather_rows_2D(x, row_idx):
+    """utils/util.py:19-36: x[row_idx] for a [L, D] tensor."""
+    _check(x, "x", None, 2)
+    ri = _i64(row_idx)
+    out = torch.empty((ri.numel(), x.shape[1]), dtype=x.dtype, device=x.device)
+    if ri.numel():
+        _lib.call("dyllm_gather_rows", _ptr(x), _ptr(out), _row_bytes(x), _ptr(ri), ri.numel(), _stream())
+    return out
+
+
+# ---------------------------------------------------------------------------------------
+# FFN / MoE
+# ---------------------------------------------------------------------------------------
+def swiglu_ffn(x, w_gate_up, w_down, rows_idx=None, out=None, out_rows=None):
+    """down(silu(a Wg^T) * (a Wu^T)) for a = x[rows_idx] (or all rows of x). With
+    ``out``/``out_rows`` the result rows are written to out[out_rows[m]] (in-place scatter
+    into a cache); otherwise a new [M, hidden] tensor is returned."""
+    _check(x, "x", torch.bfloat16, 2)
+    _check(w_gate_up, "w_gate_up", torch.bfloat16, 2)
+    _check(w_down, "w_down", torch.bfloat16, 2)
+    hidden = x.shape[1]
+    inter = w_gate_up.shape[0] // 2
+    if w_gate_up.shape[1] != hidden or tuple(w_down.shape) != (hidden, inter):
+        raise RuntimeError("weights must be w_gate_up [2I, hidden] and w_down [hidden, I]")
+    ri = _i32(rows_idx) if rows_idx is not None else None
+    M = ri.numel() if ri is not None else x.shape[0]
+    if out is None:
+        out = torch.empty((M, hidden), dtype=x.dtype, device=x.device)
+        orow = None
+    else:
+        _check(out, "out", torch.bfloat16, 2)
+        orow = _i64(out_rows) if out_rows is not None else None
+    if M == 0:
+        return out
+    ws_bytes = _lib.load().dyllm_swiglu_ffn_workspace_bytes(M, inter)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    _lib.call("dyllm_swiglu_ffn", _ptr(x), x.stride(0), _ptr(ri), M, _ptr(w_gate_up), _ptr(w_down), hidden, inter,
+              _ptr(ws), ws_bytes, _ptr(out), _ptr(orow), _stream())
+    return out
+
+
+def moe_gate(hidden_states, router_weight, top_k, renormalize=False):
+    """fp32 softmax top-k routing (fused_moe.py:375-408 without the DiffusionGemma extras)."""
+    _check(hidden_states, "hidden_states", torch.bfloat16, 2)
+    rw = router_weight.to(torch.bfloat16).contiguous()
+    T = hidden_states.shape[0]
+    w = torch.empty((T, top_k), dtype=torch.bfloat16, device=hidden_states.device)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=hidden_states.device)
+    if T:
+        _lib.call("dyllm_moe_gate", _ptr(hidden_states), None, T, hidden_states.shape[1], _ptr(rw), rw.shape[0],
+                  int(top_k), int(bool(renormalize)), _ptr(w), _ptr(ids), _stream())
+    return w, ids
+
+
+def moe_align_block_size(topk_ids, block_size, num_experts):
+    """Device moe_align_block_size (fused_moe.py:37-85). Returns (sorted_token_ids,
+    expert_ids, num_tokens_post_pad) with capacity-sized id buffers."""
+    ids = _i32(topk_ids).reshape(-1)
+    S = ids.numel()
+    cap = -(-(S + num_experts * (block_size - 1)) // block_size) * block_size
+    sorted_ids = torch.empty(cap, dtype=torch.int32, device=ids.device)
+    tile_e = torch.empty(cap // block_size, dtype=torch.int32, device=ids.device)
+    npp = torch.empty(1, dtype=torch.int32, device=ids.device)
+    _lib.call("dyllm_moe_align_block_size", _ptr(ids), S, num_experts, block_size, _ptr(sorted_ids), cap,
+              _ptr(tile_e), _ptr(npp), _stream())
+    return sorted_ids, tile_e, npp
+
+
+def fused_experts(hidden_states, w1, w2, topk_weights, topk_ids, activation="silu", out=None, out_rows=None):
+    """fused_experts (fused_moe.py:269-335) with SiLU gating."""
+    if activation != "silu":
+        raise RuntimeError("only the silu activation (LLaDA-MoE) is implemented")
+    x = hidden_states
+    _check(x, "hidden_states", torch.bfloat16, 2)
+    _check(w1, "w1", torch.bfloat16, 3)
+    _check(w2, "w2", torch.bfloat16, 3)
+    T, hidden = x.shape
+    E, two_i, _ = w1.shape
+    inter = two_i // 2
+    top_k = topk_ids.shape[1]
+    tw = topk_weights.to(torch.bfloat16).contiguous()
+    ti = _i32(topk_ids)
+    if out is None:
+        out = torch.empty((T, hidden), dtype=x.dtype, device=x.device)
+        orow = None
+    else:
+        orow = _i64(out_rows) if out_rows is not None else None
+    if T == 0:
+        return out
+    ws_bytes = _lib.load().dyllm_fused_experts_workspace_bytes(T, top_k, E, hidden, inter)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+    _lib.call("dyllm_fused_experts", _ptr(x), None, T, hidden, _ptr(w1), _ptr(w2), E, inter, _ptr(tw), _ptr(ti),
+              top_k, _ptr(out), _ptr(orow), _ptr(ws), ws_bytes, _stream())
+    return out

@@ -1,0 +1,163 @@
+/*
+ * dyllm_hip.h -- C ABI of the MI355X (gfx950) DyLLM saliency hot path.
+ *
+ * Every entry point takes raw device pointers, element counts and a hipStream_t (passed as
+ * void*), enqueues its kernels on that stream without any host synchronisation, and
+ * returns 0 on success or a non-zero status with a message available from
+ * dyllm_last_error() (thread-local). No entry point allocates device memory: temporaries
+ * come from a caller-provided workspace whose size the matching *_workspace_bytes()
+ * reports. bf16 tensors are passed as uint16_t bit patterns, row-major and contiguous
+ * ([tokens, heads, head_dim] == [tokens, heads*head_dim]).
+ *
+ * Reference interfaces replaced (paths relative to the DyLLM source tree):
+ *   dyllm_attention_sparse_varlen  <- attention_sparse_varlen_cuda, dyllm/csrc/attention/attention.cpp:64-179
+ *                                     (pybind name "attention_sparse_varlen", attention.cpp:198-203)
+ *   dyllm_fused_offset_launch      <- dyllm_launch_fused_offset, attention_aux_kernels.cu:173-200
+ *                                     (pybind name "fused_offset_launch", attention.cpp:204)
+ *   dyllm_get_seqs / get_block / reset_full / reset_block / scatter_update
+ *                                  <- get_seqs_cuda, get_block_cuda, reset_full_cuda, reset_block_cuda,
+ *                                     scatter_update_cuda (dyllm/csrc/cache/cache.cpp:19-25,
+ *                                     cache_kernels.cu:66-460)
+ *   dyllm_flash_attn_varlen        <- flash_attn_varlen_func (third-party flash-attn 2.8.3) as called at
+ *                                     dyllm/model_executor/layers/attention.py:41-52 and :76-87
+ *   dyllm_cosine_mask              <- tensor_parallel_cosine_mask, dyllm/distributed/parallel_state.py:52-66
+ *   dyllm_salient_compact          <- torch.nonzero + torch.searchsorted + fused_offset at attention.py:147-166
+ *   dyllm_gather_rows              <- gather_rows_2D, dyllm/utils/util.py:19-36
+ *   dyllm_swiglu_ffn               <- LLaDAMLP.forward, dyllm/model_executor/models/llada.py:38-43
+ *                                     (+ MLPcache.scatter_update, mlp_cache_manage.py:24-40)
+ *   dyllm_moe_gate                 <- moe_gate, dyllm/model_executor/layers/fused_moe.py:375-408
+ *   dyllm_moe_align_block_size     <- moe_align_block_size, fused_moe.py:37-85
+ *   dyllm_fused_experts            <- fused_experts, fused_moe.py:269-335
+ *   dyllm_saliency_stats           <- the statistics epilogue of attention_ops_kernels_sm80.cu:436-481
+ *                                     as a standalone pass over two bf16 row sets
+ */
+#ifndef DYLLM_HIP_H_
+#define DYLLM_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Last error message of the calling thread ("" when none). */
+const char* dyllm_last_error(void);
+/* ABI version of this library. */
+int dyllm_abi_version(void);
+
+/* ---- attention ------------------------------------------------------------------------ */
+
+/* Workspace for dyllm_attention_sparse_varlen. */
+size_t dyllm_attention_sparse_workspace_bytes(int batch, int num_heads, int64_t total_q, int max_seqlen_k);
+
+/* Column-sparse attention + saliency statistics + tau test (attention.cpp:64-179).
+ * q, c, o: [total_q, H, D]; k, v_delta: [total_k, H_kv, D]; o_sal: [num_salient, H, D].
+ * idx_salient_q (int32, Q space) lists the rows whose output is o_sal; idx_salient_k (int32,
+ * K space) the key rows where v_delta may be non-zero (NULL: same as idx_salient_q).
+ * cosine_stats [total_q, 3] fp32 is overwritten (no zero-initialisation needed);
+ * cosine_out [total_q] bytes: 1 where cos < threshold. head_dim must be 128. */
+int dyllm_attention_sparse_varlen(const void* q, const void* k, const void* v_delta, const void* c,
+                                  const void* o_sal, void* o, int batch, int num_heads, int num_kv_heads,
+                                  int head_dim, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int max_seqlen_q, int max_seqlen_k, int64_t total_q, int num_salient,
+                                  const int32_t* cu_salientlens, const int32_t* idx_salient_q,
+                                  const int32_t* idx_salient_k, float* cosine_stats, uint8_t* cosine_out,
+                                  float threshold, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Non-causal varlen softmax attention, scale = softmax_scale (head_dim must be 128).
+ * q_rows == NULL: rows are q[cu_seqlens_q[b] .. cu_seqlens_q[b+1]) -> o rows at the same index.
+ * q_rows != NULL: cu_seqlens_q is the prefix of a compact row list (cu_salientlens); compact
+ * row j reads q[q_rows[j]] and writes o[j] (the row-sparse call at attention.py:76-87).
+ * max_seqlen_q bounds the rows of one sequence. */
+int dyllm_flash_attn_varlen(const void* q, const void* k, const void* v, void* o, int batch, int num_heads,
+                            int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
+                            const int32_t* cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, float softmax_scale,
+                            const int32_t* q_rows, void* stream);
+
+/* ---- saliency and compaction ----------------------------------------------------------- */
+
+/* mask[t] = cos(stats[t]) < threshold (parallel_state.py:62-66). */
+int dyllm_cosine_mask(const float* stats, int64_t rows, float threshold, uint8_t* mask, void* stream);
+
+/* Standalone saliency pass: stats[t] = {sum new*old, sum new^2, sum old^2} of bf16 rows of
+ * width dim, then the tau test. */
+int dyllm_saliency_stats(const void* c_new, const void* c_old, int64_t rows, int64_t dim, float threshold,
+                         float* stats, uint8_t* mask, void* stream);
+
+/* Stream compaction of a byte mask over rows [0, rows): ascending salient indices
+ * (idx64, and idx32 when non-NULL), cu_salientlens[b] = #indices < cu_seqlens_q[b]
+ * for b in [0, batch], count[0] = number of indices, and, when idx_k != NULL,
+ * idx_k[t] = idx64[t] + cu_promptlens[seg(t)+1] (fused_offset). idx buffers need
+ * capacity `rows`. Runs on the device; the caller reads count[0] when it needs it. */
+int dyllm_salient_compact(const uint8_t* mask, int64_t rows, const int32_t* cu_seqlens_q, int batch,
+                          const int32_t* cu_promptlens, int64_t* idx64, int32_t* idx32, int64_t* idx_k,
+                          int32_t* cu_salientlens, int32_t* count, void* stream);
+
+/* fused_offset_launch (attention_aux_kernels.cu:173-200): out[t] = idxs[t] +
+ * cu_promptlens[seg(t)+1] for t < min(*num_idxs, max_threads); num_groups = batch. */
+int dyllm_fused_offset_launch(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_promptlens,
+                              const int32_t* cu_salientlens, int num_groups, int64_t* out, int64_t max_threads,
+                              void* stream);
+
+/* ---- packed row caches (row_bytes: bytes per row, multiple of 16) ---------------------- */
+int dyllm_get_seqs(const void* cache, void* out, int64_t row_bytes, const int64_t* seq_starts,
+                   const int32_t* cu_seqlens, const int64_t* seq_ids, int batch, int64_t total_rows, void* stream);
+int dyllm_get_block(const void* cache, void* out, int64_t row_bytes, const int64_t* seq_starts,
+                    const int32_t* cu_seqlens_k, const int32_t* cu_seqlens_q, const int64_t* seq_ids, int batch,
+                    int64_t total_rows, void* stream);
+int dyllm_reset_full(void* cache, const void* in, int64_t row_bytes, const int64_t* seq_starts,
+                     const int32_t* cu_seqlens, const int64_t* seq_ids, int batch, int64_t total_rows, void* stream);
+int dyllm_reset_block(void* cache, const void* in, int64_t row_bytes, const int64_t* seq_starts,
+                      const int32_t* cu_seqlens_k, const int32_t* cu_seqlens_q, const int64_t* seq_ids, int batch,
+                      int64_t total_rows, void* stream);
+int dyllm_scatter_update(void* cache, const void* new_vals, int64_t row_bytes, const int64_t* row_idx, int64_t rows,
+                         const int32_t* cu_seqlens, const int64_t* seq_starts, const int64_t* seq_ids, int batch,
+                         void* stream);
+/* Destination cache row of each packed row index (the address part of scatter_update). */
+int dyllm_scatter_dest_rows(const int64_t* row_idx, int64_t rows, const int32_t* cu_seqlens,
+                            const int64_t* seq_starts, const int64_t* seq_ids, int batch, int64_t* dest,
+                            void* stream);
+/* out[m] = x[idx[m]] */
+int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t* idx, int64_t rows, void* stream);
+
+/* ---- FFN ------------------------------------------------------------------------------- */
+
+/* Bytes of the intermediate buffer dyllm_swiglu_ffn needs: rows * intermediate * 2. */
+size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate);
+
+/* Gathered SwiGLU FFN: for m < rows, a = x[rows_idx ? rows_idx[m] : m] (row stride ld_x),
+ * h = silu(a W_g^T) * (a W_u^T), y = h W_d^T written to out[out_rows ? out_rows[m] : m]
+ * (row stride hidden). w_gate_up: [2*intermediate, hidden] (gate rows first);
+ * w_down: [hidden, intermediate]. */
+int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
+                     const void* w_down, int hidden, int intermediate, void* workspace, size_t workspace_bytes,
+                     void* out, const int64_t* out_rows, void* stream);
+
+/* ---- MoE ------------------------------------------------------------------------------- */
+
+/* Router: topk_weights (bf16) / topk_ids (int32) [tokens, top_k] from fp32 softmax of
+ * x[rows_idx[t] or t] . router_w^T; router_w: [num_experts, hidden] bf16; num_experts <= 64. */
+int dyllm_moe_gate(const void* x, const int32_t* rows_idx, int64_t tokens, int hidden, const void* router_w,
+                   int num_experts, int top_k, int renormalize, void* topk_weights, int32_t* topk_ids, void* stream);
+
+/* moe_align_block_size on the device. capacity >= tokens*top_k + E*(block-1), multiple of block. */
+int dyllm_moe_align_block_size(const int32_t* topk_ids, int64_t slots, int num_experts, int block,
+                               int32_t* sorted_token_ids, int64_t capacity, int32_t* tile_expert,
+                               int32_t* num_post_pad, void* stream);
+
+size_t dyllm_fused_experts_workspace_bytes(int64_t tokens, int top_k, int num_experts, int hidden,
+                                           int intermediate);
+
+/* fused_experts with SiLU gating: w1 [E, 2*I, hidden], w2 [E, hidden, I]; routing from
+ * dyllm_moe_gate. out[out_rows ? out_rows[t] : t] = sum_k w_k * FFN_{e_k}(x_t), bf16. */
+int dyllm_fused_experts(const void* x, const int32_t* rows_idx, int64_t tokens, int hidden, const void* w1,
+                        const void* w2, int num_experts, int intermediate, const void* topk_weights,
+                        const int32_t* topk_ids, int top_k, void* out, const int64_t* out_rows, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DYLLM_HIP_H_ */
