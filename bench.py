@@ -1,0 +1,273 @@
+"""Salient-path throughput of one sparse denoise step at the LLaDA-8B shape (config 1).
+
+Workload (one MI355X): 32 layers, hidden 4096, 32 heads x 128,
+SwiGLU 12288, batch 8 x 1024 rows (256 prompt + 768 response), tau = 0.99, a Q-pruned sparse
+step. Random-init bf16 weights N(0, 0.02); K/V/Q ~ N(0, 1). The caches hold a dense
+"step 1" (our dense attention); 15% of the response rows of every sequence are perturbed in
+the cached context with Gaussian noise of 0.5 x row RMS and get fresh K/V rows, which makes
+~15% of the rows salient at every layer, as in the reference's synthetic recipe.
+
+One step = for every layer: K-cache scatter of the salient rows, dV + V-cache update,
+row-sparse attention of the salient queries vs the full cached K/V, column-sparse attention
+with the saliency statistics and the tau test, compaction of the next salient set (one host
+read of its size, as the reference's torch.nonzero), gathered SwiGLU GEMMs with the
+scatter into the FFN cache, and the FFN-cache read-back of all queried rows. The dense
+projections/norms on either side of the path are outside the timed region (their inputs are
+pre-generated per layer). The caches are restored between steps (untimed) so every timed
+step sees the same salient fraction.
+
+value = B * Lq / step time (tokens/s). The roofline object is for the dominant kernel, the
+gathered gate_up SwiGLU GEMM, timed with HIP events on its own launches.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+CONFIG1 = dict(layers=32, hidden=4096, heads=32, kv_heads=32, head_dim=128, inter=12288, batch=8, prompt=256,
+               response=768, tau=0.99, perturb=0.15)
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def build_workload(cfg, layers, device, seed=0):
+    import torch
+
+    from dyllm_amd import ops
+    from dyllm_amd.engine.cache_manager import CacheManager
+    from dyllm_amd.model_executor.layers.attention import Attention
+    from dyllm_amd.model_executor.models.llada import LLaDAMLP
+    from dyllm_amd.utils.context import set_context
+    from dyllm_amd.utils.metadata import get_metadata
+
+    B, P, R = cfg["batch"], cfg["prompt"], cfg["response"]
+    L = P + R
+    H, Hkv, D, hid, inter = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["hidden"], cfg["inter"]
+    Tk, Tq = B * L, B * R
+    g = torch.Generator(device=device).manual_seed(seed)
+    gcpu = torch.Generator().manual_seed(seed)
+    md = get_metadata()
+    md.running_seqs = list(range(B))
+    md.running_seqs_tensor = torch.arange(B, dtype=torch.long, device=device)
+    md.finished_seqs = []
+    cu_k_cpu = [i * L for i in range(B + 1)]
+    cu_q_cpu = [i * R for i in range(B + 1)]
+    cu_p_cpu = [i * P for i in range(B + 1)]
+    i32 = dict(dtype=torch.int32, device=device)
+    cu_k, cu_q, cu_p = (torch.tensor(x, **i32) for x in (cu_k_cpu, cu_q_cpu, cu_p_cpu))
+
+    # salient rows: the same 15% of each sequence's response rows at every layer
+    n_per = int(round(cfg["perturb"] * R))
+    sq, sk = [], []
+    for b in range(B):
+        sel = torch.randperm(R, generator=gcpu)[:n_per].sort().values
+        sq += (b * R + sel).tolist()
+        sk += (b * L + P + sel).tolist()
+    S_q = torch.tensor(sq, dtype=torch.long, device=device)
+    S_k = torch.tensor(sk, dtype=torch.long, device=device)
+    cu_s = torch.tensor([i * n_per for i in range(B + 1)], **i32)
+
+    def randn(*shape, std=1.0):
+        x = torch.empty(*shape, dtype=torch.float32, device=device)
+        x.normal_(0.0, std, generator=g)
+        return x.to(torch.bfloat16)
+
+    state = []
+    for _ in range(layers):
+        # dense "step 1": fill K, V and context caches (attention.py:39-62)
+        set_context(True, cu_seqlens_q=cu_k, cu_seqlens_q_cpu=cu_k_cpu, cu_seqlens_k=cu_k,
+                    cu_seqlens_k_cpu=cu_k_cpu, max_seqlen_q=L, max_seqlen_k=L, context_lens_cpu=[L] * B,
+                    total_seqlen=Tk, total_seqlen_k=Tk)
+        attn = Attention(H, D, D ** -0.5, Hkv, cfg["tau"], device=device)
+        k_cache = CacheManager(Hkv * D, device=torch.device(device))
+        mlp = LLaDAMLP(hid, inter, device=device, gen=g)
+        q_all, k_all, v_all = randn(Tk, H, D), randn(Tk, Hkv, D), randn(Tk, Hkv, D)
+        k_cache.reset_full(k_all.view(Tk, -1), md.running_seqs_tensor, md.running_seqs)
+        attn(q_all, k_all, v_all)
+        mlp.cache_update(randn(Tk, hid))
+        # perturb the cached context of the salient rows (sigma = 0.5 x row RMS)
+        c = attn.context_cache.cache
+        rows = c[S_k].float()
+        rms = rows.pow(2).mean(-1, keepdim=True).sqrt()
+        c[S_k] = (rows + 0.5 * rms * randn(len(sk), H * D).float()).to(torch.bfloat16)
+        resp = torch.cat([torch.arange(b * L + P, (b + 1) * L, device=device) for b in range(B)])
+        q = q_all[resp].contiguous()
+        k_new = (k_all[resp].float() + 0.1 * randn(Tq, Hkv, D).float()).to(torch.bfloat16)
+        v_new = (v_all[resp].float() + 0.1 * randn(Tq, Hkv, D).float()).to(torch.bfloat16)
+        del q_all, k_all, v_all
+        state.append(dict(attn=attn, k_cache=k_cache, mlp=mlp, q=q, k_new=k_new.view(Tq, -1),
+                          v_new=v_new.view(Tq, -1), c_saved=attn.context_cache.cache.clone(),
+                          v_saved=attn.v_cache.cache.clone()))
+    torch.cuda.synchronize()
+
+    def set_sparse_context():
+        return set_context(False, cu_seqlens_q=cu_q, cu_seqlens_q_cpu=cu_q_cpu, cu_seqlens_k=cu_k,
+                           cu_seqlens_k_cpu=cu_k_cpu, cu_promptlens=cu_p, max_seqlen_q=R, max_seqlen_k=L,
+                           context_lens_cpu=[L] * B, cu_salientlens=cu_s, idx_salient_row=S_q,
+                           idx_salient_row_i32=S_q.to(torch.int32), idx_salient_row_k=S_k, total_seqlen=Tq,
+                           total_seqlen_k=Tk)
+
+    def restore():
+        for st in state:
+            st["attn"].context_cache.cache.copy_(st["c_saved"])
+            st["attn"].v_cache.cache.copy_(st["v_saved"])
+
+    def step(events=None, n_sal=None):
+        ctx = set_sparse_context()
+        for li, st in enumerate(state):
+            idx = ctx.idx_salient_row
+            if n_sal is not None:
+                n_sal.append(idx.numel())
+            k_sal = ops.gather_rows_2D(st["k_new"], idx)
+            v_sal = ops.gather_rows_2D(st["v_new"], idx)
+            st["k_cache"].scatter_update(md.running_seqs_tensor, ctx.idx_salient_row_k, k_sal)
+            k_full = st["k_cache"].get_seqs(md.running_seqs_tensor, md.running_seqs).view(-1, Hkv, D)
+            o = st["attn"](st["q"], k_full, v_sal.view(-1, Hkv, D))
+            st["mlp"].forward_salient(o.view(Tq, H * D), gate_up_events=None if events is None else events[li])
+        return ctx
+
+    return dict(step=step, restore=restore, Tq=Tq, Tk=Tk, n_per=n_per, S_q=S_q, state=state)
+
+
+def cpu_baseline(cfg, n_sal, threads):
+    """One layer of the same workload through the CPU oracle (fp32 torch / numpy),
+    extrapolated to the model's layer count."""
+    import numpy as np
+    import torch
+
+    from oracle import dyllm_oracle as ref
+
+    torch.set_num_threads(threads)
+    B, P, R = cfg["batch"], cfg["prompt"], cfg["response"]
+    L = P + R
+    H, Hkv, D, hid, inter = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["hidden"], cfg["inter"]
+    Tk, Tq = B * L, B * R
+    g = torch.Generator().manual_seed(1)
+    bf = torch.bfloat16
+    q = torch.randn(Tq, H, D, generator=g).to(bf)
+    k = torch.randn(Tk, Hkv, D, generator=g).to(bf)
+    v = torch.randn(Tk, Hkv, D, generator=g).to(bf)
+    c = torch.randn(Tq, H, D, generator=g).to(bf)
+    n_per = max(1, n_sal // B)
+    rng = np.random.default_rng(1)
+    idx_q, idx_k = [], []
+    for b in range(B):
+        sel = np.sort(rng.choice(R, size=n_per, replace=False))
+        idx_q += (b * R + sel).tolist()
+        idx_k += (b * L + P + sel).tolist()
+    idx_q, idx_k = np.asarray(idx_q), np.asarray(idx_k)
+    cu_q = np.arange(B + 1) * R
+    cu_k = np.arange(B + 1) * L
+    cu_p = np.arange(B + 1) * P
+    cu_s = np.arange(B + 1) * n_per
+    dv = torch.zeros_like(k)
+    dv[idx_k] = (0.1 * torch.randn(len(idx_k), Hkv, D, generator=g)).to(bf)
+    w_gu = (0.02 * torch.randn(2 * inter, hid, generator=g)).to(bf)
+    w_d = (0.02 * torch.randn(hid, inter, generator=g)).to(bf)
+    t0 = time.perf_counter()
+    o_sal = ref.flash_attn_varlen(q[torch.from_numpy(idx_q)], k, v, cu_s, cu_k)
+    new_c, _, mask = ref.attention_sparse_varlen(q, k, dv, c, o_sal, cu_q, cu_k, idx_q, cfg["tau"])
+    idxs, cu_sal = ref.compact(mask.numpy(), cu_q)
+    ref.fused_offset(idxs, cu_p, cu_sal)
+    ref.swiglu_ffn(new_c.reshape(Tq, -1)[torch.from_numpy(idx_q)], w_gu, w_d)
+    t_layer = time.perf_counter() - t0
+    return dict(value=Tq / (t_layer * cfg["layers"]), unit="tokens/s", cores=threads, kind="port",
+                sample=f"1 of {cfg['layers']} layers at full config-1 shape ({n_sal} salient rows), "
+                       f"{t_layer:.2f} s, x{cfg['layers']}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers than the model has")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU; the hot path is not sharded across GPUs "
+              "(see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    cfg = dict(CONFIG1)
+    layers = args.layers or cfg["layers"]
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    print(f"[bench] building config-1 workload ({layers} layers)", file=sys.stderr, flush=True)
+    wl = build_workload(cfg, layers, dev)
+    for _ in range(args.warmup):
+        wl["restore"]()
+        wl["step"]()
+    torch.cuda.synchronize()
+
+    total_ms = 0.0
+    gate_ms, n_sals = [], []
+    for _ in range(args.steps):
+        wl["restore"]()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(layers)]
+        n_sal = []
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        wl["step"](events=evs, n_sal=n_sal)
+        torch.cuda.synchronize()
+        total_ms += (time.perf_counter() - t0) * 1e3
+        gate_ms += [a.elapsed_time(b) for a, b in evs]
+        n_sals += n_sal
+    ms_per_step = total_ms / args.steps
+    Tq = wl["Tq"]
+    value = Tq / (ms_per_step / 1e3)
+
+    hid, inter = cfg["hidden"], cfg["inter"]
+    avg_n = sum(n_sals) / len(n_sals)
+    flops = 2.0 * avg_n * hid * 2 * inter
+    avg_gate_ms = sum(gate_ms) / len(gate_ms)
+    achieved = flops / (avg_gate_ms * 1e-3) / 1e12
+    print(f"[bench] {ms_per_step:.3f} ms/step, avg salient rows per layer {avg_n:.1f}, "
+          f"gate_up {avg_gate_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        del wl
+        torch.cuda.empty_cache()
+        threads = min(16, os.cpu_count() or 1)
+        print(f"[bench] CPU baseline on {threads} threads", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(cfg, int(round(avg_n)), threads)
+
+    line = {
+        "metric": "salient-path tokens/s per denoise step, LLaDA-8B shape bf16; % HBM/MFMA roofline",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights, N(0,1) K/V/Q, 15% perturbed response rows)",
+        "config": {"workload": "config1: LLaDA-8B shape, Q-pruned sparse step over 32 layers",
+                   "layers": layers, "batch": cfg["batch"], "seq_len": cfg["prompt"] + cfg["response"],
+                   "response_len": cfg["response"], "hidden": hid, "heads": cfg["heads"], "ffn": inter,
+                   "tau": cfg["tau"], "avg_salient_rows_per_layer": round(avg_n, 1)},
+        "roofline": {"kernel": "gemm_kernel<256,256,SwiGLU> (gathered gate_up + SiLU*up)", "bound": "mfma",
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "avg_launch_us": round(avg_gate_ms * 1e3, 2),
+                     "flop_per_launch": flops},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -22,7 +22,12 @@ SIGNATURES = {
     "dyllm_attention_sparse_workspace_bytes": [_I, _I, _L, _I],
     "dyllm_attention_sparse_varlen": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _L, _I, _P, _P, _P,
                                       _P, _P, c_float, _P, c_size_t, _P],
-    "dyllm_flash_attn_varlen": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, c_float, _P, _P],
+    "dyllm_flash_attn_varlen": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I, c_float, _P, _P],
+    "dyllm_attention_colsparse_workspace_bytes": [_I, _I, _L, _L, _I],
+    "dyllm_attention_colsparse_cached": [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _L,
+                                         _L, _I, _P, _P, _P, _P, c_float, _P, c_size_t, _P],
+    "dyllm_v_delta_update": [_P, _P, _P, _L, _L, _P, _P],
+    "dyllm_seq_row_starts": [_P, _P, _P, _P, _I, _P, _P],
     "dyllm_cosine_mask": [_P, _L, c_float, _P, _P],
     "dyllm_saliency_stats": [_P, _P, _L, _L, c_float, _P, _P, _P],
     "dyllm_salient_compact": [_P, _L, _P, _I, _P, _P, _P, _P, _P, _P, _P],
@@ -36,6 +41,8 @@ SIGNATURES = {
     "dyllm_gather_rows": [_P, _P, _L, _P, _L, _P],
     "dyllm_swiglu_ffn_workspace_bytes": [_L, _I],
     "dyllm_swiglu_ffn": [_P, _L, _P, _L, _P, _P, _I, _I, _P, c_size_t, _P, _P, _P],
+    "dyllm_ffn_gate_up": [_P, _L, _P, _L, _P, _I, _I, _P, _P],
+    "dyllm_ffn_down": [_P, _L, _P, _I, _I, _P, _P, _P],
     "dyllm_moe_gate": [_P, _P, _L, _I, _P, _I, _I, _I, _P, _P, _P],
     "dyllm_moe_align_block_size": [_P, _L, _I, _I, _P, _L, _P, _P, _P],
     "dyllm_fused_experts_workspace_bytes": [_L, _I, _I, _I, _I],
@@ -45,6 +52,7 @@ _RET = {
     "dyllm_last_error": ctypes.c_char_p,
     "dyllm_abi_version": c_int,
     "dyllm_attention_sparse_workspace_bytes": c_size_t,
+    "dyllm_attention_colsparse_workspace_bytes": c_size_t,
     "dyllm_swiglu_ffn_workspace_bytes": c_size_t,
     "dyllm_fused_experts_workspace_bytes": c_size_t,
 }

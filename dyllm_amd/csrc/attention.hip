@@ -60,6 +60,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   const int row_beg = a.cu_rows[b], row_end = a.cu_rows[b + 1];
   if (row_beg + tile * kBQ >= row_end) return;
   const int k_beg = a.cu_k[b], Lk = a.cu_k[b + 1] - k_beg;
+  const int64_t kv0 = a.kv_start ? a.kv_start[b] : int64_t(k_beg);
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int ql = lane & 31, half = lane >> 5;
@@ -90,8 +91,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   float m_run = -FLT_MAX, l_run = 0.f;
   const float c2 = a.scale_log2;
 
-  const uint16_t* Kb = a.K + int64_t(k_beg) * ldkv + kvh * kD;
-  const uint16_t* Vb = a.V + int64_t(k_beg) * ldkv + kvh * kD;
+  const uint16_t* Kb = a.K + kv0 * ldkv + kvh * kD;
+  const uint16_t* Vb = a.V + (a.kslot ? 0 : kv0) * ldkv + kvh * kD;
+  const int32_t* ks_b = a.kslot ? a.kslot + k_beg : nullptr;
   const int nkb = (Lk + kBK - 1) / kBK;
 
   for (int kb = 0; kb < nkb; ++kb) {
@@ -115,8 +117,16 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         const int kp = c & 31, dc = c >> 5;
         const int k0 = 2 * kp;
         uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-        if (key0 + k0 < Lk) v0 = *reinterpret_cast<const uint4*>(Vb + int64_t(key0 + k0) * ldkv + dc * 8);
-        if (key0 + k0 + 1 < Lk) v1 = *reinterpret_cast<const uint4*>(Vb + int64_t(key0 + k0 + 1) * ldkv + dc * 8);
+        int64_t r0 = key0 + k0, r1 = key0 + k0 + 1;
+        if (ks_b) {  // compact dV: key -> slot (or no salient row: zero)
+          r0 = (r0 < Lk) ? ks_b[r0] : -1;
+          r1 = (r1 < Lk) ? ks_b[r1] : -1;
+        } else {
+          r0 = (r0 < Lk) ? r0 : -1;
+          r1 = (r1 < Lk) ? r1 : -1;
+        }
+        if (r0 >= 0) v0 = *reinterpret_cast<const uint4*>(Vb + r0 * ldkv + dc * 8);
+        if (r1 >= 0) v1 = *reinterpret_cast<const uint4*>(Vb + r1 * ldkv + dc * 8);
         const uint32_t x0[4] = {v0.x, v0.y, v0.z, v0.w}, x1[4] = {v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -224,7 +234,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     float dot = 0.f, nn = 0.f, oo = 0.f;
     if (row_ok) {
       const int slot = a.sal_slot[row];
-      const uint16_t* cp = a.C + int64_t(row) * ldq + head * kD + half * 4;
+      const int64_t crow = a.c_start ? a.c_start[b] + (row - row_beg) : int64_t(row);
+      uint16_t* cp = const_cast<uint16_t*>(a.C) + crow * ldq + head * kD + half * 4;
       uint16_t* op = a.O + int64_t(row) * ldq + head * kD + half * 4;
       const uint16_t* sp = slot >= 0 ? a.o_sal + int64_t(slot) * ldq + head * kD + half * 4 : nullptr;
 #pragma unroll
@@ -250,6 +261,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             st.y = pack_bf16x2(nw[2], nw[3]);
           }
           *reinterpret_cast<uint2*>(op + off) = st;
+          if (a.c_inplace) *reinterpret_cast<uint2*>(cp + off) = st;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             dot += nw[j] * old[j];
@@ -269,27 +281,85 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   }
 }
 
-// ---- column-sparse preparation: slot map + per-block salient key bits ------------------
+// ---- column-sparse preparation: slot maps + per-block salient key bits -----------------
 __global__ __launch_bounds__(256) void colsparse_fill_kernel(int32_t* __restrict__ slot, int64_t Tq,
-                                                             uint64_t* __restrict__ kmask, int64_t nmask) {
+                                                             uint64_t* __restrict__ kmask, int64_t nmask,
+                                                             int32_t* __restrict__ kslot, int64_t Tk) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i < Tq) slot[i] = -1;
   if (i < nmask) kmask[i] = 0;
+  if (kslot && i < Tk) kslot[i] = -1;
 }
 
 __global__ __launch_bounds__(256) void colsparse_scatter_kernel(const int32_t* __restrict__ idx_q,
                                                                 const int32_t* __restrict__ idx_k, int n_sal,
                                                                 const int32_t* __restrict__ cu_k, int B, int nblk,
                                                                 int32_t* __restrict__ slot,
-                                                                unsigned long long* __restrict__ kmask) {
+                                                                unsigned long long* __restrict__ kmask,
+                                                                int32_t* __restrict__ kslot) {
   const int j = blockIdx.x * 256 + threadIdx.x;
   if (j >= n_sal) return;
   slot[idx_q[j]] = j;
   const int64_t k = idx_k[j];
+  if (kslot) kslot[k] = j;
   const int b = find_segment(cu_k, B + 1, k);
   if (b >= B || k >= cu_k[b + 1]) return;
   const int off = int(k - cu_k[b]);
   atomicOr(&kmask[int64_t(b) * nblk + off / kBK], 1ull << (off % kBK));
+}
+
+// dV = bf16(v_new - v_cache[row]) then v_cache[row] = v_new (attention.py:67-74, 89-96),
+// one wavefront per salient row, 16-byte lanes.
+__global__ __launch_bounds__(256) void v_delta_update_kernel(uint16_t* __restrict__ v_cache,
+                                                             const uint16_t* __restrict__ v_new,
+                                                             const int64_t* __restrict__ dest_rows, int64_t n,
+                                                             int64_t row_elems, uint16_t* __restrict__ dv) {
+  const int64_t j = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (j >= n) return;
+  uint4* cr = reinterpret_cast<uint4*>(v_cache + dest_rows[j] * row_elems);
+  const uint4* nr = reinterpret_cast<const uint4*>(v_new + j * row_elems);
+  uint4* dr = reinterpret_cast<uint4*>(dv + j * row_elems);
+  for (int64_t i = lane; i < row_elems / 8; i += 64) {
+    const uint4 o = cr[i], nw = nr[i];
+    const uint32_t ov[4] = {o.x, o.y, o.z, o.w}, nv[4] = {nw.x, nw.y, nw.z, nw.w};
+    uint32_t d[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = __fsub_rn(__uint_as_float(nv[e] << 16), __uint_as_float(ov[e] << 16));
+      const float hi = __fsub_rn(__uint_as_float(nv[e] & 0xffff0000u), __uint_as_float(ov[e] & 0xffff0000u));
+      d[e] = pack_bf16x2(lo, hi);
+    }
+    dr[i] = make_uint4(d[0], d[1], d[2], d[3]);
+    cr[i] = nw;
+  }
+}
+
+int launch_v_delta_update(uint16_t* v_cache, const uint16_t* v_new, const int64_t* dest_rows, int64_t n,
+                          int64_t row_elems, uint16_t* dv, hipStream_t s) {
+  DYLLM_REQUIRE(row_elems % 8 == 0, "V row width must be a multiple of 8");
+  if (n <= 0) return 0;
+  v_delta_update_kernel<<<unsigned(cdiv(n, 4)), 256, 0, s>>>(v_cache, v_new, dest_rows, n, row_elems, dv);
+  return check_launch("v_delta_update_kernel");
+}
+
+// out[b] = seq_starts[seq_ids[b]] (+ Lk_b - Lq_b when cu_q is given: the first cached row of
+// the queried tail block, cache_kernels.cu:224).
+__global__ void seq_row_starts_kernel(const int64_t* __restrict__ seq_starts, const int64_t* __restrict__ seq_ids,
+                                      const int32_t* __restrict__ cu_k, const int32_t* __restrict__ cu_q, int B,
+                                      int64_t* __restrict__ out) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  int64_t v = seq_starts[seq_ids[b]];
+  if (cu_q) v += int64_t(cu_k[b + 1] - cu_k[b]) - int64_t(cu_q[b + 1] - cu_q[b]);
+  out[b] = v;
+}
+
+int launch_seq_row_starts(const int64_t* seq_starts, const int64_t* seq_ids, const int32_t* cu_k,
+                          const int32_t* cu_q, int B, int64_t* out, hipStream_t s) {
+  if (B <= 0) return 0;
+  seq_row_starts_kernel<<<unsigned(cdiv(B, 256)), 256, 0, s>>>(seq_starts, seq_ids, cu_k, cu_q, B, out);
+  return check_launch("seq_row_starts_kernel");
 }
 
 int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s) {
@@ -309,16 +379,18 @@ int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hip
 }
 
 int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal, const int32_t* cu_k, int B,
-                          int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, hipStream_t s) {
+                          int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, int32_t* kslot, int64_t Tk,
+                          hipStream_t s) {
   const int64_t nmask = int64_t(B) * nblk;
-  const int64_t n = Tq > nmask ? Tq : nmask;
+  int64_t n = Tq > nmask ? Tq : nmask;
+  if (kslot && Tk > n) n = Tk;
   if (n > 0) {
-    colsparse_fill_kernel<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(slot, Tq, kmask, nmask);
+    colsparse_fill_kernel<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(slot, Tq, kmask, nmask, kslot, Tk);
     if (int rc = check_launch("colsparse_fill_kernel")) return rc;
   }
   if (n_sal > 0) {
     colsparse_scatter_kernel<<<unsigned(cdiv(n_sal, 256)), 256, 0, s>>>(
-        idx_q, idx_k, n_sal, cu_k, B, nblk, slot, reinterpret_cast<unsigned long long*>(kmask));
+        idx_q, idx_k, n_sal, cu_k, B, nblk, slot, reinterpret_cast<unsigned long long*>(kmask), kslot);
     return check_launch("colsparse_scatter_kernel");
   }
   return 0;

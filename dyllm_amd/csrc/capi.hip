@@ -43,16 +43,21 @@ size_t dyllm_attention_sparse_workspace_bytes(int batch, int num_heads, int64_t 
          align256(size_t(num_heads) * 3 * size_t(total_q) * 4);
 }
 
-int dyllm_attention_sparse_varlen(const void* q, const void* k, const void* v_delta, const void* c,
-                                  const void* o_sal, void* o, int batch, int num_heads, int num_kv_heads,
-                                  int head_dim, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                                  int max_seqlen_q, int max_seqlen_k, int64_t total_q, int num_salient,
-                                  const int32_t* cu_salientlens, const int32_t* idx_salient_q,
-                                  const int32_t* idx_salient_k, float* cosine_stats, uint8_t* cosine_out,
-                                  float threshold, void* workspace, size_t workspace_bytes, void* stream) {
+size_t dyllm_attention_colsparse_workspace_bytes(int batch, int num_heads, int64_t total_q, int64_t total_k,
+                                                 int max_seqlen_k) {
+  return dyllm_attention_sparse_workspace_bytes(batch, num_heads, total_q, max_seqlen_k) + align256(size_t(total_k) * 4);
+}
+
+// Shared body of the two column-sparse entry points. kslot_bytes > 0 selects a compact dV.
+static int colsparse_impl(const void* q, const void* k, const int64_t* kv_start, const void* v_delta,
+                          const void* c, const int64_t* c_start, int c_inplace, const void* o_sal, void* o, int batch,
+                          int num_heads, int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
+                          const int32_t* cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, int64_t total_q,
+                          int64_t total_k, int num_salient, const int32_t* idx_salient_q,
+                          const int32_t* idx_salient_k, float* cosine_stats, uint8_t* cosine_out, float threshold,
+                          void* workspace, size_t workspace_bytes, bool compact_dv, void* stream) {
   DYLLM_NONNULL(q);
   DYLLM_NONNULL(k);
-  DYLLM_NONNULL(v_delta);
   DYLLM_NONNULL(c);
   DYLLM_NONNULL(o);
   DYLLM_NONNULL(cu_seqlens_q);
@@ -69,7 +74,10 @@ int dyllm_attention_sparse_varlen(const void* q, const void* k, const void* v_de
                 "maximum sequence lengths must be positive and fit their packed token dimensions");
   DYLLM_REQUIRE(num_salient >= 0 && num_salient <= total_q, "salient Q index count cannot exceed Q.size(0)");
   DYLLM_REQUIRE(num_salient == 0 || (o_sal && idx_salient_q), "o_sal and idx_salient_q are required");
-  const size_t need = dyllm_attention_sparse_workspace_bytes(batch, num_heads, total_q, max_seqlen_k);
+  DYLLM_REQUIRE(v_delta != nullptr || (compact_dv && num_salient == 0), "v_delta must not be NULL");
+  const size_t need = compact_dv
+                          ? dyllm_attention_colsparse_workspace_bytes(batch, num_heads, total_q, total_k, max_seqlen_k)
+                          : dyllm_attention_sparse_workspace_bytes(batch, num_heads, total_q, max_seqlen_k);
   DYLLM_REQUIRE(workspace && workspace_bytes >= need,
                 "workspace too small: need " + std::to_string(need) + " bytes");
   const hipStream_t s = DYLLM_STREAM(stream);
@@ -80,8 +88,10 @@ int dyllm_attention_sparse_varlen(const void* q, const void* k, const void* v_de
   uint64_t* kmask = reinterpret_cast<uint64_t*>(ws);
   ws += align256(size_t(batch) * nblk * 8);
   float* part = reinterpret_cast<float*>(ws);
+  ws += align256(size_t(num_heads) * 3 * size_t(total_q) * 4);
+  int32_t* kslot = compact_dv ? reinterpret_cast<int32_t*>(ws) : nullptr;
   if (int rc = launch_colsparse_prep(idx_salient_q, idx_salient_k ? idx_salient_k : idx_salient_q, num_salient,
-                                     cu_seqlens_k, batch, nblk, slot, total_q, kmask, s))
+                                     cu_seqlens_k, batch, nblk, slot, total_q, kmask, kslot, total_k, s))
     return rc;
   AttnArgs a{};
   a.Q = static_cast<const uint16_t*>(q);
@@ -92,7 +102,11 @@ int dyllm_attention_sparse_varlen(const void* q, const void* k, const void* v_de
   a.O = static_cast<uint16_t*>(o);
   a.cu_rows = cu_seqlens_q;
   a.cu_k = cu_seqlens_k;
+  a.kv_start = kv_start;
+  a.c_start = c_start;
+  a.c_inplace = c_inplace;
   a.sal_slot = slot;
+  a.kslot = kslot;
   a.kmask = kmask;
   a.part = part;
   a.B = batch;
@@ -106,10 +120,56 @@ int dyllm_attention_sparse_varlen(const void* q, const void* k, const void* v_de
   return launch_saliency_reduce(part, cosine_stats, cosine_out, total_q, num_heads, threshold, s);
 }
 
+int dyllm_attention_sparse_varlen(const void* q, const void* k, const void* v_delta, const void* c,
+                                  const void* o_sal, void* o, int batch, int num_heads, int num_kv_heads,
+                                  int head_dim, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                  int max_seqlen_q, int max_seqlen_k, int64_t total_q, int num_salient,
+                                  const int32_t* cu_salientlens, const int32_t* idx_salient_q,
+                                  const int32_t* idx_salient_k, float* cosine_stats, uint8_t* cosine_out,
+                                  float threshold, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)cu_salientlens;  // per-sequence salient ranges are implied by the sorted index lists
+  return colsparse_impl(q, k, nullptr, v_delta, c, nullptr, 0, o_sal, o, batch, num_heads, num_kv_heads, head_dim,
+                        cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, total_q, 0, num_salient,
+                        idx_salient_q, idx_salient_k, cosine_stats, cosine_out, threshold, workspace,
+                        workspace_bytes, false, stream);
+}
+
+int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const int64_t* kv_start,
+                                     const void* dv_compact, void* c_cache, const int64_t* c_start,
+                                     int c_inplace, const void* o_sal, void* o, int batch, int num_heads,
+                                     int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
+                                     const int32_t* cu_seqlens_k, int max_seqlen_q, int max_seqlen_k,
+                                     int64_t total_q, int64_t total_k, int num_salient,
+                                     const int32_t* idx_salient_q, const int32_t* idx_salient_k,
+                                     float* cosine_stats, uint8_t* cosine_out, float threshold, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  DYLLM_REQUIRE(total_k > 0, "total_k must be positive");
+  return colsparse_impl(q, k_cache, kv_start, dv_compact, c_cache, c_start, c_inplace, o_sal, o, batch, num_heads,
+                        num_kv_heads, head_dim, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, total_q,
+                        total_k, num_salient, idx_salient_q, idx_salient_k, cosine_stats, cosine_out, threshold,
+                        workspace, workspace_bytes, true, stream);
+}
+
+int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,
+                         int64_t row_elems, void* dv_out, void* stream) {
+  DYLLM_REQUIRE(rows == 0 || (v_cache && v_new && dest_rows && dv_out), "null pointer argument");
+  return launch_v_delta_update(static_cast<uint16_t*>(v_cache), static_cast<const uint16_t*>(v_new), dest_rows, rows,
+                               row_elems, static_cast<uint16_t*>(dv_out), DYLLM_STREAM(stream));
+}
+
+int dyllm_seq_row_starts(const int64_t* seq_starts, const int64_t* seq_ids, const int32_t* cu_seqlens_k,
+                         const int32_t* cu_seqlens_q, int batch, int64_t* out, void* stream) {
+  DYLLM_NONNULL(seq_starts);
+  DYLLM_NONNULL(seq_ids);
+  DYLLM_NONNULL(out);
+  DYLLM_REQUIRE(cu_seqlens_q == nullptr || cu_seqlens_k != nullptr, "cu_seqlens_k is required with cu_seqlens_q");
+  return launch_seq_row_starts(seq_starts, seq_ids, cu_seqlens_k, cu_seqlens_q, batch, out, DYLLM_STREAM(stream));
+}
+
 int dyllm_flash_attn_varlen(const void* q, const void* k, const void* v, void* o, int batch, int num_heads,
                             int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
-                            const int32_t* cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, float softmax_scale,
-                            const int32_t* q_rows, void* stream) {
+                            const int32_t* cu_seqlens_k, const int64_t* kv_start, int max_seqlen_q, int max_seqlen_k,
+                            float softmax_scale, const int32_t* q_rows, void* stream) {
   DYLLM_NONNULL(q);
   DYLLM_NONNULL(k);
   DYLLM_NONNULL(v);
@@ -127,6 +187,7 @@ int dyllm_flash_attn_varlen(const void* q, const void* k, const void* v, void* o
   a.O = static_cast<uint16_t*>(o);
   a.cu_rows = cu_seqlens_q;
   a.cu_k = cu_seqlens_k;
+  a.kv_start = kv_start;
   a.q_rows = q_rows;
   a.B = batch;
   a.H = num_heads;
@@ -269,20 +330,14 @@ size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate) {
 // 256x256 tiles when they still give >= one workgroup per CU, else 128x128.
 static int pick_tile(int64_t M, int64_t N) { return (cdiv(M, 256) * cdiv(N, 256) >= 256) ? 256 : 128; }
 
-int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
-                     const void* w_down, int hidden, int intermediate, void* workspace, size_t workspace_bytes,
-                     void* out, const int64_t* out_rows, void* stream) {
+int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
+                      int hidden, int intermediate, void* h_out, void* stream) {
   DYLLM_NONNULL(x);
   DYLLM_NONNULL(w_gate_up);
-  DYLLM_NONNULL(w_down);
-  DYLLM_NONNULL(out);
+  DYLLM_NONNULL(h_out);
   DYLLM_REQUIRE(hidden > 0 && hidden % 64 == 0, "hidden size must be a positive multiple of 64");
   DYLLM_REQUIRE(intermediate > 0 && intermediate % 64 == 0, "intermediate size must be a positive multiple of 64");
   if (rows <= 0) return 0;
-  const size_t need = dyllm_swiglu_ffn_workspace_bytes(rows, intermediate);
-  DYLLM_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need " + std::to_string(need) + " bytes");
-  const hipStream_t s = DYLLM_STREAM(stream);
-  uint16_t* h = static_cast<uint16_t*>(workspace);
   GemmArgs g{};
   g.A = static_cast<const uint16_t*>(x);
   g.lda = ld_x;
@@ -291,16 +346,26 @@ int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64
   g.id_limit = INT64_MAX;
   g.W = static_cast<const uint16_t*>(w_gate_up);
   g.ldw = hidden;
-  g.Cout = h;
+  g.Cout = static_cast<uint16_t*>(h_out);
   g.ldc = intermediate;
   g.M = rows;
   g.N = 2 * intermediate;
   g.K = hidden;
   g.half_n = intermediate;
   const int t1 = (pick_tile(rows, g.N) == 256 && intermediate % 128 == 0) ? 256 : 128;
-  if (int rc = launch_gemm(GemmEpi::SwiGLU, g, rows, t1, s)) return rc;
+  return launch_gemm(GemmEpi::SwiGLU, g, rows, t1, DYLLM_STREAM(stream));
+}
+
+int dyllm_ffn_down(const void* h, int64_t rows, const void* w_down, int hidden, int intermediate, void* out,
+                   const int64_t* out_rows, void* stream) {
+  DYLLM_NONNULL(h);
+  DYLLM_NONNULL(w_down);
+  DYLLM_NONNULL(out);
+  DYLLM_REQUIRE(hidden > 0 && hidden % 64 == 0, "hidden size must be a positive multiple of 64");
+  DYLLM_REQUIRE(intermediate > 0 && intermediate % 64 == 0, "intermediate size must be a positive multiple of 64");
+  if (rows <= 0) return 0;
   GemmArgs d{};
-  d.A = h;
+  d.A = static_cast<const uint16_t*>(h);
   d.lda = intermediate;
   d.a_div = 1;
   d.id_limit = INT64_MAX;
@@ -312,7 +377,18 @@ int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64
   d.M = rows;
   d.N = hidden;
   d.K = intermediate;
-  return launch_gemm(GemmEpi::Store, d, rows, pick_tile(rows, hidden), s);
+  return launch_gemm(GemmEpi::Store, d, rows, pick_tile(rows, hidden), DYLLM_STREAM(stream));
+}
+
+int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
+                     const void* w_down, int hidden, int intermediate, void* workspace, size_t workspace_bytes,
+                     void* out, const int64_t* out_rows, void* stream) {
+  if (rows <= 0) return 0;
+  const size_t need = dyllm_swiglu_ffn_workspace_bytes(rows, intermediate);
+  DYLLM_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need " + std::to_string(need) + " bytes");
+  if (int rc = dyllm_ffn_gate_up(x, ld_x, rows_idx, rows, w_gate_up, hidden, intermediate, workspace, stream))
+    return rc;
+  return dyllm_ffn_down(workspace, rows, w_down, hidden, intermediate, out, out_rows, stream);
 }
 
 // ---------------------------------------------------------------------------------------

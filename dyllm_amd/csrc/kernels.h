@@ -33,27 +33,36 @@ int launch_fused_offset(const int32_t* idxs, const int32_t* num_idxs, const int3
 
 enum class AttnMode : int { Dense = 0, RowSparse = 1, ColSparse = 2 };
 struct AttnArgs {
-  const uint16_t* Q;
-  const uint16_t* K;
-  const uint16_t* V;
-  const uint16_t* C;
-  const uint16_t* o_sal;
-  uint16_t* O;
-  const int32_t* cu_rows;
-  const int32_t* cu_k;
-  const int32_t* q_rows;
-  const int32_t* sal_slot;
-  const uint64_t* kmask;
-  float* part;
+  const uint16_t* Q;        // [Tq_all, H, 128]
+  const uint16_t* K;        // [*, Hkv, 128]
+  const uint16_t* V;        // [*, Hkv, 128]; ColSparse: dV (full, or compact when kslot != NULL)
+  const uint16_t* C;        // ColSparse: cached context rows
+  const uint16_t* o_sal;    // ColSparse: [n_sal, H, 128]
+  uint16_t* O;              // [rows, H, 128]
+  const int32_t* cu_rows;   // [B+1] prefix of the rows this launch produces
+  const int32_t* cu_k;      // [B+1]
+  const int64_t* kv_start;  // optional [B]: first K/V row of sequence b (else cu_k[b])
+  const int64_t* c_start;   // optional [B]: first C row of sequence b (else cu_rows[b])
+  int c_inplace;            // ColSparse: also write the new rows back to C
+  const int32_t* q_rows;    // RowSparse: Q row of compact row j
+  const int32_t* sal_slot;  // ColSparse: [Tq] index into o_sal or -1
+  const int32_t* kslot;     // ColSparse, optional: [Tk] row of compact dV or -1
+  const uint64_t* kmask;    // ColSparse: [B][nblk] salient-key bits per 64-key block
+  float* part;              // ColSparse: [H][3][Tq] per-head partial statistics
   int B, H, Hkv;
-  int tiles_per_seq;
-  int nblk;
-  int64_t Tq;
+  int tiles_per_seq;        // cdiv(max rows per sequence, 128)
+  int nblk;                 // kmask row stride
+  int64_t Tq;               // ColSparse: rows of part
   float scale_log2;
 };
 int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s);
 int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal, const int32_t* cu_k, int B,
-                          int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, hipStream_t s);
+                          int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, int32_t* kslot, int64_t Tk,
+                          hipStream_t s);
+int launch_v_delta_update(uint16_t* v_cache, const uint16_t* v_new, const int64_t* dest_rows, int64_t n,
+                          int64_t row_elems, uint16_t* dv, hipStream_t s);
+int launch_seq_row_starts(const int64_t* seq_starts, const int64_t* seq_ids, const int32_t* cu_k,
+                          const int32_t* cu_q, int B, int64_t* out, hipStream_t s);
 
 enum class GemmEpi : int { Store = 0, SwiGLU = 1 };
 struct GemmArgs {

@@ -1,0 +1,200 @@
+"""LLaDA bidirectional decoder wired to the sparse hot path
+(dyllm/model_executor/models/llada.py:26-260), random-initialised from shape fields only.
+
+The hot path (attention saliency / compaction / gathered SwiGLU + scatter) runs on the HIP
+kernels; the dense ops on either side of it (embeddings, RMSNorm, RoPE, the Q/K/V/O
+projections, the LM head) use PyTorch-ROCm, as SURVEY's scope table places them outside the
+path. MLP and Dream/MoE variants share this structure.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ... import ops
+from ...engine.cache_manager import CacheManager
+from ...utils.context import get_context
+from ...utils.metadata import get_metadata
+from ..layers.attention import Attention
+from ..layers.mlp_cache_manage import MLPcache
+
+
+def _param(*shape, std=0.02, device="cuda", dtype=torch.bfloat16, gen=None):
+    w = torch.empty(*shape, dtype=torch.float32, device=device)
+    w.normal_(0.0, std, generator=gen)
+    return nn.Parameter(w.to(dtype), requires_grad=False)
+
+
+class RMSNorm(nn.Module):
+    """RMSNorm / fused residual-add RMSNorm (layernorm.py:5-51)."""
+
+    def __init__(self, hidden, eps=1e-6, device="cuda"):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(hidden, dtype=torch.bfloat16, device=device), requires_grad=False)
+
+    def forward(self, x, residual=None):
+        if residual is not None:
+            xf = x.float() + residual.float()
+            residual = xf.to(x.dtype)
+        else:
+            xf = x.float()
+        y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.weight
+        return y if residual is None else (y, residual)
+
+
+class RotaryEmbedding(nn.Module):
+    """Neox-style rotary embedding (rotary_embedding.py:8-54)."""
+
+    def __init__(self, head_dim, max_position, base, device="cuda"):
+        super().__init__()
+        inv = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim))
+        t = torch.arange(max_position, dtype=torch.float32, device=device)
+        f = torch.outer(t, inv)
+        self.register_buffer("cos", f.cos(), persistent=False)
+        self.register_buffer("sin", f.sin(), persistent=False)
+
+    def rotate(self, positions, x):
+        pos = positions.clamp(0, self.cos.shape[0] - 1)
+        c, s = self.cos[pos].unsqueeze(1), self.sin[pos].unsqueeze(1)
+        x1, x2 = x.float().chunk(2, dim=-1)
+        return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
+
+
+class LLaDAMLP(nn.Module):
+    """SwiGLU FFN + FFN-output cache (llada.py:26-43). On sparse steps the salient rows are
+    gathered inside the gate_up GEMM and the down GEMM scatters straight into the cache."""
+
+    def __init__(self, hidden, inter, device="cuda", gen=None):
+        super().__init__()
+        self.gate_up_proj = _param(2 * inter, hidden, device=device, gen=gen)  # gate rows, then up rows
+        self.down_proj = _param(hidden, inter, device=device, gen=gen)
+        self.cache_update = MLPcache(hidden, device=device)
+
+    def forward(self, x):
+        """Reference interface: x = gathered salient rows (sparse) or all rows (full)."""
+        y = ops.swiglu_ffn(x.contiguous(), self.gate_up_proj, self.down_proj)
+        return self.cache_update(y)
+
+    def forward_salient(self, h_all, gate_up_events=None):
+        """Sparse step, fused: h_all = all queried rows after post_attention_layernorm.
+        ``gate_up_events`` (start, end) brackets the gathered gate_up GEMM for timing."""
+        ctx = get_context()
+        cm = self.cache_update.cache_manager
+        rows = ctx.idx_salient_row_i32 if ctx.idx_salient_row_i32 is not None else ctx.idx_salient_row.to(torch.int32)
+        h_all = h_all.contiguous()
+        if gate_up_events is not None:
+            gate_up_events[0].record()
+        h = ops.ffn_gate_up(h_all, self.gate_up_proj, rows_idx=rows)
+        if gate_up_events is not None:
+            gate_up_events[1].record()
+        ops.ffn_down(h, self.down_proj, out=cm._slab, out_rows=self.cache_update.dest_rows())
+        return self.cache_update.gather_all()
+
+
+class LLaDAAttention(nn.Module):
+    """Projections + RoPE + K cache around ``Attention`` (llada.py:46-149)."""
+
+    def __init__(self, hidden, num_heads, num_kv_heads, head_dim, max_position, rope_theta, threshold,
+                 qkv_bias=False, device="cuda", gen=None):
+        super().__init__()
+        self.num_heads, self.num_kv_heads, self.head_dim = num_heads, num_kv_heads, head_dim
+        self.q_size, self.kv_size = num_heads * head_dim, num_kv_heads * head_dim
+        self.q_proj = _param(self.q_size, hidden, device=device, gen=gen)
+        self.kv_proj = _param(2 * self.kv_size, hidden, device=device, gen=gen)
+        self.q_bias = nn.Parameter(torch.zeros(self.q_size, dtype=torch.bfloat16, device=device),
+                                   requires_grad=False) if qkv_bias else None
+        self.kv_bias = nn.Parameter(torch.zeros(2 * self.kv_size, dtype=torch.bfloat16, device=device),
+                                    requires_grad=False) if qkv_bias else None
+        self.o_proj = _param(hidden, self.q_size, device=device, gen=gen)
+        self.k_cache = CacheManager(self.kv_size, device=torch.device(device))
+        self.rotary = RotaryEmbedding(head_dim, max_position, rope_theta, device=device)
+        self.attn = Attention(num_heads, head_dim, head_dim ** -0.5, num_kv_heads, threshold, device=device)
+
+    def forward(self, positions, hidden):
+        ctx = get_context()
+        md = get_metadata()
+        q = F.linear(hidden, self.q_proj, self.q_bias).view(-1, self.num_heads, self.head_dim)
+        q = self.rotary.rotate(positions, q)
+        if ctx.is_full:
+            kv = F.linear(hidden, self.kv_proj, self.kv_bias)
+            k, v = kv.split([self.kv_size, self.kv_size], dim=-1)
+            k = self.rotary.rotate(positions, k.reshape(-1, self.num_kv_heads, self.head_dim))
+            v = v.reshape(-1, self.num_kv_heads, self.head_dim)
+            self.k_cache.reset_full(k.reshape(k.shape[0], -1), md.running_seqs_tensor, seq_ids_list=md.running_seqs)
+            o = self.attn(q, k, v)
+        else:
+            idx = ctx.idx_salient_row
+            kv = F.linear(ops.gather_rows_2D(hidden, idx), self.kv_proj, self.kv_bias)
+            k, v = kv.split([self.kv_size, self.kv_size], dim=-1)
+            k = self.rotary.rotate(positions[idx], k.reshape(-1, self.num_kv_heads, self.head_dim))
+            v = v.reshape(-1, self.num_kv_heads, self.head_dim)
+            kidx = ctx.idx_salient_row_k if ctx.idx_salient_row_k is not None else idx
+            self.k_cache.scatter_update(md.running_seqs_tensor, kidx, k.reshape(k.shape[0], -1))
+            k_full = self.k_cache.get_seqs(md.running_seqs_tensor, md.running_seqs)
+            o = self.attn(q, k_full.view(-1, self.num_kv_heads, self.head_dim), v)
+        out = F.linear(o.reshape(o.shape[0], -1), self.o_proj)
+        self.k_cache.finish(md.finished_seqs)
+        return out
+
+
+class LLaDADecoderLayer(nn.Module):
+    """llada.py:152-187."""
+
+    def __init__(self, cfg, threshold, device="cuda", gen=None):
+        super().__init__()
+        self.self_attn = LLaDAAttention(cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads,
+                                        cfg.head_dim, cfg.max_position_embeddings, cfg.rope_theta, threshold,
+                                        qkv_bias=cfg.qkv_bias, device=device, gen=gen)
+        self.mlp = self._make_mlp(cfg, device, gen)
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device=device)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device=device)
+
+    def _make_mlp(self, cfg, device, gen):
+        return LLaDAMLP(cfg.hidden_size, cfg.intermediate_size, device=device, gen=gen)
+
+    def forward(self, positions, hidden, residual=None):
+        if residual is None:
+            hidden, residual = self.input_layernorm(hidden), hidden
+        else:
+            hidden, residual = self.input_layernorm(hidden, residual)
+        hidden = self.self_attn(positions, hidden)
+        hidden, residual = self.post_attention_layernorm(hidden, residual)
+        if get_context().is_full:
+            hidden = self.mlp(hidden)
+        else:
+            hidden = self.mlp.forward_salient(hidden)
+        return hidden, residual
+
+
+class LLaDAModel(nn.Module):
+    def __init__(self, cfg, threshold, device="cuda", gen=None, layer_cls=LLaDADecoderLayer):
+        super().__init__()
+        self.embed_tokens = _param(cfg.vocab_size, cfg.hidden_size, device=device, gen=gen)
+        self.layers = nn.ModuleList([layer_cls(cfg, threshold, device=device, gen=gen)
+                                     for _ in range(cfg.num_hidden_layers)])
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device=device)
+
+    def forward(self, input_ids, positions):
+        hidden = F.embedding(input_ids, self.embed_tokens)
+        residual = None
+        for layer in self.layers:
+            hidden, residual = layer(positions, hidden, residual)
+        hidden, _ = self.norm(hidden, residual)
+        return hidden
+
+
+class LLaDAForDLM(nn.Module):
+    def __init__(self, cfg, threshold, device="cuda", seed=0):
+        super().__init__()
+        gen = torch.Generator(device=device).manual_seed(seed)
+        self.config = cfg
+        self.model = LLaDAModel(cfg, threshold, device=device, gen=gen)
+        self.lm_head = _param(cfg.vocab_size, cfg.hidden_size, device=device, gen=gen)
+
+    def forward(self, input_ids, positions):
+        return self.model(input_ids, positions)
+
+    def compute_logits(self, hidden):
+        return F.linear(hidden, self.lm_head)

@@ -102,11 +102,13 @@ def attention_sparse_varlen(Q, K, V, C, o_sal, cu_seqlens_q, cu_seqlens_k, max_s
 
 
 def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
-                           softmax_scale=None, causal=False, q_rows=None):
+                           softmax_scale=None, causal=False, q_rows=None, kv_start=None):
     """Non-causal varlen attention (the two flash_attn_varlen_func call sites). With
     ``q_rows`` (int32), compact row j of the output attends with q[q_rows[j]] and
     cu_seqlens_q is the prefix of the compact rows -- the row-sparse call
-    ``flash_attn_varlen_func(q[idx], ...)`` without materialising q[idx]."""
+    ``flash_attn_varlen_func(q[idx], ...)`` without materialising q[idx]. With ``kv_start``
+    (int64 [B]) sequence b's keys start at row kv_start[b] of k/v (a per-layer cache) instead
+    of cu_seqlens_k[b]."""
     if causal or dropout_p != 0.0:
         raise RuntimeError("only non-causal attention without dropout is implemented")
     dev = q.device
@@ -125,9 +127,51 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
     if n_out == 0:
         return o
     _lib.call("dyllm_flash_attn_varlen", _ptr(q), _ptr(k), _ptr(v), _ptr(o), cu_q.numel() - 1, q.shape[1],
-              k.shape[1], D, _ptr(cu_q), _ptr(cu_k), int(max_seqlen_q), int(max_seqlen_k), float(scale),
-              _ptr(q_rows), _stream())
+              k.shape[1], D, _ptr(cu_q), _ptr(cu_k), _ptr(kv_start), int(max_seqlen_q), int(max_seqlen_k),
+              float(scale), _ptr(q_rows), _stream())
     return o
+
+
+def attention_colsparse_cached(q, k_cache, kv_start, dv_compact, c_cache, c_start, o_sal, cu_seqlens_q,
+                               cu_seqlens_k, max_seqlen_q, max_seqlen_k, total_k, idx_salient_q, idx_salient_k,
+                               threshold, c_inplace=True, out=None, cosine_stats=None, cosine_out=None):
+    """Column-sparse attention reading K and the context straight from the per-layer caches
+    and a compact dV (rows follow idx_salient_k). Returns (O, stats [T,3], mask [T] bool);
+    with ``c_inplace`` the new context rows are also written into ``c_cache``."""
+    dev = q.device
+    Tq, H, D = q.shape
+    Hkv = k_cache.shape[1] if k_cache.dim() == 3 else k_cache.shape[1] // D
+    B = cu_seqlens_q.numel() - 1
+    n = idx_salient_q.numel()
+    O = torch.empty_like(q) if out is None else out
+    stats = torch.empty(Tq, 3, dtype=torch.float32, device=dev) if cosine_stats is None else cosine_stats
+    mask = torch.empty(Tq, dtype=torch.bool, device=dev) if cosine_out is None else cosine_out
+    ws_bytes = _lib.load().dyllm_attention_colsparse_workspace_bytes(B, H, Tq, int(total_k), int(max_seqlen_k))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.call("dyllm_attention_colsparse_cached", _ptr(q), _ptr(k_cache), _ptr(kv_start), _ptr(dv_compact),
+              _ptr(c_cache), _ptr(c_start), int(bool(c_inplace)), _ptr(o_sal), _ptr(O), B, H, Hkv, D,
+              _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), int(max_seqlen_q), int(max_seqlen_k), Tq, int(total_k), n,
+              _ptr(idx_salient_q), _ptr(idx_salient_k), _ptr(stats), _ptr(mask), float(threshold), _ptr(ws),
+              ws_bytes, _stream())
+    return O, stats, mask
+
+
+def v_delta_update(v_cache, v_new, dest_rows):
+    """dv = v_new - v_cache[dest_rows]; v_cache[dest_rows] = v_new (attention.py:67-74)."""
+    v_new = v_new.reshape(v_new.shape[0], -1).contiguous()
+    dv = torch.empty_like(v_new)
+    if v_new.shape[0]:
+        _lib.call("dyllm_v_delta_update", _ptr(v_cache), _ptr(v_new), _ptr(dest_rows), v_new.shape[0],
+                  v_new.shape[1], _ptr(dv), _stream())
+    return dv
+
+
+def seq_row_starts(seq_starts, seq_ids, cu_seqlens_k=None, cu_seqlens_q=None):
+    """First cache row of each running sequence (+ the tail-block offset with cu_seqlens_q)."""
+    out = torch.empty(seq_ids.numel(), dtype=torch.int64, device=seq_ids.device)
+    _lib.call("dyllm_seq_row_starts", _ptr(seq_starts), _ptr(seq_ids), _ptr(cu_seqlens_k), _ptr(cu_seqlens_q),
+              seq_ids.numel(), _ptr(out), _stream())
+    return out
 
 
 # ---------------------------------------------------------------------------------------
@@ -298,32 +342,51 @@ def gather_rows_2D(x, row_idx):
 # ---------------------------------------------------------------------------------------
 # FFN / MoE
 # ---------------------------------------------------------------------------------------
-def swiglu_ffn(x, w_gate_up, w_down, rows_idx=None, out=None, out_rows=None):
-    """down(silu(a Wg^T) * (a Wu^T)) for a = x[rows_idx] (or all rows of x). With
-    ``out``/``out_rows`` the result rows are written to out[out_rows[m]] (in-place scatter
-    into a cache); otherwise a new [M, hidden] tensor is returned."""
+def ffn_gate_up(x, w_gate_up, rows_idx=None):
+    """h = silu(a Wg^T) * (a Wu^T) for a = x[rows_idx] (gathered inside the GEMM)."""
     _check(x, "x", torch.bfloat16, 2)
     _check(w_gate_up, "w_gate_up", torch.bfloat16, 2)
-    _check(w_down, "w_down", torch.bfloat16, 2)
     hidden = x.shape[1]
     inter = w_gate_up.shape[0] // 2
-    if w_gate_up.shape[1] != hidden or tuple(w_down.shape) != (hidden, inter):
-        raise RuntimeError("weights must be w_gate_up [2I, hidden] and w_down [hidden, I]")
+    if w_gate_up.shape[1] != hidden:
+        raise RuntimeError("w_gate_up must be [2I, hidden]")
     ri = _i32(rows_idx) if rows_idx is not None else None
     M = ri.numel() if ri is not None else x.shape[0]
+    h = torch.empty((M, inter), dtype=x.dtype, device=x.device)
+    if M:
+        _lib.call("dyllm_ffn_gate_up", _ptr(x), x.stride(0), _ptr(ri), M, _ptr(w_gate_up), hidden, inter, _ptr(h),
+                  _stream())
+    return h
+
+
+def ffn_down(h, w_down, out=None, out_rows=None):
+    """y = h Wd^T, written to out[out_rows[m]] when given (in-place scatter) else a new tensor."""
+    _check(h, "h", torch.bfloat16, 2)
+    _check(w_down, "w_down", torch.bfloat16, 2)
+    M, inter = h.shape
+    hidden = w_down.shape[0]
+    if w_down.shape[1] != inter:
+        raise RuntimeError("w_down must be [hidden, I]")
     if out is None:
-        out = torch.empty((M, hidden), dtype=x.dtype, device=x.device)
+        out = torch.empty((M, hidden), dtype=h.dtype, device=h.device)
         orow = None
     else:
         _check(out, "out", torch.bfloat16, 2)
         orow = _i64(out_rows) if out_rows is not None else None
-    if M == 0:
-        return out
-    ws_bytes = _lib.load().dyllm_swiglu_ffn_workspace_bytes(M, inter)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
-    _lib.call("dyllm_swiglu_ffn", _ptr(x), x.stride(0), _ptr(ri), M, _ptr(w_gate_up), _ptr(w_down), hidden, inter,
-              _ptr(ws), ws_bytes, _ptr(out), _ptr(orow), _stream())
+    if M:
+        _lib.call("dyllm_ffn_down", _ptr(h), M, _ptr(w_down), hidden, inter, _ptr(out), _ptr(orow), _stream())
     return out
+
+
+def swiglu_ffn(x, w_gate_up, w_down, rows_idx=None, out=None, out_rows=None):
+    """down(silu(a Wg^T) * (a Wu^T)) for a = x[rows_idx] (or all rows of x). With
+    ``out``/``out_rows`` the result rows are written to out[out_rows[m]] (in-place scatter
+    into a cache); otherwise a new [M, hidden] tensor is returned."""
+    _check(w_down, "w_down", torch.bfloat16, 2)
+    if tuple(w_down.shape) != (x.shape[1], w_gate_up.shape[0] // 2):
+        raise RuntimeError("weights must be w_gate_up [2I, hidden] and w_down [hidden, I]")
+    h = ffn_gate_up(x, w_gate_up, rows_idx)
+    return ffn_down(h, w_down, out, out_rows)
 
 
 def moe_gate(hidden_states, router_weight, top_k, renormalize=False):

@@ -28,6 +28,9 @@
  *   dyllm_moe_gate                 <- moe_gate, dyllm/model_executor/layers/fused_moe.py:375-408
  *   dyllm_moe_align_block_size     <- moe_align_block_size, fused_moe.py:37-85
  *   dyllm_fused_experts            <- fused_experts, fused_moe.py:269-335
+ *   dyllm_attention_colsparse_cached, dyllm_v_delta_update, dyllm_seq_row_starts
+ *                                  <- the sparse branch of Attention.forward, attention.py:64-178, with the
+ *                                     K/V/context cache gathers and the full-size dV fused away
  *   dyllm_saliency_stats           <- the statistics epilogue of attention_ops_kernels_sm80.cu:436-481
  *                                     as a standalone pass over two bf16 row sets
  */
@@ -72,8 +75,37 @@ int dyllm_attention_sparse_varlen(const void* q, const void* k, const void* v_de
  * max_seqlen_q bounds the rows of one sequence. */
 int dyllm_flash_attn_varlen(const void* q, const void* k, const void* v, void* o, int batch, int num_heads,
                             int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
-                            const int32_t* cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, float softmax_scale,
-                            const int32_t* q_rows, void* stream);
+                            const int32_t* cu_seqlens_k, const int64_t* kv_start, int max_seqlen_q,
+                            int max_seqlen_k, float softmax_scale, const int32_t* q_rows, void* stream);
+
+/* Column-sparse attention straight out of the per-layer caches (no reference counterpart:
+ * it fuses the cache gathers and the full-size dV of attention.py:67-139 into the kernel):
+ * K rows of sequence b start at k_cache row kv_start[b] (NULL: cu_seqlens_k[b]); dV is compact,
+ * row j belonging to key idx_salient_k[j] (packed K space); C rows of sequence b start at
+ * c_cache row c_start[b] (NULL: cu_seqlens_q[b]) and, with c_inplace, the new rows are also
+ * written back there (the context-cache reset_block). Same outputs as
+ * dyllm_attention_sparse_varlen otherwise. */
+size_t dyllm_attention_colsparse_workspace_bytes(int batch, int num_heads, int64_t total_q, int64_t total_k,
+                                                 int max_seqlen_k);
+int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const int64_t* kv_start,
+                                     const void* dv_compact, void* c_cache, const int64_t* c_start,
+                                     int c_inplace, const void* o_sal, void* o, int batch, int num_heads,
+                                     int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
+                                     const int32_t* cu_seqlens_k, int max_seqlen_q, int max_seqlen_k,
+                                     int64_t total_q, int64_t total_k, int num_salient,
+                                     const int32_t* idx_salient_q, const int32_t* idx_salient_k,
+                                     float* cosine_stats, uint8_t* cosine_out, float threshold, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+
+/* dV and V-cache update of attention.py:67-74 (dv = v_new - v_cache[row]; v_cache[row] = v_new)
+ * for compact rows; dest_rows are cache rows (dyllm_scatter_dest_rows). */
+int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,
+                         int64_t row_elems, void* dv_out, void* stream);
+
+/* out[b] = seq_starts[seq_ids[b]] (+ Lk_b - Lq_b when cu_seqlens_q != NULL: the first cached
+ * row of the queried tail block, cache_kernels.cu:224). */
+int dyllm_seq_row_starts(const int64_t* seq_starts, const int64_t* seq_ids, const int32_t* cu_seqlens_k,
+                         const int32_t* cu_seqlens_q, int batch, int64_t* out, void* stream);
 
 /* ---- saliency and compaction ----------------------------------------------------------- */
 
@@ -133,6 +165,13 @@ size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate);
 int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
                      const void* w_down, int hidden, int intermediate, void* workspace, size_t workspace_bytes,
                      void* out, const int64_t* out_rows, void* stream);
+
+/* The two stages of dyllm_swiglu_ffn: h_out [rows, intermediate] = silu(a W_g^T) * (a W_u^T)
+ * with a = x[rows_idx[m] or m]; then out[out_rows[m] or m] = h[m] W_d^T. */
+int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
+                      int hidden, int intermediate, void* h_out, void* stream);
+int dyllm_ffn_down(const void* h, int64_t rows, const void* w_down, int hidden, int intermediate, void* out,
+                   const int64_t* out_rows, void* stream);
 
 /* ---- MoE ------------------------------------------------------------------------------- */
 
