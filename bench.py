@@ -111,7 +111,7 @@ def build_workload(cfg, layers, device, seed=0):
         return set_context(False, cu_seqlens_q=cu_q, cu_seqlens_q_cpu=cu_q_cpu, cu_seqlens_k=cu_k,
                            cu_seqlens_k_cpu=cu_k_cpu, cu_promptlens=cu_p, max_seqlen_q=R, max_seqlen_k=L,
                            context_lens_cpu=[L] * B, cu_salientlens=cu_s, idx_salient_row=S_q,
-                           idx_salient_row_i32=S_q.to(torch.int32), idx_salient_row_k=S_k, total_seqlen=Tq,
+                           idx_salient_row_i32=S_q.to(torch.int32), idx_salient_row_k=S_k, max_salientlen=n_per, total_seqlen=Tq,
                            total_seqlen_k=Tk)
 
     def restore():

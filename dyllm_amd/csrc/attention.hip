@@ -4,23 +4,25 @@
 //                 the flash_attn_varlen_func call at attention.py:41-52).
 //   RowSparse  -- the same for a compact list of salient query rows (q_rows) against the
 //                 full cached K/V; output is compact (attention.py:76-87).
-//   ColSparse  -- O = C + softmax(Q K^T / sqrt(D)) dV with PV only on key blocks that hold
+//   ColSparse  -- O = C + softmax(Q K^T / sqrt(D)) dV with PV only on key groups that hold
 //                 salient rows, plus the saliency statistics of every row; salient rows take
 //                 o_sal instead (attention_ops_kernels_sm80.cu:44-483 together with
 //                 attention_aux_kernels.cu:22-72).
 //
 // Numerics follow the reference: log2-domain online softmax over 64-key blocks, running max
-// initialised to -FLT_MAX, P rounded to bf16 before the PV product while the row sum stays
-// fp32, 1/rowsum as a correctly rounded reciprocal, new = C + (acc * inv) without contraction,
-// statistics from the unrounded fp32 new values (bf16 o_sal for salient rows).
+// initialised to -FLT_MAX, P rounded to bf16 (round to nearest even) relative to the running
+// max before the PV product while the row sum stays fp32, 1/rowsum as a correctly rounded
+// division, new = C + (acc * inv) without contraction, statistics from the unrounded fp32 new
+// values (bf16 o_sal for salient rows).
 //
-// MI355X layout: one workgroup = 4 wavefronts = 128 query rows of one (sequence, head); each
-// wavefront owns 32 query rows. The score tile is computed transposed, S^T = K Q^T, with
-// v_mfma_f32_32x32x16_bf16 so that lane l holds query row l%32: row max / row sum / rescale
-// are lane-local (plus one cross-half swap), and the P^T accumulator feeds the PV MFMA
-// (O^T = V^T P^T) as its B operand without any data movement. K is staged row-major and V
-// transposed in LDS (padded rows, no bank-conflicting strides). Workgroups are remapped so
-// that all query tiles of one (sequence, kv-head) land on the same XCD and share its L2.
+// MI355X layout: a workgroup is NW wavefronts x 32 query rows of one (sequence, head). The
+// score tile is computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16 so that lane
+// l holds query row l%32: row max / row sum / rescale are lane-local (plus one swap with the
+// other half-wave), and the P^T accumulator feeds the PV MFMA (O^T = V^T P^T) as its B
+// operand with no data movement. K is staged row-major and V transposed in LDS (rows padded so
+// that the fragment reads are bank-conflict free); the next 64-key tile is fetched into
+// registers while the current one is multiplied. Workgroups are remapped so that all query
+// tiles of one (sequence, kv-head) land on the same XCD and share its L2.
 #include "kernels.h"
 
 #include <float.h>
@@ -28,10 +30,9 @@
 namespace dyllm {
 
 constexpr int kD = 128;
-constexpr int kBQ = 128;       // query rows per workgroup
-constexpr int kBK = 64;        // keys per block (reference block width)
-constexpr int kKStride = kD + 8;     // K tile row stride (elements)
-constexpr int kVStride = kBK + 8;    // V^T tile row stride (elements)
+constexpr int kBK = 64;              // keys per block (reference block width)
+constexpr int kKStride = kD + 8;     // K tile row stride (elements): 272 B, conflict-free b128 reads
+constexpr int kVStride = kBK + 12;   // V^T tile row stride (elements): 152 B, conflict-free b64 reads
 
 union Pack8 {
   bf16x8_t v;
@@ -41,10 +42,15 @@ union Pack8 {
 union Pack4 {
   bf16x4_t v;
   uint32_t u[2];
+  uint2 d;
 };
 
-template <AttnMode MODE>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+template <AttnMode MODE, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_kernel(AttnArgs a) {
+  constexpr int NT = NW * 64;              // threads
+  constexpr int BQ = NW * 32;              // query rows per workgroup
+  constexpr int KCH = kBK * kD / 8 / NT;   // 16-byte K chunks per thread per tile
+  constexpr int VIT = (kBK / 4) * (kD / 8) / NT;  // (4 keys x 8 d) V items per thread per tile
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
 
@@ -58,13 +64,13 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   const int kvh = head / (a.H / a.Hkv);
 
   const int row_beg = a.cu_rows[b], row_end = a.cu_rows[b + 1];
-  if (row_beg + tile * kBQ >= row_end) return;
+  if (row_beg + tile * BQ >= row_end) return;
   const int k_beg = a.cu_k[b], Lk = a.cu_k[b + 1] - k_beg;
   const int64_t kv0 = a.kv_start ? a.kv_start[b] : int64_t(k_beg);
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int ql = lane & 31, half = lane >> 5;
-  const int row = row_beg + tile * kBQ + w * 32 + ql;  // compact row of this lane
+  const int row = row_beg + tile * BQ + w * 32 + ql;  // compact row of this lane
   const bool row_ok = row < row_end;
   int64_t qrow = row;
   if constexpr (MODE == AttnMode::RowSparse) qrow = row_ok ? a.q_rows[row] : 0;
@@ -96,48 +102,75 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   const int32_t* ks_b = a.kslot ? a.kslot + k_beg : nullptr;
   const int nkb = (Lk + kBK - 1) / kBK;
 
-  for (int kb = 0; kb < nkb; ++kb) {
+  // register stage of one K/V tile
+  uint4 kreg[KCH];
+  uint4 vreg[VIT][4];
+  uint64_t mask_next = ~0ull;
+  auto fetch = [&](int kb) {
     const int key0 = kb * kBK;
-    uint64_t bmask = ~0ull;
-    if constexpr (MODE == AttnMode::ColSparse) bmask = a.kmask[int64_t(b) * a.nblk + kb];
-
-    // ---- stage K (row-major) and V (transposed) into LDS ----------------------------
+    uint64_t bm = ~0ull;
+    if constexpr (MODE == AttnMode::ColSparse) bm = a.kmask[int64_t(b) * a.nblk + kb];
+    mask_next = bm;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int c = tid + 256 * it;
+    for (int it = 0; it < KCH; ++it) {
+      const int c = tid + NT * it;
       const int key = c >> 4, dc = c & 15;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (key0 + key < Lk) v = *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8);
-      *reinterpret_cast<uint4*>(&k_lds[key * kKStride + dc * 8]) = v;
+      kreg[it] = (key0 + key < Lk) ? *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8)
+                                   : make_uint4(0, 0, 0, 0);
     }
-    if (bmask != 0) {
+    if (bm != 0) {
 #pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int c = tid + 256 * it;
-        const int kp = c & 31, dc = c >> 5;
-        const int k0 = 2 * kp;
-        uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-        int64_t r0 = key0 + k0, r1 = key0 + k0 + 1;
-        if (ks_b) {  // compact dV: key -> slot (or no salient row: zero)
-          r0 = (r0 < Lk) ? ks_b[r0] : -1;
-          r1 = (r1 < Lk) ? ks_b[r1] : -1;
-        } else {
-          r0 = (r0 < Lk) ? r0 : -1;
-          r1 = (r1 < Lk) ? r1 : -1;
-        }
-        if (r0 >= 0) v0 = *reinterpret_cast<const uint4*>(Vb + r0 * ldkv + dc * 8);
-        if (r1 >= 0) v1 = *reinterpret_cast<const uint4*>(Vb + r1 * ldkv + dc * 8);
-        const uint32_t x0[4] = {v0.x, v0.y, v0.z, v0.w}, x1[4] = {v1.x, v1.y, v1.z, v1.w};
+      for (int it = 0; it < VIT; ++it) {
+        const int c = tid + NT * it;
+        const int kq = c & 15, dc = c >> 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t lo = (x0[j] & 0xffffu) | (x1[j] << 16);
-          const uint32_t hi = (x0[j] >> 16) | (x1[j] & 0xffff0000u);
-          *reinterpret_cast<uint32_t*>(&vt_lds[(dc * 8 + 2 * j) * kVStride + k0]) = lo;
-          *reinterpret_cast<uint32_t*>(&vt_lds[(dc * 8 + 2 * j + 1) * kVStride + k0]) = hi;
+          int64_t r = key0 + 4 * kq + j;
+          if (r >= Lk) r = -1;
+          else if (ks_b) r = ks_b[r];
+          vreg[it][j] = (r >= 0) ? *reinterpret_cast<const uint4*>(Vb + r * ldkv + dc * 8) : make_uint4(0, 0, 0, 0);
         }
       }
     }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int it = 0; it < KCH; ++it) {
+      const int c = tid + NT * it;
+      const int key = c >> 4, dc = c & 15;
+      *reinterpret_cast<uint4*>(&k_lds[key * kKStride + dc * 8]) = kreg[it];
+    }
+    if (mask_next != 0) {
+#pragma unroll
+      for (int it = 0; it < VIT; ++it) {
+        const int c = tid + NT * it;
+        const int kq = c & 15, dc = c >> 4;
+        const uint32_t x[4][4] = {{vreg[it][0].x, vreg[it][0].y, vreg[it][0].z, vreg[it][0].w},
+                                  {vreg[it][1].x, vreg[it][1].y, vreg[it][1].z, vreg[it][1].w},
+                                  {vreg[it][2].x, vreg[it][2].y, vreg[it][2].z, vreg[it][2].w},
+                                  {vreg[it][3].x, vreg[it][3].y, vreg[it][3].z, vreg[it][3].w}};
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+          // d = dc*8 + 2*wd (low halves) and +1 (high halves) for the 4 keys
+          uint2 lo, hi;
+          lo.x = __builtin_amdgcn_perm(x[1][wd], x[0][wd], 0x05040100u);
+          lo.y = __builtin_amdgcn_perm(x[3][wd], x[2][wd], 0x05040100u);
+          hi.x = __builtin_amdgcn_perm(x[1][wd], x[0][wd], 0x07060302u);
+          hi.y = __builtin_amdgcn_perm(x[3][wd], x[2][wd], 0x07060302u);
+          *reinterpret_cast<uint2*>(&vt_lds[(dc * 8 + 2 * wd) * kVStride + 4 * kq]) = lo;
+          *reinterpret_cast<uint2*>(&vt_lds[(dc * 8 + 2 * wd + 1) * kVStride + 4 * kq]) = hi;
+        }
+      }
+    }
+  };
+
+  if (nkb > 0) fetch(0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int key0 = kb * kBK;
+    const uint64_t bmask = mask_next;
+    stage();
     __syncthreads();
+    if (kb + 1 < nkb) fetch(kb + 1);
 
     // ---- S^T = K Q^T for two 32-key tiles --------------------------------------------
     f32x16_t s_acc[2];
@@ -153,18 +186,23 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     }
 
     // ---- online softmax (lane = query row) ----------------------------------------------
-    float bm = -FLT_MAX;
+    if (key0 + kBK > Lk) {  // ragged last block only
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = key0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+          if (key >= Lk) s_acc[t][r] = -FLT_MAX;
+        }
+    }
+    float bm = s_acc[0][0];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = key0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        if (key >= Lk) s_acc[t][r] = -FLT_MAX;
-        bm = fmaxf(bm, s_acc[t][r]);
-      }
+      for (int r = 0; r < 16; ++r) bm = fmaxf(bm, s_acc[t][r]);
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
     const float m_new = fmaxf(m_run, bm);
-    const float rescale = exp2f((m_run - m_new) * c2);
+    const float rescale = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
     const float m2 = m_new * c2;
     m_run = m_new;
     float psum = 0.f;
@@ -176,8 +214,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         Pack8 p;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float e0 = exp2f(fmaf(s_acc[t][8 * u + 2 * j], c2, -m2));
-          const float e1 = exp2f(fmaf(s_acc[t][8 * u + 2 * j + 1], c2, -m2));
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(s_acc[t][8 * u + 2 * j], c2, -m2));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(s_acc[t][8 * u + 2 * j + 1], c2, -m2));
           psum += e0 + e1;
           p.u[j] = pack_bf16x2(e0, e1);
         }
@@ -201,8 +239,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
           for (int dt = 0; dt < 4; ++dt) {
             const uint16_t* vr = &vt_lds[(dt * 32 + ql) * kVStride + kofs];
             Pack4 lo, hi;
-            lo.v = *reinterpret_cast<const bf16x4_t*>(vr);
-            hi.v = *reinterpret_cast<const bf16x4_t*>(vr + 8);
+            lo.d = *reinterpret_cast<const uint2*>(vr);
+            hi.d = *reinterpret_cast<const uint2*>(vr + 8);
             Pack8 va;
             va.u[0] = lo.u[0];
             va.u[1] = lo.u[1];
@@ -362,18 +400,34 @@ int launch_seq_row_starts(const int64_t* seq_starts, const int64_t* seq_ids, con
   return check_launch("seq_row_starts_kernel");
 }
 
+template <AttnMode MODE, int NW>
+static void launch_mode(const AttnArgs& a, int max_rows_per_seq, hipStream_t s) {
+  AttnArgs g = a;
+  g.tiles_per_seq = int(cdiv(max_rows_per_seq, NW * 32));
+  const int64_t nwg = int64_t(g.tiles_per_seq) * a.H * a.B;
+  attention_kernel<MODE, NW><<<unsigned(nwg), NW * 64, 0, s>>>(g);
+}
+
 int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s) {
   DYLLM_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.H % a.Hkv == 0, "bad head counts");
   DYLLM_REQUIRE(max_rows_per_seq >= 0, "bad row bound");
   if (max_rows_per_seq == 0) return 0;
-  AttnArgs g = a;
-  g.tiles_per_seq = int(cdiv(max_rows_per_seq, kBQ));
-  const int64_t nwg = int64_t(g.tiles_per_seq) * a.H * a.B;
-  DYLLM_REQUIRE(nwg < (int64_t(1) << 31), "grid too large");
+  DYLLM_REQUIRE(cdiv(max_rows_per_seq, 64) * a.H * a.B < (int64_t(1) << 31), "grid too large");
+  // 4-wave workgroups (128 rows) when the grid has enough of them to fill 256 CUs twice,
+  // otherwise 2-wave workgroups (64 rows) for twice the parallelism on few rows.
+  const bool wide = cdiv(max_rows_per_seq, 128) * a.H * a.B >= 512;
   switch (mode) {
-    case AttnMode::Dense: attention_kernel<AttnMode::Dense><<<unsigned(nwg), 256, 0, s>>>(g); break;
-    case AttnMode::RowSparse: attention_kernel<AttnMode::RowSparse><<<unsigned(nwg), 256, 0, s>>>(g); break;
-    case AttnMode::ColSparse: attention_kernel<AttnMode::ColSparse><<<unsigned(nwg), 256, 0, s>>>(g); break;
+    case AttnMode::Dense:
+      wide ? launch_mode<AttnMode::Dense, 4>(a, max_rows_per_seq, s) : launch_mode<AttnMode::Dense, 2>(a, max_rows_per_seq, s);
+      break;
+    case AttnMode::RowSparse:
+      wide ? launch_mode<AttnMode::RowSparse, 4>(a, max_rows_per_seq, s)
+           : launch_mode<AttnMode::RowSparse, 2>(a, max_rows_per_seq, s);
+      break;
+    case AttnMode::ColSparse:
+      wide ? launch_mode<AttnMode::ColSparse, 4>(a, max_rows_per_seq, s)
+           : launch_mode<AttnMode::ColSparse, 2>(a, max_rows_per_seq, s);
+      break;
   }
   return check_launch("attention_kernel");
 }

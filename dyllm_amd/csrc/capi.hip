@@ -323,12 +323,15 @@ int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t
 }
 
 // ---------------------------------------------------------------------------------------
+size_t dyllm_ffn_down_workspace_bytes(int64_t rows, int hidden, int intermediate) {
+  if (rows <= 0) return 0;
+  const int tm = gemm_pick_tile(rows, hidden, GemmEpi::Store);
+  return align256(gemm_partial_bytes(rows, hidden, tm, gemm_pick_ksplit(rows, hidden, intermediate, tm)));
+}
+
 size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate) {
   return align256(size_t(rows > 0 ? rows : 0) * size_t(intermediate) * 2);
 }
-
-// 256x256 tiles when they still give >= one workgroup per CU, else 128x128.
-static int pick_tile(int64_t M, int64_t N) { return (cdiv(M, 256) * cdiv(N, 256) >= 256) ? 256 : 128; }
 
 int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
                       int hidden, int intermediate, void* h_out, void* stream) {
@@ -352,12 +355,11 @@ int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int6
   g.N = 2 * intermediate;
   g.K = hidden;
   g.half_n = intermediate;
-  const int t1 = (pick_tile(rows, g.N) == 256 && intermediate % 128 == 0) ? 256 : 128;
-  return launch_gemm(GemmEpi::SwiGLU, g, rows, t1, DYLLM_STREAM(stream));
+  return launch_gemm(GemmEpi::SwiGLU, g, rows, 0, 1, DYLLM_STREAM(stream));
 }
 
 int dyllm_ffn_down(const void* h, int64_t rows, const void* w_down, int hidden, int intermediate, void* out,
-                   const int64_t* out_rows, void* stream) {
+                   const int64_t* out_rows, void* workspace, size_t workspace_bytes, void* stream) {
   DYLLM_NONNULL(h);
   DYLLM_NONNULL(w_down);
   DYLLM_NONNULL(out);
@@ -377,18 +379,29 @@ int dyllm_ffn_down(const void* h, int64_t rows, const void* w_down, int hidden, 
   d.M = rows;
   d.N = hidden;
   d.K = intermediate;
-  return launch_gemm(GemmEpi::Store, d, rows, pick_tile(rows, hidden), DYLLM_STREAM(stream));
+  const int tm = gemm_pick_tile(rows, hidden, GemmEpi::Store);
+  const int ks = gemm_pick_ksplit(rows, hidden, intermediate, tm);
+  if (ks > 1) {
+    const size_t need = gemm_partial_bytes(rows, hidden, tm, ks);
+    DYLLM_REQUIRE(workspace && workspace_bytes >= need,
+                  "workspace too small: need " + std::to_string(need) + " bytes (dyllm_ffn_down_workspace_bytes)");
+    d.partial = static_cast<float*>(workspace);
+  }
+  return launch_gemm(GemmEpi::Store, d, rows, tm, ks, DYLLM_STREAM(stream));
 }
 
 int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
                      const void* w_down, int hidden, int intermediate, void* workspace, size_t workspace_bytes,
                      void* out, const int64_t* out_rows, void* stream) {
   if (rows <= 0) return 0;
-  const size_t need = dyllm_swiglu_ffn_workspace_bytes(rows, intermediate);
-  DYLLM_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need " + std::to_string(need) + " bytes");
+  const size_t hb = dyllm_swiglu_ffn_workspace_bytes(rows, intermediate);
+  const size_t db = dyllm_ffn_down_workspace_bytes(rows, hidden, intermediate);
+  DYLLM_REQUIRE(workspace && workspace_bytes >= hb + db,
+                "workspace too small: need " + std::to_string(hb + db) + " bytes");
   if (int rc = dyllm_ffn_gate_up(x, ld_x, rows_idx, rows, w_gate_up, hidden, intermediate, workspace, stream))
     return rc;
-  return dyllm_ffn_down(workspace, rows, w_down, hidden, intermediate, out, out_rows, stream);
+  return dyllm_ffn_down(workspace, rows, w_down, hidden, intermediate, out, out_rows,
+                        static_cast<char*>(workspace) + hb, db, stream);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -471,7 +484,7 @@ int dyllm_fused_experts(const void* x, const int32_t* rows_idx, int64_t tokens, 
   g.N = 2 * intermediate;
   g.K = hidden;
   g.half_n = intermediate;
-  if (int rc = launch_gemm(GemmEpi::SwiGLU, g, cap, kMoeBlock, s)) return rc;
+  if (int rc = launch_gemm(GemmEpi::SwiGLU, g, cap, kMoeBlock, 1, s)) return rc;
   // GEMM 2: y[slot] = (inter[slot] W2^T) * w[slot]
   GemmArgs d{};
   d.A = inter;
@@ -491,7 +504,7 @@ int dyllm_fused_experts(const void* x, const int32_t* rows_idx, int64_t tokens, 
   d.M = cap;
   d.N = hidden;
   d.K = intermediate;
-  if (int rc = launch_gemm(GemmEpi::Store, d, cap, kMoeBlock, s)) return rc;
+  if (int rc = launch_gemm(GemmEpi::Store, d, cap, kMoeBlock, 1, s)) return rc;
   return launch_moe_combine(y, tokens, hidden, top_k, static_cast<uint16_t*>(out), out_rows, s);
 }
 

@@ -12,40 +12,54 @@
 //                               the reference's bf16 GEMM output is);
 //   * a store epilogue       -- optional per-row routing weight (fused_moe.py:160-162) and a
 //                               row remap that scatters straight into the cached FFN output
-//                               (MLPcache.scatter_update, mlp_cache_manage.py:24-40).
+//                               (MLPcache.scatter_update, mlp_cache_manage.py:24-40);
+//   * split-K                -- for short-M, wide-K products (the down projection of a few
+//                               hundred salient rows) the K range is cut into slices whose fp32
+//                               partial tiles are summed in slice order by a reduction kernel
+//                               that applies the store epilogue (deterministic).
 //
-// Tiling: workgroup tile BM x BN x 64, 4 wavefronts in a 2 x 2 grid, each wavefront a
-// (BM/2) x (BN/2) block of v_mfma_f32_32x32x16_bf16 tiles. Operands are staged through LDS
-// in two buffers (rows padded to 144 B so the 16-byte fragment reads are conflict free),
-// with the next K slice prefetched into registers while the current one is multiplied.
-// The MFMA is issued as D = W_tile * A_tile^T so that each lane owns one output row and
-// four consecutive output columns per register group: 8-byte stores and one row lookup
-// per lane for the scatter. Workgroups are ordered M-fastest and remapped XCD-major so the
-// M tiles sharing a weight slice run on one XCD and read that slice from HBM once.
+// Tiling: workgroup tile BM x 256 x 64, 8 wavefronts (2 per SIMD) in a 2 (M) x 4 (N) grid,
+// each wavefront (BM/2) x 64 of v_mfma_f32_32x32x16_bf16 tiles. Operands are staged through
+// LDS in two buffers of unpadded 128-byte rows whose 16-byte chunks are XOR-swizzled by row
+// (chunk ^ (row & 7)), so both the 16-byte stores and the fragment reads are spread over the
+// banks; the next K slice is fetched into registers while the current one is multiplied and
+// one barrier per K slice separates the buffers. The MFMA is issued as D = W_tile * A_tile^T
+// so that each lane owns one output row and four consecutive output columns per register
+// group: 8-byte stores and one row lookup per lane for the scatter. Workgroups are ordered
+// M-fastest and remapped XCD-major so the M tiles sharing a weight slice run on one XCD and
+// read that slice from HBM once. BM is 128, 192 or 256, picked so the number of tiles
+// quantises well onto the 256 CUs.
 #include "kernels.h"
 
 namespace dyllm {
 
 constexpr int kGemmBK = 64;
-constexpr int kGemmLds = kGemmBK + 8;  // 72 elements = 144 B per staged row
+constexpr int kGemmBN = 256;
+constexpr int kGemmThreads = 512;
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float bf16_rt(float x) { return __uint_as_float(uint32_t(f32_to_bf16(x)) << 16); }
 
-template <int BM, int BN, GemmEpi EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+// element offset of (row, 16-byte chunk) in a swizzled 64-element-wide tile
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kGemmBK + ((chunk ^ (row & 7)) << 3); }
+
+template <int BM, GemmEpi EPI>
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t gsm[];
-  constexpr int WM = BM / 2, WN = BN / 2;     // wave tile (rows of A, rows of W)
+  constexpr int BN = kGemmBN;
+  constexpr int WM = BM / 2, WN = BN / 4;     // wave tile (rows of A, rows of W)
   constexpr int TM = WM / 32, TN = WN / 32;   // 32x32 MFMA tiles per wave
-  constexpr int CA = BM / 32, CW = BN / 32;   // 16-byte chunks per thread per K slice
-  constexpr int BUF = (BM + BN) * kGemmLds;
+  constexpr int BUF = (BM + BN) * kGemmBK;
 
   const int64_t M = g.num_m_dev ? int64_t(g.num_m_dev[0]) : g.M;
   const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (BN / 2)) : int(cdiv(g.N, BN));
   const int nwg = gridDim.x;
   int wg = blockIdx.x;
   if ((nwg & 7) == 0) wg = (wg & 7) * (nwg >> 3) + (wg >> 3);
-  const int m_tiles_launched = nwg / n_tiles;
+  const int per_split = nwg / g.ksplit;
+  const int kz = wg / per_split;
+  wg -= kz * per_split;
+  const int m_tiles_launched = per_split / n_tiles;
   const int mt = wg % m_tiles_launched, nt = wg / m_tiles_launched;
   const int64_t m0 = int64_t(mt) * BM;
   if (m0 >= M) return;
@@ -57,55 +71,62 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   const uint16_t* Wb = g.W;
   if (g.tile_expert) Wb += int64_t(g.tile_expert[mt]) * g.w_expert_stride;
 
-  // rows this thread stages: A row r = tid/8 + 32*i, W row likewise; k chunk = tid%8
-  const int kc = tid & 7;
+  const int nk_total = g.K / kGemmBK;
+  const int nk = nk_total / g.ksplit;
+  const int k_begin = kz * nk;
+
+  // Direct global->LDS staging: each wavefront fills 1 KB blocks of 8 swizzled rows; lane L
+  // of a block lands at byte 16*L, i.e. row L/8, physical chunk L%8, which holds logical
+  // chunk (L%8) ^ (L/8). Rows outside the problem (m >= M, padding ids, n >= N) are clamped
+  // to a valid row: their products are never stored.
+  constexpr int CA = BM / 64, CW = BN / 64;    // 1 KB blocks per wavefront per K slice
+  const int lrow = lane >> 3, lchunk = (lane & 7) ^ (lane >> 3);
   const uint16_t* a_src[CA];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
-    const int64_t m = m0 + (tid >> 3) + 32 * i;
-    a_src[i] = nullptr;
+    const int64_t m = m0 + (w + 8 * i) * 8 + lrow;
+    int64_t row = 0;
     if (m < M) {
-      int64_t row = m;
+      row = m;
       if (g.a_ids) {
         const int64_t id = g.a_ids[m];
-        row = (id < g.id_limit) ? id / g.a_div : -1;
+        row = (id < g.id_limit) ? id / g.a_div : 0;
       }
-      if (row >= 0) a_src[i] = g.A + row * g.lda + kc * 8;
     }
+    a_src[i] = g.A + row * g.lda + int64_t(k_begin) * kGemmBK + lchunk * 8;
   }
   const uint16_t* w_src[CW];
 #pragma unroll
   for (int i = 0; i < CW; ++i) {
-    const int r = (tid >> 3) + 32 * i;
+    const int r = (w + 8 * i) * 8 + lrow;
     int64_t wrow;
     if constexpr (EPI == GemmEpi::SwiGLU)
       wrow = (r < BN / 2) ? int64_t(nt) * (BN / 2) + r : int64_t(g.half_n) + int64_t(nt) * (BN / 2) + (r - BN / 2);
     else
       wrow = int64_t(nt) * BN + r;
-    w_src[i] = (wrow < g.N) ? Wb + wrow * g.ldw + kc * 8 : nullptr;
+    if (wrow >= g.N) wrow = 0;
+    w_src[i] = Wb + wrow * g.ldw + int64_t(k_begin) * kGemmBK + lchunk * 8;
   }
-
-  uint4 ra[CA], rw[CW];
-  auto gload = [&](int kt) {
+  typedef __attribute__((address_space(3))) void lds_void;
+  typedef const __attribute__((address_space(1))) void glb_void;
+  auto stage = [&](int kt, int buf) {
     const int64_t ko = int64_t(kt) * kGemmBK;
-#pragma unroll
-    for (int i = 0; i < CA; ++i) ra[i] = a_src[i] ? *reinterpret_cast<const uint4*>(a_src[i] + ko) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < CW; ++i) rw[i] = w_src[i] ? *reinterpret_cast<const uint4*>(w_src[i] + ko) : make_uint4(0, 0, 0, 0);
-  };
-  auto lstore = [&](int buf) {
     uint16_t* As = gsm + buf * BUF;
-    uint16_t* Ws = As + BM * kGemmLds;
+    uint16_t* Ws = As + BM * kGemmBK;
 #pragma unroll
-    for (int i = 0; i < CA; ++i) *reinterpret_cast<uint4*>(&As[((tid >> 3) + 32 * i) * kGemmLds + kc * 8]) = ra[i];
+    for (int i = 0; i < CA; ++i)
+      __builtin_amdgcn_global_load_lds((glb_void*)(a_src[i] + ko),
+                                       (lds_void*)(As + (w + 8 * i) * 8 * kGemmBK), 16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < CW; ++i) *reinterpret_cast<uint4*>(&Ws[((tid >> 3) + 32 * i) * kGemmLds + kc * 8]) = rw[i];
+    for (int i = 0; i < CW; ++i)
+      __builtin_amdgcn_global_load_lds((glb_void*)(w_src[i] + ko),
+                                       (lds_void*)(Ws + (w + 8 * i) * 8 * kGemmBK), 16, 0, 0);
   };
 
   // W-tile row base of the wave's n-subtile i
   auto wrow_base = [&](int i) -> int {
     if constexpr (EPI == GemmEpi::SwiGLU)
-      return (i < TN / 2) ? wn * (BN / 4) + 32 * i : BN / 2 + wn * (BN / 4) + 32 * (i - TN / 2);
+      return (i < TN / 2) ? wn * (BN / 8) + 32 * i : BN / 2 + wn * (BN / 8) + 32 * (i - TN / 2);
     else
       return wn * WN + 32 * i;
   };
@@ -118,34 +139,62 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = g.K / kGemmBK;
-  gload(0);
-  lstore(0);
+  stage(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
+    if (kt + 1 < nk) stage(kt + 1, cur ^ 1);
     const uint16_t* As = gsm + cur * BUF;
-    const uint16_t* Ws = As + BM * kGemmLds;
-#pragma unroll
-    for (int ks = 0; ks < kGemmBK / 16; ++ks) {
-      bf16x8_t wf[TN], af[TM];
-#pragma unroll
-      for (int i = 0; i < TN; ++i)
-        wf[i] = *reinterpret_cast<const bf16x8_t*>(&Ws[(wrow_base(i) + l32) * kGemmLds + ks * 16 + half * 8]);
-#pragma unroll
-      for (int j = 0; j < TM; ++j)
-        af[j] = *reinterpret_cast<const bf16x8_t*>(&As[(wm * WM + 32 * j + l32) * kGemmLds + ks * 16 + half * 8]);
-#pragma unroll
-      for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) lstore(cur ^ 1);
+    const uint16_t* Ws = As + BM * kGemmBK;
+    // fragments of K-substep ks+1 are read while the MFMAs of ks run (two named buffers so
+    // every register index stays static)
+    bf16x8_t wf0[TN], af0[TM], wf1[TN], af1[TM];
+#define DYLLM_GEMM_FLOAD(KS, WF, AF)                                                                      \
+  {                                                                                                      \
+    const int ch_ = 2 * (KS) + half;                                                                     \
+    _Pragma("unroll") for (int i = 0; i < TN; ++i) WF[i] =                                               \
+        *reinterpret_cast<const bf16x8_t*>(&Ws[swz(wrow_base(i) + l32, ch_)]);                           \
+    _Pragma("unroll") for (int j = 0; j < TM; ++j) AF[j] =                                               \
+        *reinterpret_cast<const bf16x8_t*>(&As[swz(wm * WM + 32 * j + l32, ch_)]);                       \
+  }
+#define DYLLM_GEMM_MMA(WF, AF)                                                                            \
+  _Pragma("unroll") for (int i = 0; i < TN; ++i) _Pragma("unroll") for (int j = 0; j < TM; ++j) acc[i][j] = \
+      __builtin_amdgcn_mfma_f32_32x32x16_bf16(WF[i], AF[j], acc[i][j], 0, 0, 0);
+    DYLLM_GEMM_FLOAD(0, wf0, af0)
+    DYLLM_GEMM_FLOAD(1, wf1, af1)
+    DYLLM_GEMM_MMA(wf0, af0)
+    DYLLM_GEMM_FLOAD(2, wf0, af0)
+    DYLLM_GEMM_MMA(wf1, af1)
+    DYLLM_GEMM_FLOAD(3, wf1, af1)
+    DYLLM_GEMM_MMA(wf0, af0)
+    DYLLM_GEMM_MMA(wf1, af1)
+#undef DYLLM_GEMM_FLOAD
+#undef DYLLM_GEMM_MMA
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
 
   // ---- epilogue: lane owns row m = m0 + wm*WM + 32j + l32 -------------------------------
+  if constexpr (EPI == GemmEpi::Store) {
+    if (g.partial) {  // split-K slice: raw fp32 partial tile
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int64_t m = m0 + wm * WM + 32 * j + l32;
+        float* prow = g.partial + (int64_t(kz) * g.m_pad + m) * g.N;
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = nt * BN + wn * WN + 32 * i + half * 4 + q * 8;
+            if (n >= g.N) continue;
+            *reinterpret_cast<float4*>(prow + n) =
+                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < TM; ++j) {
     const int64_t m = m0 + wm * WM + 32 * j + l32;
@@ -165,7 +214,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     if constexpr (EPI == GemmEpi::SwiGLU) {
 #pragma unroll
       for (int i = 0; i < TN / 2; ++i) {
-        const int hc0 = nt * (BN / 2) + wn * (BN / 4) + 32 * i + half * 4;
+        const int hc0 = nt * (BN / 2) + wn * (BN / 8) + 32 * i + half * 4;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           float h[4];
@@ -199,41 +248,132 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   }
 }
 
-template <int BM, int BN, GemmEpi EPI>
-static int launch_gemm_cfg(const GemmArgs& g, int64_t m_tiles, hipStream_t s) {
-  const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (BN / 2)) : int(cdiv(g.N, BN));
-  const int64_t nwg = m_tiles * n_tiles;
+// Sum of the split-K slices in slice order, then the store epilogue (row remap, row scale,
+// bf16). One thread per 4 output columns.
+__global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs g) {
+  const int64_t M = g.num_m_dev ? int64_t(g.num_m_dev[0]) : g.M;
+  const int nq = g.N / 4;
+  const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t m = t / nq;
+  const int n = int(t - m * nq) * 4;
+  if (m >= M) return;
+  int64_t drow = m, id = m;
+  if (g.a_ids) {
+    id = g.a_ids[m];
+    if (id >= g.id_limit) return;
+    if (g.c_by_id) drow = id;
+  }
+  if (g.c_rows) drow = g.c_rows[m];
+  float scale = 1.0f;
+  if (g.row_scale_f32) scale = g.row_scale_f32[id];
+  if (g.row_scale_bf16) scale = bf16_to_f32(g.row_scale_bf16[id]);
+  float4 s = *reinterpret_cast<const float4*>(g.partial + m * g.N + n);
+  for (int z = 1; z < g.ksplit; ++z) {
+    const float4 v = *reinterpret_cast<const float4*>(g.partial + (int64_t(z) * g.m_pad + m) * g.N + n);
+    s.x += v.x;
+    s.y += v.y;
+    s.z += v.z;
+    s.w += v.w;
+  }
+  uint2 st;
+  st.x = pack_bf16x2(s.x * scale, s.y * scale);
+  st.y = pack_bf16x2(s.z * scale, s.w * scale);
+  *reinterpret_cast<uint2*>(g.Cout + drow * g.ldc + n) = st;
+}
+
+static constexpr size_t lds_bytes(int bm) { return size_t(2) * (bm + kGemmBN) * kGemmBK * sizeof(uint16_t); }
+
+template <int BM, GemmEpi EPI>
+static int launch_gemm_cfg(const GemmArgs& g0, int64_t m_tiles, int ksplit, hipStream_t s) {
+  GemmArgs g = g0;
+  g.ksplit = ksplit;
+  g.m_pad = m_tiles * BM;
+  const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (kGemmBN / 2)) : int(cdiv(g.N, kGemmBN));
+  const int64_t nwg = m_tiles * n_tiles * ksplit;
   if (nwg == 0) return 0;
   DYLLM_REQUIRE(nwg < (int64_t(1) << 31), "GEMM grid too large");
-  const size_t lds = size_t(2) * (BM + BN) * kGemmLds * sizeof(uint16_t);
+  const size_t lds = lds_bytes(BM);
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN, EPI>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, EPI>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
       return fail("hipFuncSetAttribute(max dynamic LDS) failed for the GEMM kernel");
     attr_set = true;
   }
-  gemm_kernel<BM, BN, EPI><<<unsigned(nwg), 256, lds, s>>>(g);
-  return check_launch("gemm_kernel");
+  gemm_kernel<BM, EPI><<<unsigned(nwg), kGemmThreads, lds, s>>>(g);
+  if (int rc = check_launch("gemm_kernel")) return rc;
+  if (ksplit > 1) {
+    const int64_t threads = m_tiles * BM * (g.N / 4);
+    gemm_partial_reduce_kernel<<<unsigned(cdiv(threads, 256)), 256, 0, s>>>(g);
+    return check_launch("gemm_partial_reduce_kernel");
+  }
+  return 0;
+}
+
+// Estimated time of a tile choice: rounds of 256 CUs x the tile's height (work per tile).
+static double tile_cost(int64_t M, int n_tiles, int bm, int ksplit) {
+  const int64_t tiles = cdiv(M, bm) * n_tiles * ksplit;
+  const int64_t rounds = cdiv(tiles, 256);
+  return double(rounds) * bm / ksplit + (ksplit > 1 ? 0.15 * bm : 0.0);
+}
+
+int gemm_pick_tile(int64_t M, int N, GemmEpi epi) {
+  const int n_tiles = (epi == GemmEpi::SwiGLU) ? int(cdiv(N / 2, kGemmBN / 2)) : int(cdiv(N, kGemmBN));
+  int best = 256;
+  double best_cost = 1e30;
+  for (int bm : {256, 192, 128}) {
+    const double c = tile_cost(M, n_tiles, bm, 1);
+    if (c < best_cost - 1e-9) {
+      best_cost = c;
+      best = bm;
+    }
+  }
+  return best;
+}
+
+int gemm_pick_ksplit(int64_t M, int N, int K, int tile_m) {
+  const int n_tiles = int(cdiv(N, kGemmBN));
+  const int nk = K / kGemmBK;
+  int best = 1;
+  double best_cost = tile_cost(M, n_tiles, tile_m, 1);
+  for (int ks : {2, 3, 4, 6, 8}) {
+    if (nk % ks != 0 || nk / ks < 4) continue;
+    const double c = tile_cost(M, n_tiles, tile_m, ks);
+    if (c < best_cost - 1e-9) {
+      best_cost = c;
+      best = ks;
+    }
+  }
+  return best;
+}
+
+size_t gemm_partial_bytes(int64_t m_bound, int N, int tile_m, int ksplit) {
+  if (ksplit <= 1) return 0;
+  return size_t(ksplit) * size_t(cdiv(m_bound, tile_m) * tile_m) * size_t(N) * sizeof(float);
 }
 
 // m_bound: host-side upper bound of M (number of BM tiles launched = cdiv(m_bound, BM)).
-int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, hipStream_t s) {
+int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, int ksplit, hipStream_t s) {
   DYLLM_REQUIRE(g.K > 0 && g.K % kGemmBK == 0, "GEMM K must be a positive multiple of 64");
-  DYLLM_REQUIRE(g.N > 0, "GEMM N must be positive");
+  DYLLM_REQUIRE(g.N > 0 && g.N % 8 == 0, "GEMM N must be a positive multiple of 8");
   DYLLM_REQUIRE(g.lda % 8 == 0 && g.ldw % 8 == 0 && g.ldc % 4 == 0, "GEMM leading dimensions must keep 16-byte rows");
   if (m_bound <= 0) return 0;
+  if (tile_m == 0) tile_m = gemm_pick_tile(m_bound, g.N, epi);
+  DYLLM_REQUIRE(tile_m == 128 || tile_m == 192 || tile_m == 256, "tile height must be 128, 192 or 256");
+  if (ksplit < 1) ksplit = 1;
+  DYLLM_REQUIRE((g.K / kGemmBK) % ksplit == 0, "split-K must divide the number of 64-wide K slices");
+  DYLLM_REQUIRE(ksplit == 1 || (epi == GemmEpi::Store && g.partial != nullptr), "split-K needs a partial buffer");
+  const int64_t mt = cdiv(m_bound, tile_m);
   if (epi == GemmEpi::SwiGLU) {
     DYLLM_REQUIRE(g.N == 2 * g.half_n, "SwiGLU weight must hold gate rows then up rows (N = 2 * intermediate)");
-    if (tile_m == 256) {
-      DYLLM_REQUIRE(g.half_n % 128 == 0, "SwiGLU intermediate size must be a multiple of 128");
-      return launch_gemm_cfg<256, 256, GemmEpi::SwiGLU>(g, cdiv(m_bound, 256), s);
-    }
-    DYLLM_REQUIRE(g.half_n % 64 == 0, "SwiGLU intermediate size must be a multiple of 64");
-    return launch_gemm_cfg<128, 128, GemmEpi::SwiGLU>(g, cdiv(m_bound, 128), s);
+    DYLLM_REQUIRE(g.half_n % (kGemmBN / 2) == 0, "SwiGLU intermediate size must be a multiple of 128");
+    if (tile_m == 256) return launch_gemm_cfg<256, GemmEpi::SwiGLU>(g, mt, 1, s);
+    if (tile_m == 192) return launch_gemm_cfg<192, GemmEpi::SwiGLU>(g, mt, 1, s);
+    return launch_gemm_cfg<128, GemmEpi::SwiGLU>(g, mt, 1, s);
   }
-  if (tile_m == 256) return launch_gemm_cfg<256, 256, GemmEpi::Store>(g, cdiv(m_bound, 256), s);
-  return launch_gemm_cfg<128, 128, GemmEpi::Store>(g, cdiv(m_bound, 128), s);
+  if (tile_m == 256) return launch_gemm_cfg<256, GemmEpi::Store>(g, mt, ksplit, s);
+  if (tile_m == 192) return launch_gemm_cfg<192, GemmEpi::Store>(g, mt, ksplit, s);
+  return launch_gemm_cfg<128, GemmEpi::Store>(g, mt, ksplit, s);
 }
 
 }  // namespace dyllm

@@ -85,8 +85,16 @@ struct GemmArgs {
   int64_t M;
   int N, K;
   int half_n;
+  float* partial;             // split-K: fp32 partial tiles [ksplit][m_pad][N] (Store epilogue only)
+  int ksplit;                 // number of K slices (1: no split)
+  int64_t m_pad;              // rows of one partial slice (m tiles launched * BM)
 };
-int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, hipStream_t s);
+// tile_m: 128 / 192 / 256, or 0 to choose from M and the grid size. ksplit > 1 needs
+// g.partial with gemm_partial_bytes() bytes and is followed by the reduction kernel.
+int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, int ksplit, hipStream_t s);
+size_t gemm_partial_bytes(int64_t m_bound, int N, int tile_m, int ksplit);
+int gemm_pick_tile(int64_t M, int N, GemmEpi epi);
+int gemm_pick_ksplit(int64_t M, int N, int K, int tile_m);
 
 int launch_moe_router(const uint16_t* x, const int32_t* rows, const uint16_t* wr, int64_t T, int Hd, int E, int top_k,
                       int renorm, uint16_t* topk_w, int32_t* topk_ids, hipStream_t s);

@@ -71,7 +71,8 @@ class Attention(nn.Module):
         v_full = self.v_cache.get_seqs(seq_ids, md.running_seqs).view(-1, self.num_kv_heads, self.head_dim)
 
         # row-sparse attention of the salient queries vs the full cached K/V (attention.py:76-87)
-        o_sal = ops.flash_attn_varlen_func(q, k, v_full, ctx.cu_salientlens, ctx.cu_seqlens_k, ctx.max_seqlen_q,
+        max_sal = ctx.max_salientlen if ctx.max_salientlen > 0 else ctx.max_seqlen_q
+        o_sal = ops.flash_attn_varlen_func(q, k, v_full, ctx.cu_salientlens, ctx.cu_seqlens_k, max_sal,
                                            ctx.max_seqlen_k, softmax_scale=self.scale, q_rows=idx_q32)
 
         # column-sparse attention + stats + tau test, context cache updated in place
@@ -84,7 +85,8 @@ class Attention(nn.Module):
 
         # compaction of the next salient set (attention.py:147-173)
         comp = ops.salient_compact(mask, ctx.cu_seqlens_q, ctx.cu_promptlens if q_pruned else None)
-        n = comp.n()
+        n, cu_host = comp.host()
+        ctx.max_salientlen = max(cu_host[i + 1] - cu_host[i] for i in range(len(cu_host) - 1))
         ctx.idx_salient_row = comp.idx64[:n]
         ctx.idx_salient_row_i32 = comp.idx32[:n]
         ctx.cu_salientlens = comp.cu_salientlens

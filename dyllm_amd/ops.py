@@ -207,6 +207,11 @@ class Compacted:
         self.idx64, self.idx32, self.idx_k = idx64, idx32, idx_k
         self.cu_salientlens, self.count = cu_salientlens, count
 
+    def host(self):
+        """(count, cu_salientlens as a list): one device->host read for both."""
+        h = torch.cat([self.count, self.cu_salientlens]).cpu().tolist()
+        return h[0], h[1:]
+
     def n(self) -> int:
         return int(self.count.item())
 
@@ -374,7 +379,10 @@ def ffn_down(h, w_down, out=None, out_rows=None):
         _check(out, "out", torch.bfloat16, 2)
         orow = _i64(out_rows) if out_rows is not None else None
     if M:
-        _lib.call("dyllm_ffn_down", _ptr(h), M, _ptr(w_down), hidden, inter, _ptr(out), _ptr(orow), _stream())
+        ws_bytes = _lib.load().dyllm_ffn_down_workspace_bytes(M, hidden, inter)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=h.device)
+        _lib.call("dyllm_ffn_down", _ptr(h), M, _ptr(w_down), hidden, inter, _ptr(out), _ptr(orow), _ptr(ws),
+                  ws_bytes, _stream())
     return out
 
 

@@ -24,6 +24,7 @@ class Context:
     idx_salient_row: Optional[torch.Tensor] = None   # int64 [n] (Q space)
     idx_salient_row_k: Optional[torch.Tensor] = None  # int64 [n] (K space) when Q-pruned, else None
     idx_salient_row_i32: Optional[torch.Tensor] = None  # int32 copy of idx_salient_row (kernel operand)
+    max_salientlen: int = 0                          # max salient rows of one sequence (0: unknown)
     idx_updated_row: Optional[torch.Tensor] = None
     total_seqlen_k: int = 0
     total_seqlen: int = 0

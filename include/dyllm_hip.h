@@ -155,8 +155,10 @@ int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t
 
 /* ---- FFN ------------------------------------------------------------------------------- */
 
-/* Bytes of the intermediate buffer dyllm_swiglu_ffn needs: rows * intermediate * 2. */
+/* Workspace of dyllm_swiglu_ffn: dyllm_swiglu_ffn_workspace_bytes (the [rows, intermediate]
+ * bf16 activations) + dyllm_ffn_down_workspace_bytes (split-K partials of the down GEMM). */
 size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate);
+size_t dyllm_ffn_down_workspace_bytes(int64_t rows, int hidden, int intermediate);
 
 /* Gathered SwiGLU FFN: for m < rows, a = x[rows_idx ? rows_idx[m] : m] (row stride ld_x),
  * h = silu(a W_g^T) * (a W_u^T), y = h W_d^T written to out[out_rows ? out_rows[m] : m]
@@ -171,7 +173,7 @@ int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64
 int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
                       int hidden, int intermediate, void* h_out, void* stream);
 int dyllm_ffn_down(const void* h, int64_t rows, const void* w_down, int hidden, int intermediate, void* out,
-                   const int64_t* out_rows, void* stream);
+                   const int64_t* out_rows, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- MoE ------------------------------------------------------------------------------- */
 

@@ -240,7 +240,8 @@ def test_attention_sparse_varlen(dev, q_pruned, H, Hkv):
 # ---------------------------------------------------------------------------------------
 # FFN / MoE
 # ---------------------------------------------------------------------------------------
-@pytest.mark.parametrize("M,hidden,inter", [(77, 256, 512), (300, 512, 384), (600, 256, 11008)])
+@pytest.mark.parametrize("M,hidden,inter", [(77, 256, 512), (300, 512, 384), (600, 256, 11008), (920, 4096, 1024),
+                                            (1500, 1024, 2048)])
 def test_swiglu_ffn_gathered(dev, M, hidden, inter):
     ops = _ops()
     g = _gen(M)
