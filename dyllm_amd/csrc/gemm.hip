@@ -18,12 +18,14 @@
 //                               partial tiles are summed in slice order by a reduction kernel
 //                               that applies the store epilogue (deterministic).
 //
-// Tiling: workgroup tile BM x 256 x 64, 8 wavefronts (2 per SIMD) in a 2 (M) x 4 (N) grid,
-// each wavefront (BM/2) x 64 of v_mfma_f32_32x32x16_bf16 tiles. Operands are staged through
+// Tiling: workgroup tile BM x 256 x 64, 8 wavefronts (2 per SIMD) in a 2 (M) x 4 (N) grid
+// (WGN = 4; a 2 x 2 grid of 1-wave-per-SIMD tiles measured slower), each wavefront (BM/2) x 64
+// of v_mfma_f32_32x32x16_bf16 tiles. Operands move global -> LDS with the gfx950 direct
+// LDS-load (global_load_lds_dwordx4), no register staging. Operands are staged through
 // LDS in two buffers of unpadded 128-byte rows whose 16-byte chunks are XOR-swizzled by row
-// (chunk ^ (row & 7)), so both the 16-byte stores and the fragment reads are spread over the
-// banks; the next K slice is fetched into registers while the current one is multiplied and
-// one barrier per K slice separates the buffers. The MFMA is issued as D = W_tile * A_tile^T
+// (chunk ^ (row & 7)), so the fragment reads are spread over the banks; the next K slice is
+// loaded into the other buffer while the current one is multiplied, and one wait + barrier
+// per K slice separates the buffers. The MFMA is issued as D = W_tile * A_tile^T
 // so that each lane owns one output row and four consecutive output columns per register
 // group: 8-byte stores and one row lookup per lane for the scatter. Workgroups are ordered
 // M-fastest and remapped XCD-major so the M tiles sharing a weight slice run on one XCD and
@@ -35,7 +37,6 @@ namespace dyllm {
 
 constexpr int kGemmBK = 64;
 constexpr int kGemmBN = 256;
-constexpr int kGemmThreads = 512;
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float bf16_rt(float x) { return __uint_as_float(uint32_t(f32_to_bf16(x)) << 16); }
@@ -43,11 +44,12 @@ __device__ __forceinline__ float bf16_rt(float x) { return __uint_as_float(uint3
 // element offset of (row, 16-byte chunk) in a swizzled 64-element-wide tile
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kGemmBK + ((chunk ^ (row & 7)) << 3); }
 
-template <int BM, GemmEpi EPI>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(GemmArgs g) {
+template <int BM, int WGN, GemmEpi EPI>
+__global__ __launch_bounds__(128 * WGN) void gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint16_t gsm[];
   constexpr int BN = kGemmBN;
-  constexpr int WM = BM / 2, WN = BN / 4;     // wave tile (rows of A, rows of W)
+  constexpr int NW = 2 * WGN;                 // wavefronts: 2 along M x WGN along N
+  constexpr int WM = BM / 2, WN = BN / WGN;   // wave tile (rows of A, rows of W)
   constexpr int TM = WM / 32, TN = WN / 32;   // 32x32 MFMA tiles per wave
   constexpr int BUF = (BM + BN) * kGemmBK;
 
@@ -66,6 +68,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w & 1, wn = w >> 1;
+  constexpr int GW = BN / (2 * WGN);          // SwiGLU: gate (and up) rows per wavefront
   const int l32 = lane & 31, half = lane >> 5;
 
   const uint16_t* Wb = g.W;
@@ -79,12 +82,12 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
   // of a block lands at byte 16*L, i.e. row L/8, physical chunk L%8, which holds logical
   // chunk (L%8) ^ (L/8). Rows outside the problem (m >= M, padding ids, n >= N) are clamped
   // to a valid row: their products are never stored.
-  constexpr int CA = BM / 64, CW = BN / 64;    // 1 KB blocks per wavefront per K slice
+  constexpr int CA = BM / (8 * NW), CW = BN / (8 * NW);  // 1 KB blocks per wavefront per K slice
   const int lrow = lane >> 3, lchunk = (lane & 7) ^ (lane >> 3);
   const uint16_t* a_src[CA];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
-    const int64_t m = m0 + (w + 8 * i) * 8 + lrow;
+    const int64_t m = m0 + (w + NW * i) * 8 + lrow;
     int64_t row = 0;
     if (m < M) {
       row = m;
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
   const uint16_t* w_src[CW];
 #pragma unroll
   for (int i = 0; i < CW; ++i) {
-    const int r = (w + 8 * i) * 8 + lrow;
+    const int r = (w + NW * i) * 8 + lrow;
     int64_t wrow;
     if constexpr (EPI == GemmEpi::SwiGLU)
       wrow = (r < BN / 2) ? int64_t(nt) * (BN / 2) + r : int64_t(g.half_n) + int64_t(nt) * (BN / 2) + (r - BN / 2);
@@ -116,17 +119,17 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
     for (int i = 0; i < CA; ++i)
       __builtin_amdgcn_global_load_lds((glb_void*)(a_src[i] + ko),
-                                       (lds_void*)(As + (w + 8 * i) * 8 * kGemmBK), 16, 0, 0);
+                                       (lds_void*)(As + (w + NW * i) * 8 * kGemmBK), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < CW; ++i)
       __builtin_amdgcn_global_load_lds((glb_void*)(w_src[i] + ko),
-                                       (lds_void*)(Ws + (w + 8 * i) * 8 * kGemmBK), 16, 0, 0);
+                                       (lds_void*)(Ws + (w + NW * i) * 8 * kGemmBK), 16, 0, 0);
   };
 
   // W-tile row base of the wave's n-subtile i
   auto wrow_base = [&](int i) -> int {
     if constexpr (EPI == GemmEpi::SwiGLU)
-      return (i < TN / 2) ? wn * (BN / 8) + 32 * i : BN / 2 + wn * (BN / 8) + 32 * (i - TN / 2);
+      return (i < TN / 2) ? wn * GW + 32 * i : BN / 2 + wn * GW + 32 * (i - TN / 2);
     else
       return wn * WN + 32 * i;
   };
@@ -214,7 +217,7 @@ __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2,
     if constexpr (EPI == GemmEpi::SwiGLU) {
 #pragma unroll
       for (int i = 0; i < TN / 2; ++i) {
-        const int hc0 = nt * (BN / 2) + wn * (BN / 8) + 32 * i + half * 4;
+        const int hc0 = nt * (BN / 2) + wn * GW + 32 * i + half * 4;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           float h[4];
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs g) {
 
 static constexpr size_t lds_bytes(int bm) { return size_t(2) * (bm + kGemmBN) * kGemmBK * sizeof(uint16_t); }
 
-template <int BM, GemmEpi EPI>
+template <int BM, int WGN, GemmEpi EPI>
 static int launch_gemm_cfg(const GemmArgs& g0, int64_t m_tiles, int ksplit, hipStream_t s) {
   GemmArgs g = g0;
   g.ksplit = ksplit;
@@ -295,12 +298,12 @@ static int launch_gemm_cfg(const GemmArgs& g0, int64_t m_tiles, int ksplit, hipS
   const size_t lds = lds_bytes(BM);
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, EPI>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, WGN, EPI>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
       return fail("hipFuncSetAttribute(max dynamic LDS) failed for the GEMM kernel");
     attr_set = true;
   }
-  gemm_kernel<BM, EPI><<<unsigned(nwg), kGemmThreads, lds, s>>>(g);
+  gemm_kernel<BM, WGN, EPI><<<unsigned(nwg), 128 * WGN, lds, s>>>(g);
   if (int rc = check_launch("gemm_kernel")) return rc;
   if (ksplit > 1) {
     const int64_t threads = m_tiles * BM * (g.N / 4);
@@ -367,13 +370,13 @@ int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, int
   if (epi == GemmEpi::SwiGLU) {
     DYLLM_REQUIRE(g.N == 2 * g.half_n, "SwiGLU weight must hold gate rows then up rows (N = 2 * intermediate)");
     DYLLM_REQUIRE(g.half_n % (kGemmBN / 2) == 0, "SwiGLU intermediate size must be a multiple of 128");
-    if (tile_m == 256) return launch_gemm_cfg<256, GemmEpi::SwiGLU>(g, mt, 1, s);
-    if (tile_m == 192) return launch_gemm_cfg<192, GemmEpi::SwiGLU>(g, mt, 1, s);
-    return launch_gemm_cfg<128, GemmEpi::SwiGLU>(g, mt, 1, s);
+    if (tile_m == 256) return launch_gemm_cfg<256, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
+    if (tile_m == 192) return launch_gemm_cfg<192, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
+    return launch_gemm_cfg<128, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
   }
-  if (tile_m == 256) return launch_gemm_cfg<256, GemmEpi::Store>(g, mt, ksplit, s);
-  if (tile_m == 192) return launch_gemm_cfg<192, GemmEpi::Store>(g, mt, ksplit, s);
-  return launch_gemm_cfg<128, GemmEpi::Store>(g, mt, ksplit, s);
+  if (tile_m == 256) return launch_gemm_cfg<256, 4, GemmEpi::Store>(g, mt, ksplit, s);
+  if (tile_m == 192) return launch_gemm_cfg<192, 4, GemmEpi::Store>(g, mt, ksplit, s);
+  return launch_gemm_cfg<128, 4, GemmEpi::Store>(g, mt, ksplit, s);
 }
 
 }  // namespace dyllm
