@@ -230,6 +230,8 @@ def main():
     avg_n = sum(n_sals) / len(n_sals)
     flops = 2.0 * avg_n * hid * 2 * inter
     avg_gate_ms = sum(gate_ms) / len(gate_ms)
+    from dyllm_amd import _lib
+    gate_bm = _lib.load().dyllm_ffn_tile_rows(int(round(avg_n)), 2 * inter, 1)
     achieved = flops / (avg_gate_ms * 1e-3) / 1e12
     print(f"[bench] {ms_per_step:.3f} ms/step, avg salient rows per layer {avg_n:.1f}, "
           f"gate_up {avg_gate_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)
@@ -259,7 +261,8 @@ def main():
                    "layers": layers, "batch": cfg["batch"], "seq_len": cfg["prompt"] + cfg["response"],
                    "response_len": cfg["response"], "hidden": hid, "heads": cfg["heads"], "ffn": inter,
                    "tau": cfg["tau"], "avg_salient_rows_per_layer": round(avg_n, 1)},
-        "roofline": {"kernel": "gemm_kernel<256,256,SwiGLU> (gathered gate_up + SiLU*up)", "bound": "mfma",
+        "roofline": {"kernel": f"gemm_kernel<{gate_bm},4,SwiGLU> (gathered gate_up + SiLU*up, tile {gate_bm}x256)",
+                     "bound": "mfma",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
                      "avg_launch_us": round(avg_gate_ms * 1e3, 2),

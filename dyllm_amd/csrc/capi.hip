@@ -333,6 +333,10 @@ size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate) {
   return align256(size_t(rows > 0 ? rows : 0) * size_t(intermediate) * 2);
 }
 
+int dyllm_ffn_tile_rows(int64_t rows, int n, int swiglu) {
+  return gemm_pick_tile(rows, n, swiglu ? GemmEpi::SwiGLU : GemmEpi::Store);
+}
+
 int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
                       int hidden, int intermediate, void* h_out, void* stream) {
   DYLLM_NONNULL(x);

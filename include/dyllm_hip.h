@@ -175,6 +175,9 @@ int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int6
 int dyllm_ffn_down(const void* h, int64_t rows, const void* w_down, int hidden, int intermediate, void* out,
                    const int64_t* out_rows, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Tile height (128/192/256) the FFN GEMMs use for `rows` rows and output width n. */
+int dyllm_ffn_tile_rows(int64_t rows, int n, int swiglu);
+
 /* ---- MoE ------------------------------------------------------------------------------- */
 
 /* Router: topk_weights (bf16) / topk_ids (int32) [tokens, top_k] from fp32 softmax of

@@ -1,0 +1,260 @@
+"""Pins the CPU oracle (oracle/dyllm_oracle.py) before it is trusted as the checker: against the
+reference's own known-answer test, against closed forms / library routines, against brute
+force on tiny inputs, and against invariants chosen so that a plausible mistake (dropped term,
+wrong sign or index, transposed operand, wrong rounding point) fails."""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import dyllm_oracle as ref
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+BF = torch.bfloat16
+
+
+def test_tau_known_answer_fixture():
+    """The reference's additive-shard cosine test (tests/test_parallelism.py:34-44)."""
+    with open(os.path.join(GOLDEN, "tau_known_answer.json")) as f:
+        fx = json.load(f)
+    stats = torch.tensor(fx["stats"], dtype=torch.float32)
+    assert ref.cosine_mask(stats, fx["threshold"]).tolist() == fx["expected_mask"]
+    # and it equals torch's cosine_similarity decision, as the reference test asserts
+    old, new = torch.tensor(fx["old"]), torch.tensor(fx["new"])
+    assert ref.cosine_mask(stats, fx["threshold"]).tolist() == (F.cosine_similarity(old, new, dim=-1) < 0.5).tolist()
+
+
+def test_cosine_mask_clamps_and_orientation():
+    # zero vectors: both norms clamp to 1e-8 -> cos = 0 -> salient for any positive tau
+    s = torch.tensor([[0.0, 0.0, 0.0], [4.0, 4.0, 4.0], [-1.0, 1.0, 1.0]])
+    assert ref.cosine_mask(s, 0.5).tolist() == [True, False, True]
+    # the test is strict: cos == tau is not salient
+    assert ref.cosine_mask(torch.tensor([[1.0, 1.0, 1.0]]), 1.0).tolist() == [False]
+
+
+def test_saliency_stats_closed_form():
+    g = torch.Generator().manual_seed(0)
+    a, b = torch.randn(7, 33, generator=g), torch.randn(7, 33, generator=g)
+    st = ref.saliency_stats(a, b)
+    torch.testing.assert_close(st[:, 0], (a * b).sum(-1), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(st[:, 1], (a * a).sum(-1), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(st[:, 2], (b * b).sum(-1), rtol=1e-5, atol=1e-5)
+    cos = ref.cosine_from_stats(st)
+    torch.testing.assert_close(cos.float(), F.cosine_similarity(a, b, dim=-1), rtol=1e-5, atol=1e-6)
+
+
+def _lens_case(seed, lens, H=4, Hkv=2, D=128):
+    g = torch.Generator().manual_seed(seed)
+    cu_q = np.concatenate([[0], np.cumsum([a for a, _ in lens])])
+    cu_k = np.concatenate([[0], np.cumsum([b for _, b in lens])])
+    q = torch.randn(int(cu_q[-1]), H, D, generator=g).to(BF)
+    k = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).to(BF)
+    v = torch.randn(int(cu_k[-1]), Hkv, D, generator=g).to(BF)
+    return q, k, v, cu_q, cu_k
+
+
+def test_flash_attention_matches_sdpa():
+    """Exact path equals torch's scaled_dot_product_attention per sequence (GQA expanded)."""
+    q, k, v, cu_q, cu_k = _lens_case(1, [(5, 70), (64, 64), (1, 130)])
+    out = ref.flash_attn_varlen(q, k, v, cu_q, cu_k, out_dtype=None, bf16_p=False)
+    for b in range(3):
+        qs, qe, ks, ke = cu_q[b], cu_q[b + 1], cu_k[b], cu_k[b + 1]
+        qb = q[qs:qe].float().transpose(0, 1)
+        kb = k[ks:ke].float().transpose(0, 1).repeat_interleave(2, 0)
+        vb = v[ks:ke].float().transpose(0, 1).repeat_interleave(2, 0)
+        want = F.scaled_dot_product_attention(qb, kb, vb).transpose(0, 1)
+        torch.testing.assert_close(out[qs:qe], want, rtol=1e-4, atol=1e-5)
+    # head h uses kv head h // 2: swapping kv heads changes the answer
+    out2 = ref.flash_attn_varlen(q, k.flip(1), v.flip(1), cu_q, cu_k, out_dtype=None, bf16_p=False)
+    assert (out2 - out).abs().max() > 1e-2
+
+
+def test_blocked_bf16_softmax_close_to_exact_and_blockwise():
+    q, k, v, cu_q, cu_k = _lens_case(2, [(16, 200)], H=2, Hkv=2)
+    exact = ref.flash_attn_varlen(q, k, v, cu_q, cu_k, out_dtype=None, bf16_p=False)
+    blocked = ref.flash_attn_varlen(q, k, v, cu_q, cu_k, out_dtype=None, bf16_p=True)
+    rel = ((blocked - exact).abs().mean() / exact.abs().mean()).item()
+    assert 0 < rel < 4e-3  # bf16 rounding of P is visible but small
+    # the running-max blocking matters: rounding relative to the final max differs
+    c2 = float(np.float32(np.float32(128 ** -0.5) * np.float32(ref.LOG2E)))
+    qb, kb, vb = (t.float().transpose(0, 1) for t in (q, k, v))
+    acc, l = ref._online_softmax_pv(qb, kb, vb, c2, 200)  # one block = final-max rounding
+    assert not torch.equal((acc / l).transpose(0, 1), blocked)
+
+
+def test_column_sparse_linearity_invariant():
+    """C_old = attn(Q,K,V_old); dV = V_new - V_old on salient keys only; then
+    C_old + softmax(QK^T/sqrt(D)) dV == attn(Q,K,V_new) for every row (the identity the
+    reference's approximation rests on, attention.py:89-139)."""
+    lens = [(40, 96), (20, 64)]
+    q, k, v_old, cu_q, cu_k = _lens_case(3, lens, H=4, Hkv=4)
+    g = torch.Generator().manual_seed(9)
+    sal_k = np.array([3, 50, 95, 96 + 7, 96 + 33])
+    v_new = v_old.clone()
+    v_new[sal_k] = (v_old[sal_k].float() + torch.randn(len(sal_k), 4, 128, generator=g)).to(BF)
+    dv = torch.zeros_like(v_old, dtype=torch.float32)
+    dv[sal_k] = v_new[sal_k].float() - v_old[sal_k].float()
+    c_old = ref.flash_attn_varlen(q, k, v_old, cu_q, cu_k, out_dtype=None, bf16_p=False)
+    want = ref.flash_attn_varlen(q, k, v_new, cu_q, cu_k, out_dtype=None, bf16_p=False)
+    o, stats, _ = ref.attention_sparse_varlen(q, k, dv, c_old, torch.zeros(0, 4, 128), cu_q, cu_k, [], 0.99)
+    # o is bf16-rounded; the dV term carries the bf16 rounding of P
+    assert (o.float() - want).abs().max().item() < 2e-2
+    # stats are the closed form of the fp32 new rows vs C_old
+    torch.testing.assert_close(ref.cosine_from_stats(stats).float(),
+                               F.cosine_similarity(want.reshape(len(want), -1), c_old.reshape(len(want), -1), dim=-1),
+                               rtol=1e-4, atol=1e-4)
+    # dropping the dV term (or flipping its sign) breaks the identity
+    o0, _, _ = ref.attention_sparse_varlen(q, k, torch.zeros_like(dv), c_old, torch.zeros(0, 4, 128), cu_q, cu_k,
+                                           [], 0.99)
+    assert (o0.float() - want).abs().max().item() > 5e-2
+
+
+def test_column_sparse_salient_rows_take_o_sal():
+    q, k, v, cu_q, cu_k = _lens_case(4, [(10, 40)], H=2, Hkv=2)
+    c = ref.flash_attn_varlen(q, k, v, cu_q, cu_k)
+    o_sal = torch.randn(2, 2, 128).to(BF)
+    idx = [2, 7]
+    o, st, m = ref.attention_sparse_varlen(q, k, torch.zeros_like(k), c, o_sal, cu_q, cu_k, idx, 0.99)
+    assert torch.equal(o[idx], o_sal)
+    # stats of salient rows come from bf16 o_sal vs C (attention_aux_kernels.cu:33-42)
+    torch.testing.assert_close(st[idx], ref.saliency_stats(o_sal.float(), c[idx].float()))
+    # unchanged rows: new == old -> cos == 1 -> not salient; random o_sal rows -> salient
+    others = [i for i in range(10) if i not in idx]
+    assert not m[others].any() and m[idx].all()
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_compaction_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    T = int(rng.integers(0, 60))
+    B = int(rng.integers(1, 5))
+    mask = rng.random(T) < rng.random()
+    cuts = np.sort(rng.integers(0, T + 1, size=B - 1))
+    cu_q = np.concatenate([[0], cuts, [T]])
+    cu_p = np.concatenate([[0], np.cumsum(rng.integers(0, 9, size=B))])
+    idxs, cu = ref.compact(mask, cu_q)
+    want = [t for t in range(T) if mask[t]]
+    assert idxs.tolist() == want
+    assert all(idxs[i] < idxs[i + 1] for i in range(len(idxs) - 1))
+    assert cu.tolist() == [sum(1 for t in want if t < c) for c in cu_q]
+    # per-sequence counts add up and every index lies in its sequence
+    for b in range(B):
+        for t in idxs[cu[b]:cu[b + 1]]:
+            assert cu_q[b] <= t < cu_q[b + 1]
+    # fused_offset: K-space row = Q-space index + prompt rows of all sequences up to and including its own
+    k = ref.fused_offset(idxs, cu_p, cu)
+    for j, t in enumerate(idxs):
+        b = max(i for i in range(B) if cu[i] <= j < cu[i + 1]) if cu[-1] else 0
+        assert k[j] == t + cu_p[b + 1]
+
+
+def test_k_block_masks_brute_force():
+    cu_k = [0, 100, 130]
+    cu_s = [0, 3, 4]
+    idx = [0, 63, 64, 129]
+    m = ref.k_block_masks(idx, cu_s, cu_k, 100)
+    assert m.shape == (2, 2)
+    assert int(m[0, 0]) == (1 | (1 << 63)) and int(m[0, 1]) == 1 and int(m[1, 0]) == (1 << 29) and int(m[1, 1]) == 0
+
+
+def test_cache_ops_round_trips():
+    g = torch.Generator().manual_seed(5)
+    cache = torch.randn(60, 8, generator=g)
+    starts = torch.tensor([-1, 40, 2, -1, 17], dtype=torch.long)
+    ids = torch.tensor([2, 4, 1])
+    cu_k = [0, 10, 22, 30]
+    cu_q = [0, 4, 10, 12]
+    x = torch.randn(30, 8, generator=g)
+    c2 = ref.reset_full(cache, x, starts, cu_k, ids)
+    assert torch.equal(ref.get_seqs(c2, starts, cu_k, ids, 30), x)
+    assert torch.equal(c2[2:12], x[0:10]) and torch.equal(c2[17:29], x[10:22]) and torch.equal(c2[40:48], x[22:30])
+    xq = torch.randn(12, 8, generator=g)
+    c3 = ref.reset_block(cache, xq, starts, cu_k, cu_q, ids)
+    assert torch.equal(ref.get_block(c3, starts, cu_k, cu_q, ids, 12), xq)
+    assert torch.equal(c3[2 + 6:12], xq[0:4])  # tail 4 rows of a 10-row sequence
+    nv = torch.randn(2, 8, generator=g)
+    c4 = ref.scatter_update(cache, nv, [9, 22], cu_k, starts, ids)
+    assert torch.equal(c4[2 + 9], nv[0]) and torch.equal(c4[40], nv[1])
+    assert torch.equal(ref.gather_rows_2D(cache, [3, 1]), cache[[3, 1]])
+
+
+def test_swiglu_matches_per_row_loop():
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(5, 16, generator=g).to(BF)
+    wgu = (torch.randn(24, 16, generator=g) * 0.3).to(BF)
+    wd = (torch.randn(16, 12, generator=g) * 0.3).to(BF)
+    y = ref.swiglu_ffn(x, wgu, wd)
+    for r in range(5):
+        gate = ref.bf16_round(x[r].float() @ wgu[:12].float().t())
+        up = ref.bf16_round(x[r].float() @ wgu[12:].float().t())
+        h = ref.bf16_round(gate * torch.sigmoid(gate) * up)
+        torch.testing.assert_close(y[r], h @ wd.float().t(), rtol=1e-5, atol=1e-5)
+    # swapping the gate and up halves changes the result (silu is not symmetric)
+    y2 = ref.swiglu_ffn(x, torch.cat([wgu[12:], wgu[:12]]), wd)
+    assert (y2 - y).abs().max() > 1e-3
+
+
+def test_moe_gate_and_experts_brute_force():
+    g = torch.Generator().manual_seed(7)
+    T, Hd, E, K, I = 6, 16, 8, 3, 4
+    x = torch.randn(T, Hd, generator=g).to(BF)
+    wr = torch.randn(E, Hd, generator=g).to(BF)
+    w, ids = ref.moe_gate(x, wr, K)
+    w1 = (torch.randn(E, 2 * I, Hd, generator=g) * 0.3).to(BF)
+    w2 = (torch.randn(E, Hd, I, generator=g) * 0.3).to(BF)
+    out = ref.naive_experts(x, w1, w2, w, ids)
+    for t in range(T):
+        logits = [float((x[t].float() * wr[e].float()).sum()) for e in range(E)]
+        mx = max(logits)
+        ex = [math.exp(l - mx) for l in logits]
+        p = [a / sum(ex) for a in ex]
+        top = sorted(range(E), key=lambda e: -p[e])[:K]
+        assert ids[t].tolist() == top
+        torch.testing.assert_close(w[t].float(), torch.tensor([p[e] for e in top]).to(BF).float())
+        acc = torch.zeros(Hd)
+        for kk, e in enumerate(top):
+            gu = ref.bf16_round(x[t].float() @ w1[e].float().t())
+            h = ref.bf16_round(F.silu(gu[:I]) * gu[I:])
+            acc += ref.bf16_round((h @ w2[e].float().t()) * w[t, kk].float())
+        torch.testing.assert_close(out[t], acc, rtol=1e-5, atol=1e-5)
+    wn, _ = ref.moe_gate(x, wr, K, renormalize=True)
+    torch.testing.assert_close(wn.float().sum(-1), torch.ones(T), rtol=1e-2, atol=1e-2)
+
+
+def test_moe_align_invariants():
+    rng = np.random.default_rng(8)
+    ids = rng.integers(0, 5, size=(11, 3))
+    sorted_ids, eids, npp = ref.moe_align_block_size(ids, 4, 5)
+    S = ids.size
+    assert npp % 4 == 0 and len(sorted_ids) == npp and len(eids) == npp // 4
+    real = sorted_ids[sorted_ids < S]
+    assert sorted(real.tolist()) == list(range(S))  # a permutation of all slots
+    flat = ids.reshape(-1)
+    for blk, e in enumerate(eids):
+        for s in sorted_ids[4 * blk:4 * blk + 4]:
+            if s < S:
+                assert flat[s] == e  # each block is owned by one expert
+    # stable: within an expert the slots keep their flattened order
+    for e in range(5):
+        own = [s for s in sorted_ids if s < S and flat[s] == e]
+        assert own == sorted(own)
+
+
+def test_synthetic_perturbation_known_answer():
+    """Config-0 style: unperturbed rows keep cos == 1; rows perturbed with sigma = 0.5 x row
+    RMS have cos ~ 1/sqrt(1.25) = 0.894 < 0.99, so the salient set is the perturbed set."""
+    g = torch.Generator().manual_seed(10)
+    old = torch.randn(64, 4096, generator=g)
+    new = old.clone()
+    pert = torch.tensor(sorted(torch.randperm(64, generator=g)[:7].tolist()))
+    rms = old[pert].pow(2).mean(-1, keepdim=True).sqrt()
+    new[pert] += 0.5 * rms * torch.randn(7, 4096, generator=g)
+    st = ref.saliency_stats(new, old)
+    mask = ref.cosine_mask(st, 0.99)
+    assert torch.nonzero(mask).squeeze(-1).tolist() == pert.tolist()
+    cos = ref.cosine_from_stats(st)[pert]
+    assert ((cos - 1 / math.sqrt(1.25)).abs() < 0.02).all()
