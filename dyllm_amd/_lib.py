@@ -26,6 +26,10 @@ SIGNATURES = {
     "dyllm_attention_colsparse_workspace_bytes": [_I, _I, _L, _L, _I],
     "dyllm_attention_colsparse_cached": [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _L,
                                          _L, _I, _P, _P, _P, _P, c_float, _P, c_size_t, _P],
+    "dyllm_sparse_step_workspace_bytes": [_I, _I, _I, _I, _L, _L, _I, _L],
+    "dyllm_sparse_attention_step": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I, _L, _L,
+                                    _I, _I, _P, _P, _P, _P, c_float, c_float, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                    _P, c_size_t, _P],
     "dyllm_v_delta_update": [_P, _P, _P, _L, _L, _P, _P],
     "dyllm_seq_row_starts": [_P, _P, _P, _P, _I, _P, _P],
     "dyllm_cosine_mask": [_P, _L, c_float, _P, _P],
@@ -37,14 +41,14 @@ SIGNATURES = {
     "dyllm_reset_full": [_P, _P, _L, _P, _P, _P, _I, _L, _P],
     "dyllm_reset_block": [_P, _P, _L, _P, _P, _P, _P, _I, _L, _P],
     "dyllm_scatter_update": [_P, _P, _L, _P, _L, _P, _P, _P, _I, _P],
-    "dyllm_scatter_dest_rows": [_P, _L, _P, _P, _P, _I, _P, _P],
+    "dyllm_scatter_dest_rows": [_P, _L, _P, _P, _P, _P, _I, _P, _P],
     "dyllm_gather_rows": [_P, _P, _L, _P, _L, _P],
     "dyllm_swiglu_ffn_workspace_bytes": [_L, _I],
     "dyllm_swiglu_ffn": [_P, _L, _P, _L, _P, _P, _I, _I, _P, c_size_t, _P, _P, _P],
     "dyllm_ffn_tile_rows": [_L, _I, _I],
-    "dyllm_ffn_gate_up": [_P, _L, _P, _L, _P, _I, _I, _P, _P],
-    "dyllm_ffn_down": [_P, _L, _P, _I, _I, _P, _P, _P, c_size_t, _P],
-    "dyllm_ffn_down_workspace_bytes": [_L, _I, _I],
+    "dyllm_ffn_gate_up": [_P, _L, _P, _L, _P, _L, _P, _I, _I, _P, _P],
+    "dyllm_ffn_down": [_P, _L, _P, _L, _P, _I, _I, _P, _P, _P, c_size_t, _P],
+    "dyllm_ffn_down_workspace_bytes": [_L, _L, _I, _I],
     "dyllm_moe_gate": [_P, _P, _L, _I, _P, _I, _I, _I, _P, _P, _P],
     "dyllm_moe_align_block_size": [_P, _L, _I, _I, _P, _L, _P, _P, _P],
     "dyllm_fused_experts_workspace_bytes": [_L, _I, _I, _I, _I],
@@ -56,6 +60,7 @@ _RET = {
     "dyllm_ffn_tile_rows": c_int,
     "dyllm_attention_sparse_workspace_bytes": c_size_t,
     "dyllm_attention_colsparse_workspace_bytes": c_size_t,
+    "dyllm_sparse_step_workspace_bytes": c_size_t,
     "dyllm_swiglu_ffn_workspace_bytes": c_size_t,
     "dyllm_ffn_down_workspace_bytes": c_size_t,
     "dyllm_fused_experts_workspace_bytes": c_size_t,

@@ -98,7 +98,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const float c2 = a.scale_log2;
 
   const uint16_t* Kb = a.K + kv0 * ldkv + kvh * kD;
-  const uint16_t* Vb = a.V + (a.kslot ? 0 : kv0) * ldkv + kvh * kD;
+  const int64_t v0 = a.kslot ? 0 : (a.v_start ? a.v_start[b] : kv0);
+  const uint16_t* Vb = a.V + v0 * ldkv + kvh * kD;
   const int32_t* ks_b = a.kslot ? a.kslot + k_beg : nullptr;
   const int nkb = (Lk + kBK - 1) / kBK;
 

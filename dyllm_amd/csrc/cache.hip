@@ -97,21 +97,22 @@ int launch_row_map(RowMap mode, const RowMapArgs& a, hipStream_t stream) {
 // Destination cache row of each packed row index (the address computation of
 // scatter_update, cache_kernels.cu:397-419), so a GEMM epilogue can scatter in place.
 __global__ __launch_bounds__(256) void scatter_dest_rows_kernel(const int64_t* __restrict__ row_idx, int64_t M,
+                                                                const int32_t* __restrict__ m_dev,
                                                                 const int32_t* __restrict__ cu,
                                                                 const int64_t* __restrict__ seq_starts,
                                                                 const int64_t* __restrict__ seq_ids, int B,
                                                                 int64_t* __restrict__ dest) {
   const int64_t m = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (m >= M) return;
+  if (m >= M || (m_dev && m >= m_dev[0])) return;
   const int64_t k = row_idx[m];
   const int b = find_segment(cu, B + 1, k);
   dest[m] = seq_starts[seq_ids[b]] + (k - cu[b]);
 }
 
-int launch_scatter_dest_rows(const int64_t* row_idx, int64_t M, const int32_t* cu, const int64_t* seq_starts,
-                             const int64_t* seq_ids, int B, int64_t* dest, hipStream_t s) {
+int launch_scatter_dest_rows(const int64_t* row_idx, int64_t M, const int32_t* m_dev, const int32_t* cu,
+                             const int64_t* seq_starts, const int64_t* seq_ids, int B, int64_t* dest, hipStream_t s) {
   if (M <= 0) return 0;
-  scatter_dest_rows_kernel<<<unsigned(cdiv(M, 256)), 256, 0, s>>>(row_idx, M, cu, seq_starts, seq_ids, B, dest);
+  scatter_dest_rows_kernel<<<unsigned(cdiv(M, 256)), 256, 0, s>>>(row_idx, M, m_dev, cu, seq_starts, seq_ids, B, dest);
   return check_launch("scatter_dest_rows_kernel");
 }
 

@@ -150,6 +150,98 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
                         workspace, workspace_bytes, true, stream);
 }
 
+size_t dyllm_sparse_step_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim, int64_t total_q,
+                                         int64_t total_k, int max_seqlen_k, int64_t num_salient) {
+  const size_t n = size_t(num_salient > 0 ? num_salient : 0);
+  return align256(n * 8) + align256(n * num_kv_heads * head_dim * 2) + align256(n * num_heads * head_dim * 2) +
+         2 * align256(size_t(batch) * 8) +
+         dyllm_attention_colsparse_workspace_bytes(batch, num_heads, total_q, total_k, max_seqlen_k);
+}
+
+int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_start, void* v_cache,
+                                const int64_t* v_seq_starts, const void* v_new, void* c_cache,
+                                const int64_t* c_seq_starts, const int64_t* seq_ids, int batch, int num_heads,
+                                int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
+                                const int32_t* cu_seqlens_k, const int32_t* cu_promptlens, int max_seqlen_q,
+                                int max_seqlen_k, int64_t total_q, int64_t total_k, int num_salient,
+                                int max_salientlen, const int32_t* cu_salientlens, const int32_t* idx_q32,
+                                const int64_t* idx_k64, const int32_t* idx_k32, float softmax_scale, float threshold,
+                                void* out, float* cosine_stats, uint8_t* cosine_out, int64_t* next_idx64,
+                                int32_t* next_idx32, int64_t* next_idx_k64, int32_t* next_idx_k32,
+                                int32_t* next_cu_salientlens, int32_t* next_count, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  DYLLM_NONNULL(v_cache);
+  DYLLM_NONNULL(v_seq_starts);
+  DYLLM_NONNULL(c_seq_starts);
+  DYLLM_NONNULL(seq_ids);
+  DYLLM_NONNULL(next_idx64);
+  DYLLM_NONNULL(next_cu_salientlens);
+  DYLLM_NONNULL(next_count);
+  DYLLM_REQUIRE(num_salient >= 0, "num_salient must be non-negative");
+  DYLLM_REQUIRE(num_salient == 0 || (v_new && cu_salientlens && idx_q32 && idx_k64 && idx_k32),
+                "salient rows need v_new, cu_salientlens and the Q/K index lists");
+  DYLLM_REQUIRE(cu_promptlens == nullptr || next_idx_k64 != nullptr, "Q-pruned steps need next_idx_k64");
+  const size_t need = dyllm_sparse_step_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, total_q, total_k,
+                                                        max_seqlen_k, num_salient);
+  DYLLM_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need " + std::to_string(need) + " bytes");
+  const hipStream_t s = DYLLM_STREAM(stream);
+  const size_t n = size_t(num_salient);
+  char* ws = static_cast<char*>(workspace);
+  int64_t* dest = reinterpret_cast<int64_t*>(ws);
+  ws += align256(n * 8);
+  uint16_t* dv = reinterpret_cast<uint16_t*>(ws);
+  ws += align256(n * num_kv_heads * head_dim * 2);
+  uint16_t* o_sal = reinterpret_cast<uint16_t*>(ws);
+  ws += align256(n * num_heads * head_dim * 2);
+  int64_t* v_start = reinterpret_cast<int64_t*>(ws);
+  ws += align256(size_t(batch) * 8);
+  int64_t* c_start = reinterpret_cast<int64_t*>(ws);
+  ws += align256(size_t(batch) * 8);
+  const size_t cs_bytes = workspace_bytes - size_t(ws - static_cast<char*>(workspace));
+  const bool q_pruned = cu_promptlens != nullptr;
+
+  if (num_salient > 0) {
+    // dV of the salient keys + V-cache update (attention.py:67-74, 89-96)
+    if (int rc = launch_scatter_dest_rows(idx_k64, num_salient, nullptr, cu_seqlens_k, v_seq_starts, seq_ids, batch,
+                                          dest, s))
+      return rc;
+    if (int rc = launch_v_delta_update(static_cast<uint16_t*>(v_cache), static_cast<const uint16_t*>(v_new), dest,
+                                       num_salient, int64_t(num_kv_heads) * head_dim, dv, s))
+      return rc;
+    // row-sparse attention of the salient queries vs the full cached K/V (attention.py:76-87)
+    if (int rc = launch_seq_row_starts(v_seq_starts, seq_ids, cu_seqlens_k, nullptr, batch, v_start, s)) return rc;
+    AttnArgs a{};
+    a.Q = static_cast<const uint16_t*>(q);
+    a.K = static_cast<const uint16_t*>(k);
+    a.V = static_cast<const uint16_t*>(v_cache);
+    a.O = o_sal;
+    a.cu_rows = cu_salientlens;
+    a.cu_k = cu_seqlens_k;
+    a.kv_start = k_start;
+    a.v_start = v_start;
+    a.q_rows = idx_q32;
+    a.B = batch;
+    a.H = num_heads;
+    a.Hkv = num_kv_heads;
+    a.scale_log2 = softmax_scale * kLog2e;
+    if (int rc = launch_attention(AttnMode::RowSparse, a, max_salientlen > 0 ? max_salientlen : max_seqlen_q, s))
+      return rc;
+  }
+  // column-sparse attention + statistics + tau test, context cache updated in place
+  if (int rc = launch_seq_row_starts(c_seq_starts, seq_ids, cu_seqlens_k, q_pruned ? cu_seqlens_q : nullptr, batch,
+                                     c_start, s))
+    return rc;
+  if (int rc = colsparse_impl(q, k, k_start, num_salient ? dv : nullptr, c_cache, c_start, 1, o_sal, out, batch,
+                              num_heads, num_kv_heads, head_dim, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                              max_seqlen_k, total_q, total_k, num_salient, idx_q32, idx_k32, cosine_stats,
+                              cosine_out, threshold, ws, cs_bytes, true, stream))
+    return rc;
+  // compaction of the next salient set (attention.py:147-173)
+  return launch_compact(cosine_out, total_q, cu_seqlens_q, batch, cu_promptlens, next_idx64, next_idx32,
+                        q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr, next_cu_salientlens,
+                        next_count, s);
+}
+
 int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,
                          int64_t row_elems, void* dv_out, void* stream) {
   DYLLM_REQUIRE(rows == 0 || (v_cache && v_new && dest_rows && dv_out), "null pointer argument");
@@ -221,8 +313,8 @@ int dyllm_salient_compact(const uint8_t* mask, int64_t rows, const int32_t* cu_s
   DYLLM_NONNULL(idx64);
   DYLLM_NONNULL(cu_salientlens);
   DYLLM_NONNULL(count);
-  return launch_compact(mask, rows, cu_seqlens_q, batch, cu_promptlens, idx64, idx32, idx_k, cu_salientlens, count,
-                        DYLLM_STREAM(stream));
+  return launch_compact(mask, rows, cu_seqlens_q, batch, cu_promptlens, idx64, idx32, idx_k, nullptr, cu_salientlens,
+                        count, DYLLM_STREAM(stream));
 }
 
 int dyllm_fused_offset_launch(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_promptlens,
@@ -306,16 +398,17 @@ int dyllm_scatter_update(void* cache, const void* new_vals, int64_t row_bytes, c
   return row_map(RowMap::Scatter, new_vals, cache, row_bytes, rows, seq_starts, cu_seqlens, nullptr, seq_ids, row_idx,
                  batch, stream);
 }
-int dyllm_scatter_dest_rows(const int64_t* row_idx, int64_t rows, const int32_t* cu_seqlens,
-                            const int64_t* seq_starts, const int64_t* seq_ids, int batch, int64_t* dest,
-                            void* stream) {
+int dyllm_scatter_dest_rows(const int64_t* row_idx, int64_t rows, const int32_t* rows_dev,
+                            const int32_t* cu_seqlens, const int64_t* seq_starts, const int64_t* seq_ids, int batch,
+                            int64_t* dest, void* stream) {
   DYLLM_NONNULL(row_idx);
   DYLLM_NONNULL(cu_seqlens);
   DYLLM_NONNULL(seq_starts);
   DYLLM_NONNULL(seq_ids);
   DYLLM_NONNULL(dest);
   DYLLM_REQUIRE(batch >= 1, "batch must be >= 1");
-  return launch_scatter_dest_rows(row_idx, rows, cu_seqlens, seq_starts, seq_ids, batch, dest, DYLLM_STREAM(stream));
+  return launch_scatter_dest_rows(row_idx, rows, rows_dev, cu_seqlens, seq_starts, seq_ids, batch, dest,
+                                  DYLLM_STREAM(stream));
 }
 int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t* idx, int64_t rows, void* stream) {
   DYLLM_NONNULL(idx);
@@ -323,10 +416,13 @@ int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t
 }
 
 // ---------------------------------------------------------------------------------------
-size_t dyllm_ffn_down_workspace_bytes(int64_t rows, int hidden, int intermediate) {
+static int64_t hint_or(int64_t hint, int64_t rows) { return (hint > 0 && hint < rows) ? hint : rows; }
+
+size_t dyllm_ffn_down_workspace_bytes(int64_t rows, int64_t rows_hint, int hidden, int intermediate) {
   if (rows <= 0) return 0;
-  const int tm = gemm_pick_tile(rows, hidden, GemmEpi::Store);
-  return align256(gemm_partial_bytes(rows, hidden, tm, gemm_pick_ksplit(rows, hidden, intermediate, tm)));
+  const int64_t h = hint_or(rows_hint, rows);
+  const int tm = gemm_pick_tile(h, hidden, GemmEpi::Store);
+  return align256(gemm_partial_bytes(rows, hidden, tm, gemm_pick_ksplit(h, hidden, intermediate, tm)));
 }
 
 size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate) {
@@ -337,8 +433,9 @@ int dyllm_ffn_tile_rows(int64_t rows, int n, int swiglu) {
   return gemm_pick_tile(rows, n, swiglu ? GemmEpi::SwiGLU : GemmEpi::Store);
 }
 
-int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
-                      int hidden, int intermediate, void* h_out, void* stream) {
+int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const int32_t* rows_dev,
+                      int64_t rows_hint, const void* w_gate_up, int hidden, int intermediate, void* h_out,
+                      void* stream) {
   DYLLM_NONNULL(x);
   DYLLM_NONNULL(w_gate_up);
   DYLLM_NONNULL(h_out);
@@ -356,14 +453,17 @@ int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int6
   g.Cout = static_cast<uint16_t*>(h_out);
   g.ldc = intermediate;
   g.M = rows;
+  g.num_m_dev = rows_dev;
   g.N = 2 * intermediate;
   g.K = hidden;
   g.half_n = intermediate;
-  return launch_gemm(GemmEpi::SwiGLU, g, rows, 0, 1, DYLLM_STREAM(stream));
+  const int tm = gemm_pick_tile(hint_or(rows_hint, rows), g.N, GemmEpi::SwiGLU);
+  return launch_gemm(GemmEpi::SwiGLU, g, rows, tm, 1, DYLLM_STREAM(stream));
 }
 
-int dyllm_ffn_down(const void* h, int64_t rows, const void* w_down, int hidden, int intermediate, void* out,
-                   const int64_t* out_rows, void* workspace, size_t workspace_bytes, void* stream) {
+int dyllm_ffn_down(const void* h, int64_t rows, const int32_t* rows_dev, int64_t rows_hint, const void* w_down,
+                   int hidden, int intermediate, void* out, const int64_t* out_rows, void* workspace,
+                   size_t workspace_bytes, void* stream) {
   DYLLM_NONNULL(h);
   DYLLM_NONNULL(w_down);
   DYLLM_NONNULL(out);
@@ -381,10 +481,12 @@ int dyllm_ffn_down(const void* h, int64_t rows, const void* w_down, int hidden, 
   d.ldc = hidden;
   d.c_rows = out_rows;
   d.M = rows;
+  d.num_m_dev = rows_dev;
   d.N = hidden;
   d.K = intermediate;
-  const int tm = gemm_pick_tile(rows, hidden, GemmEpi::Store);
-  const int ks = gemm_pick_ksplit(rows, hidden, intermediate, tm);
+  const int64_t hr = hint_or(rows_hint, rows);
+  const int tm = gemm_pick_tile(hr, hidden, GemmEpi::Store);
+  const int ks = gemm_pick_ksplit(hr, hidden, intermediate, tm);
   if (ks > 1) {
     const size_t need = gemm_partial_bytes(rows, hidden, tm, ks);
     DYLLM_REQUIRE(workspace && workspace_bytes >= need,
@@ -399,12 +501,13 @@ int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64
                      void* out, const int64_t* out_rows, void* stream) {
   if (rows <= 0) return 0;
   const size_t hb = dyllm_swiglu_ffn_workspace_bytes(rows, intermediate);
-  const size_t db = dyllm_ffn_down_workspace_bytes(rows, hidden, intermediate);
+  const size_t db = dyllm_ffn_down_workspace_bytes(rows, 0, hidden, intermediate);
   DYLLM_REQUIRE(workspace && workspace_bytes >= hb + db,
                 "workspace too small: need " + std::to_string(hb + db) + " bytes");
-  if (int rc = dyllm_ffn_gate_up(x, ld_x, rows_idx, rows, w_gate_up, hidden, intermediate, workspace, stream))
+  if (int rc = dyllm_ffn_gate_up(x, ld_x, rows_idx, rows, nullptr, 0, w_gate_up, hidden, intermediate, workspace,
+                                 stream))
     return rc;
-  return dyllm_ffn_down(workspace, rows, w_down, hidden, intermediate, out, out_rows,
+  return dyllm_ffn_down(workspace, rows, nullptr, 0, w_down, hidden, intermediate, out, out_rows,
                         static_cast<char*>(workspace) + hb, db, stream);
 }
 

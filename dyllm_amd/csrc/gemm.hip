@@ -44,27 +44,16 @@ __device__ __forceinline__ float bf16_rt(float x) { return __uint_as_float(uint3
 // element offset of (row, 16-byte chunk) in a swizzled 64-element-wide tile
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kGemmBK + ((chunk ^ (row & 7)) << 3); }
 
+// One BM x 256 output tile (K slice kz of ksplit).
 template <int BM, int WGN, GemmEpi EPI>
-__global__ __launch_bounds__(128 * WGN) void gemm_kernel(GemmArgs g) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, int nt, int kz) {
   extern __shared__ __attribute__((aligned(16))) uint16_t gsm[];
   constexpr int BN = kGemmBN;
   constexpr int NW = 2 * WGN;                 // wavefronts: 2 along M x WGN along N
   constexpr int WM = BM / 2, WN = BN / WGN;   // wave tile (rows of A, rows of W)
   constexpr int TM = WM / 32, TN = WN / 32;   // 32x32 MFMA tiles per wave
   constexpr int BUF = (BM + BN) * kGemmBK;
-
-  const int64_t M = g.num_m_dev ? int64_t(g.num_m_dev[0]) : g.M;
-  const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (BN / 2)) : int(cdiv(g.N, BN));
-  const int nwg = gridDim.x;
-  int wg = blockIdx.x;
-  if ((nwg & 7) == 0) wg = (wg & 7) * (nwg >> 3) + (wg >> 3);
-  const int per_split = nwg / g.ksplit;
-  const int kz = wg / per_split;
-  wg -= kz * per_split;
-  const int m_tiles_launched = per_split / n_tiles;
-  const int mt = wg % m_tiles_launched, nt = wg / m_tiles_launched;
   const int64_t m0 = int64_t(mt) * BM;
-  if (m0 >= M) return;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int wm = w & 1, wn = w >> 1;
@@ -251,37 +240,80 @@ __global__ __launch_bounds__(128 * WGN) void gemm_kernel(GemmArgs g) {
   }
 }
 
+// Persistent launch: one workgroup per CU loops over the output tiles. The number of tiles can
+// come from device memory (num_m_dev: the salient count written by the compaction kernel), so
+// the GEMM is enqueued without the host knowing M. Tiles are split into 8 contiguous ranges,
+// one per XCD (workgroup b runs on XCD b % 8), ordered split-K slice > N tile > M tile, so the
+// M tiles that share a weight slice run together on one XCD and read it from HBM once.
+template <int BM, int WGN, GemmEpi EPI>
+__global__ __launch_bounds__(128 * WGN) void gemm_kernel(GemmArgs g) {
+  const int64_t M = g.num_m_dev ? int64_t(g.num_m_dev[0]) : g.M;
+  const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (kGemmBN / 2)) : int(cdiv(g.N, kGemmBN));
+  const int mtr = int(cdiv(M, BM));
+  const int64_t total = int64_t(mtr) * n_tiles * g.ksplit;
+  const int P = gridDim.x;
+  int64_t t, t_end, stride;
+  if ((P & 7) == 0) {
+    const int x = blockIdx.x & 7, local = blockIdx.x >> 3;
+    const int64_t lo = total * x / 8, hi = total * (x + 1) / 8;
+    t = lo + local;
+    t_end = hi;
+    stride = P >> 3;
+  } else {
+    t = blockIdx.x;
+    t_end = total;
+    stride = P;
+  }
+  for (; t < t_end; t += stride) {
+    const int mt = int(t % mtr);
+    const int64_t rest = t / mtr;
+    const int nt = int(rest % n_tiles);
+    const int kz = int(rest / n_tiles);
+    gemm_tile<BM, WGN, EPI>(g, M, mt, nt, kz);
+  }
+}
+
 // Sum of the split-K slices in slice order, then the store epilogue (row remap, row scale,
 // bf16). One thread per 4 output columns.
 __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs g) {
   const int64_t M = g.num_m_dev ? int64_t(g.num_m_dev[0]) : g.M;
   const int nq = g.N / 4;
-  const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t m = t / nq;
-  const int n = int(t - m * nq) * 4;
-  if (m >= M) return;
-  int64_t drow = m, id = m;
-  if (g.a_ids) {
-    id = g.a_ids[m];
-    if (id >= g.id_limit) return;
-    if (g.c_by_id) drow = id;
+  for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < M * nq; t += int64_t(gridDim.x) * 256) {
+    const int64_t m = t / nq;
+    const int n = int(t - m * nq) * 4;
+    int64_t drow = m, id = m;
+    if (g.a_ids) {
+      id = g.a_ids[m];
+      if (id >= g.id_limit) continue;
+      if (g.c_by_id) drow = id;
+    }
+    if (g.c_rows) drow = g.c_rows[m];
+    float scale = 1.0f;
+    if (g.row_scale_f32) scale = g.row_scale_f32[id];
+    if (g.row_scale_bf16) scale = bf16_to_f32(g.row_scale_bf16[id]);
+    float4 s = *reinterpret_cast<const float4*>(g.partial + m * g.N + n);
+    for (int z = 1; z < g.ksplit; ++z) {
+      const float4 v = *reinterpret_cast<const float4*>(g.partial + (int64_t(z) * g.m_pad + m) * g.N + n);
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+    uint2 st;
+    st.x = pack_bf16x2(s.x * scale, s.y * scale);
+    st.y = pack_bf16x2(s.z * scale, s.w * scale);
+    *reinterpret_cast<uint2*>(g.Cout + drow * g.ldc + n) = st;
   }
-  if (g.c_rows) drow = g.c_rows[m];
-  float scale = 1.0f;
-  if (g.row_scale_f32) scale = g.row_scale_f32[id];
-  if (g.row_scale_bf16) scale = bf16_to_f32(g.row_scale_bf16[id]);
-  float4 s = *reinterpret_cast<const float4*>(g.partial + m * g.N + n);
-  for (int z = 1; z < g.ksplit; ++z) {
-    const float4 v = *reinterpret_cast<const float4*>(g.partial + (int64_t(z) * g.m_pad + m) * g.N + n);
-    s.x += v.x;
-    s.y += v.y;
-    s.z += v.z;
-    s.w += v.w;
-  }
-  uint2 st;
-  st.x = pack_bf16x2(s.x * scale, s.y * scale);
-  st.y = pack_bf16x2(s.z * scale, s.w * scale);
-  *reinterpret_cast<uint2*>(g.Cout + drow * g.ldc + n) = st;
+}
+
+static int num_cus() {
+  static int n = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    return v;
+  }();
+  return n;
 }
 
 static constexpr size_t lds_bytes(int bm) { return size_t(2) * (bm + kGemmBN) * kGemmBK * sizeof(uint16_t); }
@@ -292,9 +324,10 @@ static int launch_gemm_cfg(const GemmArgs& g0, int64_t m_tiles, int ksplit, hipS
   g.ksplit = ksplit;
   g.m_pad = m_tiles * BM;
   const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (kGemmBN / 2)) : int(cdiv(g.N, kGemmBN));
-  const int64_t nwg = m_tiles * n_tiles * ksplit;
-  if (nwg == 0) return 0;
-  DYLLM_REQUIRE(nwg < (int64_t(1) << 31), "GEMM grid too large");
+  const int64_t tiles = m_tiles * n_tiles * ksplit;
+  if (tiles == 0) return 0;
+  int64_t nwg = tiles < num_cus() ? tiles : num_cus();
+  if (nwg >= 8) nwg &= ~int64_t(7);
   const size_t lds = lds_bytes(BM);
   static bool attr_set = false;
   if (!attr_set) {
@@ -307,7 +340,8 @@ static int launch_gemm_cfg(const GemmArgs& g0, int64_t m_tiles, int ksplit, hipS
   if (int rc = check_launch("gemm_kernel")) return rc;
   if (ksplit > 1) {
     const int64_t threads = m_tiles * BM * (g.N / 4);
-    gemm_partial_reduce_kernel<<<unsigned(cdiv(threads, 256)), 256, 0, s>>>(g);
+    const int64_t blocks = cdiv(threads, 256) < 4 * num_cus() ? cdiv(threads, 256) : 4 * num_cus();
+    gemm_partial_reduce_kernel<<<unsigned(blocks), 256, 0, s>>>(g);
     return check_launch("gemm_partial_reduce_kernel");
   }
   return 0;

@@ -19,15 +19,16 @@ struct RowMapArgs {
   int B;
 };
 int launch_row_map(RowMap mode, const RowMapArgs& a, hipStream_t stream);
-int launch_scatter_dest_rows(const int64_t* row_idx, int64_t M, const int32_t* cu, const int64_t* seq_starts,
-                             const int64_t* seq_ids, int B, int64_t* dest, hipStream_t s);
+int launch_scatter_dest_rows(const int64_t* row_idx, int64_t M, const int32_t* m_dev, const int32_t* cu,
+                             const int64_t* seq_starts, const int64_t* seq_ids, int B, int64_t* dest, hipStream_t s);
 int launch_cosine_mask(const float* stats, uint8_t* mask, int64_t T, float tau, hipStream_t s);
 int launch_saliency_rows(const uint16_t* c_new, const uint16_t* c_old, float* stats, uint8_t* mask, int64_t T,
                          int64_t D, float tau, hipStream_t s);
 int launch_saliency_reduce(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
                            hipStream_t s);
 int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
-                   int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* cu_sal, int32_t* count, hipStream_t s);
+                   int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
+                   hipStream_t s);
 int launch_fused_offset(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_prompt,
                         const int32_t* cu_sal, int groups, int64_t* out, int64_t cap, hipStream_t s);
 
@@ -41,7 +42,8 @@ struct AttnArgs {
   uint16_t* O;              // [rows, H, 128]
   const int32_t* cu_rows;   // [B+1] prefix of the rows this launch produces
   const int32_t* cu_k;      // [B+1]
-  const int64_t* kv_start;  // optional [B]: first K/V row of sequence b (else cu_k[b])
+  const int64_t* kv_start;  // optional [B]: first K (and V) row of sequence b (else cu_k[b])
+  const int64_t* v_start;   // optional [B]: first V row of sequence b (else as K)
   const int64_t* c_start;   // optional [B]: first C row of sequence b (else cu_rows[b])
   int c_inplace;            // ColSparse: also write the new rows back to C
   const int32_t* q_rows;    // RowSparse: Q row of compact row j

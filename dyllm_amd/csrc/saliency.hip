@@ -119,7 +119,8 @@ constexpr int kCompactItems = 16;
 __global__ __launch_bounds__(kCompactThreads) void compact_kernel(
     const uint8_t* __restrict__ mask, int64_t T, const int32_t* __restrict__ cu_q, int B,
     const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64, int32_t* __restrict__ idx32,
-    int64_t* __restrict__ idx_k, int32_t* __restrict__ cu_sal, int32_t* __restrict__ count) {
+    int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32, int32_t* __restrict__ cu_sal,
+    int32_t* __restrict__ count) {
   __shared__ int wave_tot[16];
   __shared__ int base_sh;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -202,16 +203,20 @@ __global__ __launch_bounds__(kCompactThreads) void compact_kernel(
       else
         hi = mid;
     }
-    idx_k[t] = idx64[t] + cu_prompt[lo + 1];
+    const int64_t kk = idx64[t] + cu_prompt[lo + 1];
+    idx_k[t] = kk;
+    if (idx_k32) idx_k32[t] = int32_t(kk);
   }
 }
 
 int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
-                   int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* cu_sal, int32_t* count, hipStream_t s) {
+                   int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
+                   hipStream_t s) {
   DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
   DYLLM_REQUIRE(T >= 0 && T < (int64_t(1) << 31), "row count out of range");
   DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
-  compact_kernel<<<1, kCompactThreads, 0, s>>>(mask, T, cu_q, B, cu_prompt, idx64, idx32, idx_k, cu_sal, count);
+  compact_kernel<<<1, kCompactThreads, 0, s>>>(mask, T, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal,
+                                                count);
   return check_launch("compact_kernel");
 }
 

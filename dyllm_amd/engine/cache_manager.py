@@ -100,10 +100,11 @@ class CacheManager:
         return ops.seq_row_starts(self.seq_start_gpu, seq_ids, ctx.cu_seqlens_k,
                                   ctx.cu_seqlens_q if block else None)
 
-    def dest_rows(self, seq_ids: torch.Tensor, row_idx: torch.Tensor) -> torch.Tensor:
-        """Cache rows of packed K-space row indices (the addressing of scatter_update)."""
+    def dest_rows(self, seq_ids: torch.Tensor, row_idx: torch.Tensor, count=None) -> torch.Tensor:
+        """Cache rows of packed K-space row indices (the addressing of scatter_update); with a
+        device ``count`` only its first count[0] entries are mapped."""
         ctx = get_context()
-        return ops.scatter_dest_rows(row_idx, ctx.cu_seqlens_k, self.seq_start_gpu, seq_ids)
+        return ops.scatter_dest_rows(row_idx, ctx.cu_seqlens_k, self.seq_start_gpu, seq_ids, count)
 
     # -- allocation ---------------------------------------------------------------------
     def reset_seq(self, c: torch.Tensor, seq_id):

@@ -15,8 +15,9 @@ Differences in *how*, not *what*: dV stays compact ([n_sal] rows addressed throu
 map inside the kernel) instead of a zero-filled [T_k] tensor; the column-sparse kernel reads the
 cached context rows in place and writes the new rows straight back (the reference's
 get_seqs_block + reset_block round trip); compaction runs on the device and returns the
-per-sequence counts without torch.nonzero/searchsorted. One host read of the salient count per
-layer remains, as in the reference (torch.nonzero).
+per-sequence counts without torch.nonzero/searchsorted. The one host read of the salient count
+per layer (the reference's torch.nonzero sync) is deferred until the next layer needs it, so the
+FFN of this layer is already enqueued when the host waits.
 """
 from __future__ import annotations
 
@@ -41,6 +42,7 @@ class Attention(nn.Module):
         self.threshold = threshold
         self.context_cache = CacheManager(self.num_heads * self.head_dim, device=torch.device(device))
         self.v_cache = CacheManager(self.num_kv_heads * self.head_dim, device=torch.device(device))
+        self._bufs = None  # reusable outputs / workspace of the sparse step (ops.StepBuffers)
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         ctx = get_context()
@@ -60,38 +62,31 @@ class Attention(nn.Module):
             return o
 
         seq_ids = md.running_seqs_tensor
-        q_pruned = ctx.idx_salient_row_k is not None
-        idx_q = ctx.idx_salient_row
-        idx_k = ctx.idx_salient_row_k if q_pruned else ctx.idx_salient_row
-        idx_q32 = ctx.idx_salient_row_i32 if ctx.idx_salient_row_i32 is not None else idx_q.to(torch.int32)
-        idx_k32 = idx_k.to(torch.int32) if q_pruned else idx_q32
-
-        # dV of the salient keys and the V-cache update (attention.py:67-74, 89-96)
-        dv = ops.v_delta_update(self.v_cache._slab, v, self.v_cache.dest_rows(seq_ids, idx_k))
-        v_full = self.v_cache.get_seqs(seq_ids, md.running_seqs).view(-1, self.num_kv_heads, self.head_dim)
-
-        # row-sparse attention of the salient queries vs the full cached K/V (attention.py:76-87)
-        max_sal = ctx.max_salientlen if ctx.max_salientlen > 0 else ctx.max_seqlen_q
-        o_sal = ops.flash_attn_varlen_func(q, k, v_full, ctx.cu_salientlens, ctx.cu_seqlens_k, max_sal,
-                                           ctx.max_seqlen_k, softmax_scale=self.scale, q_rows=idx_q32)
-
-        # column-sparse attention + stats + tau test, context cache updated in place
-        # (attention.py:107-145 and the reset_block/reset_full of :153,168)
-        c_start = self.context_cache.row_starts(seq_ids, block=q_pruned)
-        new_c, _, mask = ops.attention_colsparse_cached(
-            q, k, None, dv.view(-1, self.num_kv_heads, self.head_dim), self.context_cache._slab, c_start, o_sal,
-            ctx.cu_seqlens_q, ctx.cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k, k.shape[0], idx_q32, idx_k32,
-            self.threshold, c_inplace=True)
-
-        # compaction of the next salient set (attention.py:147-173)
-        comp = ops.salient_compact(mask, ctx.cu_seqlens_q, ctx.cu_promptlens if q_pruned else None)
-        n, cu_host = comp.host()
-        ctx.max_salientlen = max(cu_host[i + 1] - cu_host[i] for i in range(len(cu_host) - 1))
-        ctx.idx_salient_row = comp.idx64[:n]
-        ctx.idx_salient_row_i32 = comp.idx32[:n]
-        ctx.cu_salientlens = comp.cu_salientlens
+        q_pruned = ctx.q_pruned
+        idx_q = ctx.idx_salient_row            # resolves the previous layer's set (host read)
+        n = idx_q.numel()
+        idx_q32 = ctx.idx_salient_row_i32
         if q_pruned:
-            ctx.idx_salient_row_k = comp.idx_k[:n]
+            idx_k64, idx_k32 = ctx.idx_salient_row_k, ctx.idx_salient_row_k_i32
+        else:
+            idx_k64, idx_k32 = idx_q, idx_q32
+        Tq, Tk, B = q.shape[0], k.shape[0], seq_ids.numel()
+        key = (Tq, Tk, B, q_pruned, ctx.max_seqlen_k)
+        bufs = self._bufs
+        if bufs is None or bufs.key != key:
+            bufs = self._bufs = ops.StepBuffers(key, q.device, Tq, Tk, B, self.num_heads, self.num_kv_heads,
+                                                self.head_dim, ctx.max_seqlen_k, q_pruned)
+        # one native call: dV + V-cache update, row-sparse attention (attention.py:67-87),
+        # column-sparse attention + stats + tau test with the context cache updated in place
+        # (:107-145, :153/:168), and compaction of the next salient set (:147-173)
+        ops.sparse_attention_step(
+            bufs, q, k, self.v_cache._slab, self.v_cache.seq_start_gpu, v.view(n, self.num_kv_heads, self.head_dim),
+            self.context_cache._slab, self.context_cache.seq_start_gpu, seq_ids, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+            ctx.cu_promptlens if q_pruned else None, ctx.max_seqlen_q, ctx.max_seqlen_k, Tk, n, ctx.max_salientlen,
+            ctx.cu_salientlens, idx_q32, idx_k64, idx_k32, self.scale, self.threshold)
+        # the next layer's salient set stays on the device until it is needed (Context.resolve_salient)
+        ctx.set_pending(bufs.compacted())
+        new_c = bufs.out
 
         self.v_cache.finish(md.finished_seqs)
         self.context_cache.finish(md.finished_seqs)

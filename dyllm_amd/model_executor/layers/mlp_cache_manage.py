@@ -29,7 +29,7 @@ class MLPcache(nn.Module):
         """All queried rows, packed (mlp_cache_manage.py:33/38)."""
         ctx = get_context()
         md = get_metadata()
-        if ctx.idx_salient_row_k is not None:
+        if ctx.q_pruned:
             return self.cache_manager.get_seqs_block(md.running_seqs_tensor)
         return self.cache_manager.get_seqs(md.running_seqs_tensor, md.running_seqs)
 

@@ -78,18 +78,29 @@ class LLaDAMLP(nn.Module):
         return self.cache_update(y)
 
     def forward_salient(self, h_all, gate_up_events=None):
-        """Sparse step, fused: h_all = all queried rows after post_attention_layernorm.
+        """Sparse step, fused: h_all = all queried rows after post_attention_layernorm. The
+        salient rows are gathered inside the gate_up GEMM and the down GEMM scatters into the FFN
+        cache. When the salient set is still on the device (Context.salient_pending), the GEMMs
+        read its size from device memory: no host synchronisation.
         ``gate_up_events`` (start, end) brackets the gathered gate_up GEMM for timing."""
         ctx = get_context()
+        md = get_metadata()
         cm = self.cache_update.cache_manager
-        rows = ctx.idx_salient_row_i32 if ctx.idx_salient_row_i32 is not None else ctx.idx_salient_row.to(torch.int32)
+        comp = ctx.salient_pending
+        if comp is not None:
+            rows, count, hint = comp.idx32, comp.count, ctx.salient_hint
+            kidx = comp.idx_k if comp.idx_k is not None else comp.idx64
+        else:
+            rows, count, hint = ctx.idx_salient_row_i32, None, 0
+            kidx = ctx.idx_salient_row_k if ctx.idx_salient_row_k is not None else ctx.idx_salient_row
         h_all = h_all.contiguous()
         if gate_up_events is not None:
             gate_up_events[0].record()
-        h = ops.ffn_gate_up(h_all, self.gate_up_proj, rows_idx=rows)
+        h = ops.ffn_gate_up(h_all, self.gate_up_proj, rows_idx=rows, count=count, hint=hint)
         if gate_up_events is not None:
             gate_up_events[1].record()
-        ops.ffn_down(h, self.down_proj, out=cm._slab, out_rows=self.cache_update.dest_rows())
+        dest = cm.dest_rows(md.running_seqs_tensor, kidx, count)
+        ops.ffn_down(h, self.down_proj, out=cm._slab, out_rows=dest, count=count, hint=hint)
         return self.cache_update.gather_all()
 
 

@@ -203,13 +203,19 @@ def saliency_stats(c_new, c_old, threshold):
 class Compacted:
     """Device results of one compaction; ``count`` stays on the device until asked for."""
 
-    def __init__(self, idx64, idx32, idx_k, cu_salientlens, count):
-        self.idx64, self.idx32, self.idx_k = idx64, idx32, idx_k
+    def __init__(self, idx64, idx32, idx_k, cu_salientlens, count, idx_k32=None, host_meta=None, event=None):
+        self.idx64, self.idx32, self.idx_k, self.idx_k32 = idx64, idx32, idx_k, idx_k32
         self.cu_salientlens, self.count = cu_salientlens, count
+        self.host_meta, self.event = host_meta, event
 
     def host(self):
-        """(count, cu_salientlens as a list): one device->host read for both."""
-        h = torch.cat([self.count, self.cu_salientlens]).cpu().tolist()
+        """(count, cu_salientlens as a list): one device->host read for both. With a pinned
+        copy in flight (host_meta + event) only that copy is waited for, not the whole stream."""
+        if self.event is not None:
+            self.event.synchronize()
+            h = self.host_meta.tolist()
+        else:
+            h = torch.cat([self.count, self.cu_salientlens]).cpu().tolist()
         return h[0], h[1:]
 
     def n(self) -> int:
@@ -240,6 +246,51 @@ def salient_compact(mask, cu_seqlens_q, cu_promptlens=None):
     _lib.call("dyllm_salient_compact", _ptr(mask), T, _ptr(cu_q), B, _ptr(cu_p), _ptr(idx64), _ptr(idx32),
               _ptr(idx_k), _ptr(cu_sal), _ptr(count), _stream())
     return Compacted(idx64, idx32, idx_k, cu_sal, count)
+
+
+class StepBuffers:
+    """Reusable outputs and workspace of ``sparse_attention_step`` for one layer and shape."""
+
+    def __init__(self, key, dev, Tq, Tk, B, H, Hkv, D, max_k, q_pruned):
+        self.key = key
+        i64, i32 = dict(dtype=torch.int64, device=dev), dict(dtype=torch.int32, device=dev)
+        self.out = torch.empty((Tq, H, D), dtype=torch.bfloat16, device=dev)
+        self.stats = torch.empty((Tq, 3), dtype=torch.float32, device=dev)
+        self.mask = torch.empty(Tq, dtype=torch.bool, device=dev)
+        self.idx64 = torch.empty(max(Tq, 1), **i64)
+        self.idx32 = torch.empty(max(Tq, 1), **i32)
+        self.idx_k64 = torch.empty(max(Tq, 1), **i64) if q_pruned else None
+        self.idx_k32 = torch.empty(max(Tq, 1), **i32) if q_pruned else None
+        self.meta = torch.empty(B + 2, **i32)          # [count, cu_salientlens...]
+        self.count, self.cu_sal = self.meta[0:1], self.meta[1:]
+        self.host_meta = torch.empty(B + 2, dtype=torch.int32, pin_memory=True)
+        self.event = torch.cuda.Event()
+        self.ws_bytes = _lib.load().dyllm_sparse_step_workspace_bytes(B, H, Hkv, D, Tq, Tk, max_k, Tq)
+        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
+
+    def compacted(self):
+        return Compacted(self.idx64, self.idx32, self.idx_k64, self.cu_sal, self.count, self.idx_k32,
+                         self.host_meta, self.event)
+
+
+def sparse_attention_step(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_seq_starts, seq_ids, cu_seqlens_q,
+                          cu_seqlens_k, cu_promptlens, max_seqlen_q, max_seqlen_k, total_k, n_sal, max_salientlen,
+                          cu_salientlens, idx_q32, idx_k64, idx_k32, softmax_scale, threshold, k_start=None):
+    """The sparse branch of Attention.forward in one native call (dyllm_sparse_attention_step).
+    Results land in ``bufs`` (out / stats / mask and the next salient set, left on the device)."""
+    Tq, H, D = q.shape
+    Hkv = v_new.shape[1] if v_new.dim() == 3 else v_cache.shape[1] // D
+    _lib.call("dyllm_sparse_attention_step", _ptr(q), _ptr(k), _ptr(k_start), _ptr(v_cache), _ptr(v_seq_starts),
+              _ptr(v_new), _ptr(c_cache), _ptr(c_seq_starts), _ptr(seq_ids), seq_ids.numel(), H, Hkv, D,
+              _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), _ptr(cu_promptlens), int(max_seqlen_q), int(max_seqlen_k), Tq,
+              int(total_k), int(n_sal), int(max_salientlen), _ptr(cu_salientlens), _ptr(idx_q32), _ptr(idx_k64),
+              _ptr(idx_k32), float(softmax_scale), float(threshold), _ptr(bufs.out), _ptr(bufs.stats),
+              _ptr(bufs.mask), _ptr(bufs.idx64), _ptr(bufs.idx32), _ptr(bufs.idx_k64), _ptr(bufs.idx_k32),
+              _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(bufs.ws), bufs.ws_bytes, _stream())
+    # the salient count and per-sequence prefix go to pinned memory right behind the compaction
+    bufs.host_meta.copy_(bufs.meta, non_blocking=True)
+    bufs.event.record()
+    return bufs
 
 
 def fused_offset_launch(idxs, num_idxs, cu_promptlens, cu_salientlens, out_tensor, max_threads):
@@ -324,13 +375,15 @@ def scatter_update_cuda(cache, new_vals, row_idx, cu_seqlens, seq_starts, seq_id
               _ptr(cu), _ptr(seq_starts), _ptr(seq_ids), seq_ids.numel(), _stream())
 
 
-def scatter_dest_rows(row_idx, cu_seqlens, seq_starts, seq_ids):
+def scatter_dest_rows(row_idx, cu_seqlens, seq_starts, seq_ids, count=None):
+    """Cache rows of packed row indices; with ``count`` (device int32 [1]) only the first
+    count[0] entries of the capacity-sized ``row_idx`` are mapped."""
     ri = _i64(row_idx)
     cu = _i32(cu_seqlens)
     dest = torch.empty_like(ri)
     if ri.numel():
-        _lib.call("dyllm_scatter_dest_rows", _ptr(ri), ri.numel(), _ptr(cu), _ptr(seq_starts), _ptr(seq_ids),
-                  seq_ids.numel(), _ptr(dest), _stream())
+        _lib.call("dyllm_scatter_dest_rows", _ptr(ri), ri.numel(), _ptr(count), _ptr(cu), _ptr(seq_starts),
+                  _ptr(seq_ids), seq_ids.numel(), _ptr(dest), _stream())
     return dest
 
 
@@ -347,8 +400,10 @@ def gather_rows_2D(x, row_idx):
 # ---------------------------------------------------------------------------------------
 # FFN / MoE
 # ---------------------------------------------------------------------------------------
-def ffn_gate_up(x, w_gate_up, rows_idx=None):
-    """h = silu(a Wg^T) * (a Wu^T) for a = x[rows_idx] (gathered inside the GEMM)."""
+def ffn_gate_up(x, w_gate_up, rows_idx=None, count=None, hint=0):
+    """h = silu(a Wg^T) * (a Wu^T) for a = x[rows_idx] (gathered inside the GEMM). With
+    ``count`` (device int32 [1]) ``rows_idx`` is a capacity-sized buffer of which the first
+    count[0] rows are used -- no host synchronisation; ``hint`` is the expected count."""
     _check(x, "x", torch.bfloat16, 2)
     _check(w_gate_up, "w_gate_up", torch.bfloat16, 2)
     hidden = x.shape[1]
@@ -359,13 +414,14 @@ def ffn_gate_up(x, w_gate_up, rows_idx=None):
     M = ri.numel() if ri is not None else x.shape[0]
     h = torch.empty((M, inter), dtype=x.dtype, device=x.device)
     if M:
-        _lib.call("dyllm_ffn_gate_up", _ptr(x), x.stride(0), _ptr(ri), M, _ptr(w_gate_up), hidden, inter, _ptr(h),
-                  _stream())
+        _lib.call("dyllm_ffn_gate_up", _ptr(x), x.stride(0), _ptr(ri), M, _ptr(count), int(hint), _ptr(w_gate_up),
+                  hidden, inter, _ptr(h), _stream())
     return h
 
 
-def ffn_down(h, w_down, out=None, out_rows=None):
-    """y = h Wd^T, written to out[out_rows[m]] when given (in-place scatter) else a new tensor."""
+def ffn_down(h, w_down, out=None, out_rows=None, count=None, hint=0):
+    """y = h Wd^T, written to out[out_rows[m]] when given (in-place scatter) else a new tensor;
+    ``count``/``hint`` as for ffn_gate_up."""
     _check(h, "h", torch.bfloat16, 2)
     _check(w_down, "w_down", torch.bfloat16, 2)
     M, inter = h.shape
@@ -379,10 +435,10 @@ def ffn_down(h, w_down, out=None, out_rows=None):
         _check(out, "out", torch.bfloat16, 2)
         orow = _i64(out_rows) if out_rows is not None else None
     if M:
-        ws_bytes = _lib.load().dyllm_ffn_down_workspace_bytes(M, hidden, inter)
+        ws_bytes = _lib.load().dyllm_ffn_down_workspace_bytes(M, int(hint), hidden, inter)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=h.device)
-        _lib.call("dyllm_ffn_down", _ptr(h), M, _ptr(w_down), hidden, inter, _ptr(out), _ptr(orow), _ptr(ws),
-                  ws_bytes, _stream())
+        _lib.call("dyllm_ffn_down", _ptr(h), M, _ptr(count), int(hint), _ptr(w_down), hidden, inter, _ptr(out),
+                  _ptr(orow), _ptr(ws), ws_bytes, _stream())
     return out
 
 

@@ -28,7 +28,7 @@
  *   dyllm_moe_gate                 <- moe_gate, dyllm/model_executor/layers/fused_moe.py:375-408
  *   dyllm_moe_align_block_size     <- moe_align_block_size, fused_moe.py:37-85
  *   dyllm_fused_experts            <- fused_experts, fused_moe.py:269-335
- *   dyllm_attention_colsparse_cached, dyllm_v_delta_update, dyllm_seq_row_starts
+ *   dyllm_sparse_attention_step, dyllm_attention_colsparse_cached, dyllm_v_delta_update, dyllm_seq_row_starts
  *                                  <- the sparse branch of Attention.forward, attention.py:64-178, with the
  *                                     K/V/context cache gathers and the full-size dV fused away
  *   dyllm_saliency_stats           <- the statistics epilogue of attention_ops_kernels_sm80.cu:436-481
@@ -97,6 +97,31 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
                                      float* cosine_stats, uint8_t* cosine_out, float threshold, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
+/* The whole sparse branch of Attention.forward (attention.py:64-178) in one call, so the
+ * ~10 launches of a layer leave the host back to back: dV + V-cache update of the salient keys
+ * (v_new rows follow idx_k64), row-sparse attention of the salient queries against the cached
+ * K/V, column-sparse attention with statistics and the tau test (context cache updated in place,
+ * new rows also written to `out` [total_q, H, D]), and compaction of the next salient set into
+ * next_* (capacity total_q; next_count[0] = its size, left on the device). K is packed
+ * (k_start == NULL) or read from a cache through per-sequence first rows k_start[b]; the V and
+ * context caches are addressed through their seq_start tables (indexed by seq_ids[b]).
+ * cu_promptlens != NULL selects a Q-pruned step (Q rows are the response rows; the next set is
+ * also produced in K space); otherwise Q space == K space and idx_k* = idx_q*. */
+size_t dyllm_sparse_step_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim, int64_t total_q,
+                                         int64_t total_k, int max_seqlen_k, int64_t num_salient);
+int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_start, void* v_cache,
+                                const int64_t* v_seq_starts, const void* v_new, void* c_cache,
+                                const int64_t* c_seq_starts, const int64_t* seq_ids, int batch, int num_heads,
+                                int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
+                                const int32_t* cu_seqlens_k, const int32_t* cu_promptlens, int max_seqlen_q,
+                                int max_seqlen_k, int64_t total_q, int64_t total_k, int num_salient,
+                                int max_salientlen, const int32_t* cu_salientlens, const int32_t* idx_q32,
+                                const int64_t* idx_k64, const int32_t* idx_k32, float softmax_scale, float threshold,
+                                void* out, float* cosine_stats, uint8_t* cosine_out, int64_t* next_idx64,
+                                int32_t* next_idx32, int64_t* next_idx_k64, int32_t* next_idx_k32,
+                                int32_t* next_cu_salientlens, int32_t* next_count, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
 /* dV and V-cache update of attention.py:67-74 (dv = v_new - v_cache[row]; v_cache[row] = v_new)
  * for compact rows; dest_rows are cache rows (dyllm_scatter_dest_rows). */
 int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,
@@ -146,10 +171,11 @@ int dyllm_reset_block(void* cache, const void* in, int64_t row_bytes, const int6
 int dyllm_scatter_update(void* cache, const void* new_vals, int64_t row_bytes, const int64_t* row_idx, int64_t rows,
                          const int32_t* cu_seqlens, const int64_t* seq_starts, const int64_t* seq_ids, int batch,
                          void* stream);
-/* Destination cache row of each packed row index (the address part of scatter_update). */
-int dyllm_scatter_dest_rows(const int64_t* row_idx, int64_t rows, const int32_t* cu_seqlens,
-                            const int64_t* seq_starts, const int64_t* seq_ids, int batch, int64_t* dest,
-                            void* stream);
+/* Destination cache row of each packed row index (the address part of scatter_update); rows
+ * beyond *rows_dev (when given) are skipped. */
+int dyllm_scatter_dest_rows(const int64_t* row_idx, int64_t rows, const int32_t* rows_dev,
+                            const int32_t* cu_seqlens, const int64_t* seq_starts, const int64_t* seq_ids, int batch,
+                            int64_t* dest, void* stream);
 /* out[m] = x[idx[m]] */
 int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t* idx, int64_t rows, void* stream);
 
@@ -158,7 +184,7 @@ int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t
 /* Workspace of dyllm_swiglu_ffn: dyllm_swiglu_ffn_workspace_bytes (the [rows, intermediate]
  * bf16 activations) + dyllm_ffn_down_workspace_bytes (split-K partials of the down GEMM). */
 size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate);
-size_t dyllm_ffn_down_workspace_bytes(int64_t rows, int hidden, int intermediate);
+size_t dyllm_ffn_down_workspace_bytes(int64_t rows, int64_t rows_hint, int hidden, int intermediate);
 
 /* Gathered SwiGLU FFN: for m < rows, a = x[rows_idx ? rows_idx[m] : m] (row stride ld_x),
  * h = silu(a W_g^T) * (a W_u^T), y = h W_d^T written to out[out_rows ? out_rows[m] : m]
@@ -169,11 +195,16 @@ int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64
                      void* out, const int64_t* out_rows, void* stream);
 
 /* The two stages of dyllm_swiglu_ffn: h_out [rows, intermediate] = silu(a W_g^T) * (a W_u^T)
- * with a = x[rows_idx[m] or m]; then out[out_rows[m] or m] = h[m] W_d^T. */
-int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
-                      int hidden, int intermediate, void* h_out, void* stream);
-int dyllm_ffn_down(const void* h, int64_t rows, const void* w_down, int hidden, int intermediate, void* out,
-                   const int64_t* out_rows, void* workspace, size_t workspace_bytes, void* stream);
+ * with a = x[rows_idx[m] or m]; then out[out_rows[m] or m] = h[m] W_d^T. `rows` is the capacity
+ * (buffers are sized for it); when rows_dev != NULL the row count is read from device memory
+ * (e.g. the count written by dyllm_salient_compact), so no host synchronisation is needed.
+ * rows_hint (0: rows) is the expected count used to choose the tile shape. */
+int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const int32_t* rows_dev,
+                      int64_t rows_hint, const void* w_gate_up, int hidden, int intermediate, void* h_out,
+                      void* stream);
+int dyllm_ffn_down(const void* h, int64_t rows, const int32_t* rows_dev, int64_t rows_hint, const void* w_down,
+                   int hidden, int intermediate, void* out, const int64_t* out_rows, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 /* Tile height (128/192/256) the FFN GEMMs use for `rows` rows and output width n. */
 int dyllm_ffn_tile_rows(int64_t rows, int n, int swiglu);

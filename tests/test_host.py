@@ -54,7 +54,7 @@ def test_error_path_reports_message_without_gpu():
         _lib.call("dyllm_attention_sparse_varlen", 1, 1, 1, 1, 1, 1, 1, 4, 4, 128, 1, 1, 8, 8, 8, 0, 1, None, None,
                   1, 1, 0.99, 1, 16, None)
     with pytest.raises(RuntimeError, match="hidden size must be a positive multiple of 64"):
-        _lib.call("dyllm_ffn_gate_up", 1, 100, None, 10, 1, 100, 128, 1, None)
+        _lib.call("dyllm_ffn_gate_up", 1, 100, None, 10, None, 0, 1, 100, 128, 1, None)
     with pytest.raises(RuntimeError, match="must not be NULL"):
         _lib.call("dyllm_get_seqs", 1, 1, 16, None, 1, 1, 1, 4, None)
     lib = _lib.load()
