@@ -41,8 +41,12 @@ constexpr int kGemmBN = 256;
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float bf16_rt(float x) { return __uint_as_float(uint32_t(f32_to_bf16(x)) << 16); }
 
-// element offset of (row, 16-byte chunk) in a swizzled 64-element-wide tile
-__device__ __forceinline__ int swz(int row, int chunk) { return row * kGemmBK + ((chunk ^ (row & 7)) << 3); }
+// element offset of (row, 16-byte chunk) in a swizzled 64-element-wide tile. gfx950 serves a
+// 16-byte LDS read for 16 lanes at a time over 64 banks (two 128-byte rows): the 16 rows a
+// fragment read touches must land on distinct (row parity, chunk) pairs, so the chunk is
+// XOR-ed with bits 1..3 of the row (measured: zero SQ_LDS_BANK_CONFLICT).
+__device__ __forceinline__ int swz_chunk(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * kGemmBK + (swz_chunk(row, chunk) << 3); }
 
 // One BM x 256 output tile (K slice kz of ksplit).
 template <int BM, int WGN, GemmEpi EPI>
@@ -69,10 +73,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
 
   // Direct global->LDS staging: each wavefront fills 1 KB blocks of 8 swizzled rows; lane L
   // of a block lands at byte 16*L, i.e. row L/8, physical chunk L%8, which holds logical
-  // chunk (L%8) ^ (L/8). Rows outside the problem (m >= M, padding ids, n >= N) are clamped
-  // to a valid row: their products are never stored.
+  // chunk swz_chunk(row, L%8) (the XOR is its own inverse). Rows outside the problem
+  // (m >= M, padding ids, n >= N) are clamped to a valid row: their products are never stored.
   constexpr int CA = BM / (8 * NW), CW = BN / (8 * NW);  // 1 KB blocks per wavefront per K slice
-  const int lrow = lane >> 3, lchunk = (lane & 7) ^ (lane >> 3);
+  const int lrow = lane >> 3;
   const uint16_t* a_src[CA];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
@@ -85,7 +89,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
         row = (id < g.id_limit) ? id / g.a_div : 0;
       }
     }
-    a_src[i] = g.A + row * g.lda + int64_t(k_begin) * kGemmBK + lchunk * 8;
+    a_src[i] = g.A + row * g.lda + int64_t(k_begin) * kGemmBK + swz_chunk((w + NW * i) * 8 + lrow, lane & 7) * 8;
   }
   const uint16_t* w_src[CW];
 #pragma unroll
@@ -97,7 +101,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     else
       wrow = int64_t(nt) * BN + r;
     if (wrow >= g.N) wrow = 0;
-    w_src[i] = Wb + wrow * g.ldw + int64_t(k_begin) * kGemmBK + lchunk * 8;
+    w_src[i] = Wb + wrow * g.ldw + int64_t(k_begin) * kGemmBK + swz_chunk(r, lane & 7) * 8;
   }
   typedef __attribute__((address_space(3))) void lds_void;
   typedef const __attribute__((address_space(1))) void glb_void;
