@@ -35,6 +35,9 @@ CONFIG1 = dict(layers=32, hidden=4096, heads=32, kv_heads=32, head_dim=128, inte
                response=768, tau=0.99, perturb=0.15)
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per launch of the gate_up GEMM at this workload, from rocprofv3 FETCH_SIZE / WRITE_SIZE
+# calibrated against a 256 MiB copy (profiles/pmc_gemm_gate_up_config1.md).
+GATE_UP_TRAFFIC_BYTES = 365.2e6
 
 
 def build_workload(cfg, layers, device, seed=0):
@@ -183,6 +186,32 @@ def cpu_baseline(cfg, n_sal, threads):
                        f"{t_layer:.2f} s, x{cfg['layers']}")
 
 
+def profile_gate_up(cfg, reps=3):
+    """Counter-collection workload: the gathered gate_up GEMM at the bench shape (15% of the
+    response rows salient) interleaved with a 256 MiB device copy used to calibrate the HBM
+    byte counters. Run under rocprofv3 --pmc."""
+    import torch
+
+    from dyllm_amd import ops
+
+    dev = "cuda"
+    hid, inter = cfg["hidden"], cfg["inter"]
+    Tq = cfg["batch"] * cfg["response"]
+    M = int(round(cfg["perturb"] * cfg["response"])) * cfg["batch"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    w = torch.empty(2 * inter, hid, device=dev).normal_(0, 0.02, generator=g).to(torch.bfloat16)
+    x = torch.empty(Tq, hid, device=dev).normal_(generator=g).to(torch.bfloat16)
+    rows = torch.sort(torch.randperm(Tq, device=dev, generator=g)[:M]).values.to(torch.int32)
+    a = torch.empty(128 * 1024 * 1024, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        ops.ffn_gate_up(x, w, rows)
+        b.copy_(a)  # calibration: 256 MiB read + 256 MiB written
+    torch.cuda.synchronize()
+    print(f"[bench] profiled gate_up: {reps} launches of M={M}, plus {reps} calibration copies of 256 MiB",
+          file=sys.stderr)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -190,6 +219,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers than the model has")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-gate-up", action="store_true",
+                    help="run only the gate_up GEMM + a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU; the hot path is not sharded across GPUs "
@@ -199,6 +230,9 @@ def main():
     import torch
 
     cfg = dict(CONFIG1)
+    if args.profile_gate_up:
+        profile_gate_up(cfg)
+        return
     layers = args.layers or cfg["layers"]
     dev = "cuda:0"
     torch.cuda.set_device(0)
@@ -264,7 +298,8 @@ def main():
         "roofline": {"kernel": f"gemm_kernel<{gate_bm},4,SwiGLU> (gathered gate_up + SiLU*up, tile {gate_bm}x256)",
                      "bound": "mfma",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
+                     "traffic_unit": "bytes per launch (PMC)", "algorithmic_bytes": 231.4e6,
                      "avg_launch_us": round(avg_gate_ms * 1e3, 2),
                      "flop_per_launch": flops},
         "cpu_baseline": cpu,
