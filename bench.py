@@ -37,7 +37,7 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the gate_up GEMM at this workload, from rocprofv3 FETCH_SIZE / WRITE_SIZE
 # calibrated against a 256 MiB copy (profiles/pmc_gemm_gate_up_config1.md).
-GATE_UP_TRAFFIC_BYTES = 365.2e6
+GATE_UP_TRAFFIC_BYTES = 364.0e6
 
 
 def build_workload(cfg, layers, device, seed=0):
