@@ -167,7 +167,7 @@ class CacheManager:
     def reset_full(self, c: torch.Tensor, seq_ids: torch.Tensor, seq_ids_list: Optional[List[int]] = None):
         """Write all rows of the running sequences, allocating new ones (cache_manager.py:139-159)."""
         ctx = get_context()
-        c = c.reshape(c.shape[0], -1).contiguous()
+        c = c.flatten(1).contiguous()
         if seq_ids_list is None:
             seq_ids_list = seq_ids.cpu().tolist()
         lens = ctx.context_lens_cpu
@@ -183,7 +183,7 @@ class CacheManager:
     def reset_block(self, c: torch.Tensor, seq_ids: torch.Tensor):
         """Write the tail ``Lq`` rows of every running sequence (cache_manager.py:161-167)."""
         ctx = get_context()
-        c = c.reshape(c.shape[0], -1).contiguous()
+        c = c.flatten(1).contiguous()
         ops.reset_block_cuda(self._slab, c, self.seq_start_gpu, ctx.cu_seqlens_k, ctx.cu_seqlens_q, seq_ids,
                              ctx.total_seqlen)
 

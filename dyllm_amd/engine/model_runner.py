@@ -1,0 +1,198 @@
+"""Builds the per-step batch and context, runs the model and the sampler
+(dyllm/engine/model_runner.py:20-549, the mask-based model path on one GPU).
+
+Step kinds (model_runner.py:140-298):
+
+* full      -- every row of every sequence is queried; the layers run dense attention and the
+               FFN over all rows and rewrite their caches;
+* sparse    -- the first layer's salient rows are the positions the previous step unmasked;
+               each layer's attention decides the next layer's salient rows. After four
+               processed steps a sparse step queries only the response rows (Q-pruned), except
+               every fourth step, which queries all rows (refresh).
+
+A batch is Q-pruned only when all its sequences are (the reference decides per sequence but
+then drops the K-space index list as soon as one sequence refreshes, model_runner.py:213-220,
+which leaves a mixed batch inconsistent); batches of sequences admitted together, the case the
+scheduler produces, behave identically.
+"""
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+
+from ..config import Config
+from ..model_executor.layers.sampler import DreamSampler, LLaDASampler
+from ..utils.context import get_context, reset_context, set_context
+from ..utils.metadata import get_metadata
+from .sequence import Sequence
+
+
+def build_model(config: Config, device="cuda"):
+    from ..model_executor.models import model_class
+
+    hf = config.hf_config
+    cls = model_class(hf)
+    model = cls(hf, config.threshold, device=device, seed=config.seed)
+    wdir = config.model_dir
+    if wdir is not None:
+        from ..utils.weight_loader import has_safetensors, load_model
+
+        if has_safetensors(wdir):
+            load_model(model, wdir)
+    return model
+
+
+def q_pruned_step(seq: Sequence) -> bool:
+    """Sparse step that queries only the response rows (model_runner.py:205)."""
+    return seq.processed_steps > 4 and seq.processed_steps % 4 != 0
+
+
+class ModelRunner:
+
+    def __init__(self, config: Config, rank: int = 0, event=None, model=None, device="cuda"):
+        self.config = config
+        self.rank = rank
+        self.device = torch.device(device)
+        self.num_full_forwards = 0
+        self.num_sparse_forwards = 0
+        hf = config.hf_config
+        self.model = model if model is not None else build_model(config, device)
+        self.sampler = DreamSampler("entropy") if hf.model_type == "Dream" else LLaDASampler("confidence")
+
+    def _dev(self, data, dtype):
+        t = torch.tensor(data, dtype=dtype)
+        if self.device.type == "cuda":
+            return t.pin_memory().to(self.device, non_blocking=True)
+        return t.to(self.device)
+
+    # -- batch preparation -------------------------------------------------------------
+    def prepare_full(self, seqs: List[Sequence]):
+        md = get_metadata()
+        input_ids, positions, cu, lens, ids = [], [], [0], [], []
+        for seq in seqs:
+            L = len(seq)
+            input_ids.extend(seq.token_ids)
+            positions.extend(range(L))
+            cu.append(cu[-1] + L)
+            lens.append(L)
+            ids.append(seq.seq_id)
+        i32 = torch.int32
+        cu_dev = self._dev(cu, i32)
+        md.running_seqs = ids
+        md.running_seqs_tensor = self._dev(ids, torch.long)
+        set_context(True, cu_seqlens_q=cu_dev, cu_seqlens_q_cpu=cu, cu_seqlens_k=cu_dev, cu_seqlens_k_cpu=cu,
+                    max_seqlen_q=max(lens), max_seqlen_k=max(lens), context_lens=self._dev(lens, i32),
+                    context_lens_cpu=lens, total_seqlen=cu[-1], total_seqlen_k=cu[-1])
+        return self._dev(input_ids, torch.long), self._dev(positions, torch.long)
+
+    def prepare_sparse(self, seqs: List[Sequence]):
+        md = get_metadata()
+        pruned = all(q_pruned_step(s) for s in seqs)
+        input_ids, positions, positions_k = [], [], []
+        idx_q, idx_k, idx_upd = [], [], []
+        cu_q, cu_k, cu_p, cu_s, lens, ids = [0], [0], [0], [0], [], []
+        for seq in seqs:
+            L = len(seq)
+            start = seq.answer_start
+            kept = [p for p in seq.last_token_pos if p >= start]
+            if pruned:
+                input_ids.extend(seq.token_ids[start:])
+                positions.extend(range(start, L))
+                idx_q.extend(p - seq.num_prompt_tokens + cu_q[-1] for p in kept)
+                idx_k.extend(p + cu_k[-1] for p in kept)
+                lq = L - start
+            else:
+                input_ids.extend(seq.token_ids)
+                positions.extend(range(L))
+                idx_q.extend(p + cu_q[-1] for p in kept)
+                lq = L
+            positions_k.extend(kept)
+            idx_upd.extend(p + cu_k[-1] for p in kept)
+            cu_p.append(cu_p[-1] + seq.num_prompt_tokens)
+            cu_s.append(cu_s[-1] + len(kept))
+            cu_q.append(cu_q[-1] + lq)
+            cu_k.append(cu_k[-1] + L)
+            lens.append(L)
+            ids.append(seq.seq_id)
+        i32, i64 = torch.int32, torch.long
+        cu_s_dev = self._dev(cu_s, i32)
+        md.running_seqs = ids
+        md.running_seqs_tensor = self._dev(ids, i64)
+        idx_q_dev = self._dev(idx_q, i64)
+        set_context(False, cu_seqlens_q=self._dev(cu_q, i32), cu_seqlens_q_cpu=cu_q, cu_seqlens_k=self._dev(cu_k, i32),
+                    cu_seqlens_k_cpu=cu_k, cu_promptlens=self._dev(cu_p, i32), cu_updatedlens=cu_s_dev,
+                    cu_salientlens=cu_s_dev, max_seqlen_q=max(cu_q[i + 1] - cu_q[i] for i in range(len(seqs))),
+                    max_seqlen_k=max(lens), idx_updated_row=self._dev(idx_upd, i32), idx_salient_row=idx_q_dev,
+                    idx_salient_row_k=self._dev(idx_k, i64) if pruned else None,
+                    max_salientlen=max(cu_s[i + 1] - cu_s[i] for i in range(len(seqs))),
+                    context_lens=self._dev(lens, i32), context_lens_cpu=lens, total_seqlen_k=cu_k[-1],
+                    total_seqlen=cu_q[-1], positions_k=self._dev(positions_k, i64))
+        return self._dev(input_ids, i64), self._dev(positions, i64)
+
+    def prepare_sample(self, seqs: List[Sequence]):
+        """Candidate rows of the current block and the per-sequence sampling knobs
+        (model_runner.py:300-372)."""
+        mask = self.config.mask_id
+        pruned = get_context().idx_salient_row_k is not None
+        rels, counts, temps, transfers, top_ps, top_ks, thrs, offsets = [], [], [], [], [], [], [], []
+        has_t = has_p = has_k = has_thr = False
+        for seq in seqs:
+            limit = min(len(seq), seq.block_size * (seq.block_idx + 1) + seq.num_prompt_tokens)
+            mpos = [i for i in range(limit) if seq.token_ids[i] == mask]
+            off = seq.answer_start if pruned else 0
+            if pruned:
+                mpos = [p - off for p in mpos if p >= off]
+            rels.extend(mpos)
+            offsets.append(off)
+            counts.append(len(mpos))
+            t_on = seq.temperature is not None and seq.temperature > 1e-6
+            has_t |= t_on
+            # sequences without a temperature are left unscaled in a batch that has one
+            temps.extend([seq.temperature if t_on else 1.0] * len(mpos))
+            transfers.append(1 if seq.confidence_threshold is not None else seq.num_transfer_tokens)
+            top_ps.extend([seq.top_p if seq.top_p is not None else 1.0] * len(mpos))
+            top_ks.extend([seq.top_k if seq.top_k is not None else 1 << 30] * len(mpos))
+            thrs.append(seq.confidence_threshold if seq.confidence_threshold is not None else float("inf"))
+            has_p |= seq.top_p is not None
+            has_k |= seq.top_k is not None
+            has_thr |= seq.confidence_threshold is not None
+        block = max(s.block_size if s.block_size is not None else s.max_new_tokens for s in seqs)
+        cu = [0]
+        for c in counts:
+            cu.append(cu[-1] + c)
+        f32 = torch.float32
+        params = (self._dev(temps, f32) if has_t else None,
+                  self._dev(top_ks, torch.int32) if has_k else None,
+                  self._dev(top_ps, f32) if has_p else None,
+                  block,
+                  self._dev(thrs, f32) if has_thr else None)
+        indices = (self._dev(rels, torch.long), self._dev(offsets, torch.long), self._dev(cu, torch.int32))
+        return params, indices, self._dev(transfers, torch.int32)
+
+    # -- execution ------------------------------------------------------------------------
+    @torch.inference_mode()
+    def run_model(self, input_ids, positions, is_full: bool):
+        return self.model.compute_logits(self.model(input_ids, positions))
+
+    def run(self, seqs: List[Sequence], is_full: bool, finished_seqs: Optional[List[int]] = None):
+        if is_full:
+            self.num_full_forwards += 1
+        else:
+            self.num_sparse_forwards += 1
+        get_metadata().finished_seqs = list(finished_seqs or [])
+        input_ids, positions = self.prepare_full(seqs) if is_full else self.prepare_sparse(seqs)
+        logits = self.run_model(input_ids, positions, is_full)
+        params, indices, transfers = self.prepare_sample(seqs)
+        with torch.inference_mode():
+            pos, tok, cnt = self.sampler(input_logits=logits, ctx=get_context(), input_indices=indices,
+                                         temperatures=params[0], num_transfer=transfers, top_k=params[1],
+                                         top_p=params[2], block_size=params[3], confidence_thresholds=params[4])
+        reset_context()
+        return pos, tok, cnt
+
+    def call(self, method: str, *args):
+        return getattr(self, method)(*args)
+
+    def exit(self):
+        pass

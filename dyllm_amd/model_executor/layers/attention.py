@@ -54,9 +54,9 @@ class Attention(nn.Module):
         if ctx.is_full:
             o = ops.flash_attn_varlen_func(q, k, v, ctx.cu_seqlens_q, ctx.cu_seqlens_k, ctx.max_seqlen_q,
                                            ctx.max_seqlen_k, softmax_scale=self.scale)
-            self.context_cache.reset_full(o.reshape(o.shape[0], -1), md.running_seqs_tensor,
+            self.context_cache.reset_full(o.flatten(1), md.running_seqs_tensor,
                                           seq_ids_list=md.running_seqs)
-            self.v_cache.reset_full(v.reshape(v.shape[0], -1), md.running_seqs_tensor, seq_ids_list=md.running_seqs)
+            self.v_cache.reset_full(v.flatten(1), md.running_seqs_tensor, seq_ids_list=md.running_seqs)
             self.context_cache.finish(md.finished_seqs)
             self.v_cache.finish(md.finished_seqs)
             return o

@@ -1,0 +1,148 @@
+"""Unmasking sampler (dyllm/model_executor/layers/sampler.py:176-357).
+
+For every running sequence: take the logits of its still-masked positions in the current block,
+apply temperature / top-k / top-p, score every candidate (confidence, margin, random, or
+Dream's negative entropy), order the candidates by score and unmask the first
+``num_transfer`` of them plus every candidate whose score reaches the sequence's confidence
+threshold. Returns ``(positions [B, W], tokens [B, W], counts [B])`` with the kept candidates
+first in each row (W = block width). The work runs as a handful of torch ops on the device; the
+ragged->dense packing and the keep/count filter are index arithmetic on [B, W] tensors.
+
+Tie order: candidates with equal scores keep ascending position order (a stable sort); the
+reference uses an unstable descending sort there (sampler.py:300).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple, Union
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+
+def top_p_logits(logits: torch.Tensor, top_p: Union[float, torch.Tensor, None] = None) -> torch.Tensor:
+    """Nucleus filter per row (sampler.py:183-199)."""
+    if top_p is None:
+        return logits
+    p = top_p if torch.is_tensor(top_p) else torch.full((logits.size(0),), float(top_p), device=logits.device)
+    sorted_logits, sorted_idx = torch.sort(logits, descending=True)
+    cum = torch.cumsum(F.softmax(sorted_logits, dim=-1), dim=-1)
+    drop = cum > p.view(-1, 1).to(cum.dtype)
+    drop[..., 1:] = drop[..., :-1].clone()
+    drop[..., 0] = False
+    mask = torch.zeros_like(logits, dtype=torch.bool).scatter_(-1, sorted_idx, drop)
+    return logits.masked_fill(mask, torch.finfo(logits.dtype).min)
+
+
+def top_k_logits(logits: torch.Tensor, top_k: Union[int, torch.Tensor, None] = None) -> torch.Tensor:
+    """Keep the k largest logits per row (sampler.py:202-211)."""
+    if top_k is None:
+        return logits
+    k = top_k if torch.is_tensor(top_k) else torch.full((logits.size(0),), int(top_k), device=logits.device)
+    kmax = min(int(k.max().item()), logits.size(-1))
+    vals, _ = torch.topk(logits, kmax, dim=-1)
+    thr = vals.gather(1, (k.long() - 1).clamp(0, kmax - 1).unsqueeze(-1))
+    return logits.masked_fill(logits < thr, torch.finfo(logits.dtype).min)
+
+
+class BaseSampler(nn.Module):
+
+    def __init__(self, algorithm: str = "confidence"):
+        super().__init__()
+        self.algorithm = algorithm
+
+    def adjust_logits(self, logits: torch.Tensor) -> torch.Tensor:
+        return logits
+
+    def sample_token(self, probs, top_tokens, temperatures):
+        return top_tokens
+
+    def compute_scores(self, probs: torch.Tensor, top_probs: torch.Tensor) -> torch.Tensor:
+        if self.algorithm == "confidence":
+            return top_probs
+        if self.algorithm == "margin_confidence":
+            top2, _ = probs.topk(k=2, dim=-1)
+            return top2[:, 0] - top2[:, 1]
+        if self.algorithm == "random":
+            return torch.rand_like(top_probs)
+        raise ValueError(f"Unsupported algorithm for LLaDA: {self.algorithm}")
+
+    def forward(self, input_logits: torch.Tensor, ctx, input_indices: Tuple[torch.Tensor, torch.Tensor, torch.Tensor],
+                temperatures: Optional[torch.Tensor] = None, num_transfer: Optional[torch.Tensor] = None,
+                top_k: Optional[torch.Tensor] = None, top_p: Optional[torch.Tensor] = None, block_size: int = 32,
+                confidence_thresholds: Optional[torch.Tensor] = None):
+        logits = self.adjust_logits(input_logits)
+        dev = logits.device
+        rel, offsets, cu = input_indices
+        B = cu.numel() - 1
+        n = rel.numel()
+        counts = cu[1:] - cu[:-1]
+        group = torch.repeat_interleave(torch.arange(B, device=dev), counts.long(), output_size=n)
+        rows = ctx.cu_seqlens_q[:-1].long().index_select(0, group) + rel
+        cand = logits.index_select(0, rows)
+        if temperatures is not None:
+            cand = cand / temperatures.unsqueeze(-1)
+        cand = top_k_logits(cand, top_k)
+        cand = top_p_logits(cand, top_p)
+        probs = F.softmax(cand, dim=-1)
+        top_probs, top_tokens = probs.max(dim=-1)
+        scores = self.compute_scores(probs, top_probs)
+        tokens = self.sample_token(probs, top_tokens, temperatures)
+        pos = rel + offsets.index_select(0, group)
+
+        # ragged -> dense [B, W] (sampler.py:114-175), W = block width
+        W = int(block_size)
+        slot = torch.arange(n, device=dev) - cu[:-1].long().index_select(0, group)
+        inside = slot < W
+        d_scores = torch.full((B, W), float("-inf"), dtype=scores.dtype, device=dev)
+        d_tokens = torch.zeros((B, W), dtype=tokens.dtype, device=dev)
+        d_pos = torch.zeros((B, W), dtype=pos.dtype, device=dev)
+        g, s = group[inside], slot[inside]
+        d_scores[g, s] = scores[inside]
+        d_tokens[g, s] = tokens[inside]
+        d_pos[g, s] = pos[inside]
+
+        s_scores, order = torch.sort(d_scores, dim=1, descending=True, stable=True)
+        s_tokens = d_tokens.gather(1, order)
+        s_pos = d_pos.gather(1, order)
+        if num_transfer is None:
+            nt = torch.zeros(B, dtype=torch.long, device=dev)
+        else:
+            nt = num_transfer.reshape(-1).long().clamp_min(0).to(dev)
+        if confidence_thresholds is None:
+            thr = torch.full((B,), float("inf"), dtype=s_scores.dtype, device=dev)
+        else:
+            thr = confidence_thresholds.to(device=dev, dtype=s_scores.dtype)
+        # keep = top num_transfer, or score >= threshold, and a real candidate (sampler.py:44-86)
+        j = torch.arange(W, device=dev).unsqueeze(0)
+        keep = ((j < nt.unsqueeze(1)) | (s_scores >= thr.unsqueeze(1))) & (s_scores > float("-inf"))
+        out_tokens = torch.where(keep, s_tokens, torch.full_like(s_tokens, -1))
+        out_pos = torch.where(keep, s_pos, torch.zeros_like(s_pos))
+        out_counts = keep.sum(dim=1, dtype=torch.int32)
+        return out_pos, out_tokens, out_counts
+
+
+class LLaDASampler(BaseSampler):
+    pass
+
+
+class DreamSampler(BaseSampler):
+    """Dream predicts token t from position t-1: the logits are shifted by one row over the
+    packed batch (sampler.py:322-326); sampling is categorical when a temperature is set."""
+
+    def adjust_logits(self, logits):
+        if logits.size(0) <= 1:
+            return logits
+        return torch.cat([logits[:1], logits[:-1]], dim=0)
+
+    def sample_token(self, probs, top_tokens, temperatures):
+        if temperatures is not None and bool(torch.any(temperatures > 0)):
+            return torch.multinomial(probs.float(), 1).squeeze(-1)
+        return top_tokens
+
+    def compute_scores(self, probs, top_probs):
+        if self.algorithm == "entropy":
+            return torch.sum(probs * torch.log(probs + 1e-10), dim=-1)
+        if self.algorithm == "origin":
+            return torch.rand_like(top_probs)
+        raise ValueError(f"Unsupported algorithm for Dream: {self.algorithm}")

@@ -8,6 +8,8 @@ path. MLP and Dream/MoE variants share this structure.
 """
 from __future__ import annotations
 
+import re
+
 import torch
 import torch.nn.functional as F
 from torch import nn
@@ -101,6 +103,7 @@ class LLaDAMLP(nn.Module):
             gate_up_events[1].record()
         dest = cm.dest_rows(md.running_seqs_tensor, kidx, count)
         ops.ffn_down(h, self.down_proj, out=cm._slab, out_rows=dest, count=count, hint=hint)
+        cm.finish(md.finished_seqs)
         return self.cache_update.gather_all()
 
 
@@ -108,7 +111,7 @@ class LLaDAAttention(nn.Module):
     """Projections + RoPE + K cache around ``Attention`` (llada.py:46-149)."""
 
     def __init__(self, hidden, num_heads, num_kv_heads, head_dim, max_position, rope_theta, threshold,
-                 qkv_bias=False, device="cuda", gen=None):
+                 qkv_bias=False, qk_layernorm=False, rms_norm_eps=1e-6, device="cuda", gen=None):
         super().__init__()
         self.num_heads, self.num_kv_heads, self.head_dim = num_heads, num_kv_heads, head_dim
         self.q_size, self.kv_size = num_heads * head_dim, num_kv_heads * head_dim
@@ -119,6 +122,9 @@ class LLaDAAttention(nn.Module):
         self.kv_bias = nn.Parameter(torch.zeros(2 * self.kv_size, dtype=torch.bfloat16, device=device),
                                     requires_grad=False) if qkv_bias else None
         self.o_proj = _param(hidden, self.q_size, device=device, gen=gen)
+        # per-head RMSNorm of q and k before RoPE (LLaDA-MoE, lladamoe.py:194-199,227-236)
+        self.q_norm = RMSNorm(head_dim, rms_norm_eps, device=device) if qk_layernorm else None
+        self.k_norm = RMSNorm(head_dim, rms_norm_eps, device=device) if qk_layernorm else None
         self.k_cache = CacheManager(self.kv_size, device=torch.device(device))
         self.rotary = RotaryEmbedding(head_dim, max_position, rope_theta, device=device)
         self.attn = Attention(num_heads, head_dim, head_dim ** -0.5, num_kv_heads, threshold, device=device)
@@ -127,25 +133,33 @@ class LLaDAAttention(nn.Module):
         ctx = get_context()
         md = get_metadata()
         q = F.linear(hidden, self.q_proj, self.q_bias).view(-1, self.num_heads, self.head_dim)
+        if self.q_norm is not None:
+            q = self.q_norm(q)
         q = self.rotary.rotate(positions, q)
         if ctx.is_full:
             kv = F.linear(hidden, self.kv_proj, self.kv_bias)
             k, v = kv.split([self.kv_size, self.kv_size], dim=-1)
-            k = self.rotary.rotate(positions, k.reshape(-1, self.num_kv_heads, self.head_dim))
+            k = k.reshape(-1, self.num_kv_heads, self.head_dim)
+            if self.k_norm is not None:
+                k = self.k_norm(k)
+            k = self.rotary.rotate(positions, k)
             v = v.reshape(-1, self.num_kv_heads, self.head_dim)
-            self.k_cache.reset_full(k.reshape(k.shape[0], -1), md.running_seqs_tensor, seq_ids_list=md.running_seqs)
+            self.k_cache.reset_full(k.flatten(1), md.running_seqs_tensor, seq_ids_list=md.running_seqs)
             o = self.attn(q, k, v)
         else:
             idx = ctx.idx_salient_row
             kv = F.linear(ops.gather_rows_2D(hidden, idx), self.kv_proj, self.kv_bias)
             k, v = kv.split([self.kv_size, self.kv_size], dim=-1)
-            k = self.rotary.rotate(positions[idx], k.reshape(-1, self.num_kv_heads, self.head_dim))
+            k = k.reshape(-1, self.num_kv_heads, self.head_dim)
+            if self.k_norm is not None:
+                k = self.k_norm(k)
+            k = self.rotary.rotate(positions[idx], k)
             v = v.reshape(-1, self.num_kv_heads, self.head_dim)
             kidx = ctx.idx_salient_row_k if ctx.idx_salient_row_k is not None else idx
-            self.k_cache.scatter_update(md.running_seqs_tensor, kidx, k.reshape(k.shape[0], -1))
+            self.k_cache.scatter_update(md.running_seqs_tensor, kidx, k.flatten(1))
             k_full = self.k_cache.get_seqs(md.running_seqs_tensor, md.running_seqs)
             o = self.attn(q, k_full.view(-1, self.num_kv_heads, self.head_dim), v)
-        out = F.linear(o.reshape(o.shape[0], -1), self.o_proj)
+        out = F.linear(o.flatten(1), self.o_proj)
         self.k_cache.finish(md.finished_seqs)
         return out
 
@@ -157,7 +171,8 @@ class LLaDADecoderLayer(nn.Module):
         super().__init__()
         self.self_attn = LLaDAAttention(cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads,
                                         cfg.head_dim, cfg.max_position_embeddings, cfg.rope_theta, threshold,
-                                        qkv_bias=cfg.qkv_bias, device=device, gen=gen)
+                                        qkv_bias=cfg.qkv_bias, qk_layernorm=cfg.qk_layernorm,
+                                        rms_norm_eps=cfg.rms_norm_eps, device=device, gen=gen)
         self.mlp = self._make_mlp(cfg, device, gen)
         self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device=device)
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device=device)
@@ -196,16 +211,50 @@ class LLaDAModel(nn.Module):
         return hidden
 
 
+# LLaDA checkpoint names -> module names (llada.py:223-245): ordered (pattern, replacement)
+_LLADA_RENAMES = [
+    (r"transformer\.blocks\.", "layers."),
+    (r"transformer\.", ""),
+    (r"\bwte\b", "embed_tokens"),
+    (r"\bln_f\b", "norm"),
+    (r"^model\.ff_out\b", "lm_head"),
+    (r"\.(q_proj|k_proj|v_proj)\.", r".self_attn.\1."),
+    (r"\.attn_out\.", ".self_attn.o_proj."),
+    (r"\.ff_out\.", ".mlp.down_proj."),
+    (r"\.ff_proj\.", ".mlp.gate_proj."),
+    (r"\.up_proj\.", ".mlp.up_proj."),
+    (r"\battn_norm\b", "input_layernorm"),
+    (r"\bff_norm\b", "post_attention_layernorm"),
+]
+
+
 class LLaDAForDLM(nn.Module):
+    packed_modules_mapping = {"kv_proj": ["k_proj", "v_proj"], "gate_up_proj": ["gate_proj", "up_proj"]}
+    layer_cls = LLaDADecoderLayer
+
     def __init__(self, cfg, threshold, device="cuda", seed=0):
         super().__init__()
         gen = torch.Generator(device=device).manual_seed(seed)
         self.config = cfg
-        self.model = LLaDAModel(cfg, threshold, device=device, gen=gen)
+        self.model = LLaDAModel(cfg, threshold, device=device, gen=gen, layer_cls=self.layer_cls)
         self.lm_head = _param(cfg.vocab_size, cfg.hidden_size, device=device, gen=gen)
+        if cfg.tie_word_embeddings:
+            self.lm_head.data.copy_(self.model.embed_tokens.data)
 
     def forward(self, input_ids, positions):
         return self.model(input_ids, positions)
+
+    def normalize_weight_name(self, name: str) -> str:
+        if "transformer." not in name:
+            return name
+        for pat, rep in _LLADA_RENAMES:
+            name = re.sub(pat, rep, name)
+        return name
+
+    def load_weights(self, weights):
+        from ...utils.weight_loader import load_weights
+
+        return load_weights(self, weights)
 
     def compute_logits(self, hidden):
         return F.linear(hidden, self.lm_head)

@@ -158,7 +158,7 @@ def attention_colsparse_cached(q, k_cache, kv_start, dv_compact, c_cache, c_star
 
 def v_delta_update(v_cache, v_new, dest_rows):
     """dv = v_new - v_cache[dest_rows]; v_cache[dest_rows] = v_new (attention.py:67-74)."""
-    v_new = v_new.reshape(v_new.shape[0], -1).contiguous()
+    v_new = v_new.flatten(1).contiguous()
     dv = torch.empty_like(v_new)
     if v_new.shape[0]:
         _lib.call("dyllm_v_delta_update", _ptr(v_cache), _ptr(v_new), _ptr(dest_rows), v_new.shape[0],
@@ -363,13 +363,15 @@ def reset_block_cuda(cache, inp, seq_starts, cu_seqlens, cu_seqlens_q, seq_ids, 
 
 def scatter_update_cuda(cache, new_vals, row_idx, cu_seqlens, seq_starts, seq_ids):
     _check_cache(cache, seq_starts, seq_ids)
-    new_vals = new_vals.reshape(new_vals.shape[0], -1).contiguous()
+    new_vals = new_vals.flatten(1).contiguous()
     _check(new_vals, "new_vals", cache.dtype, 2)
     if new_vals.shape[1] != cache.shape[1]:
         raise RuntimeError("new_vals row width must match the cache")
     ri = _i64(row_idx)
     if ri.numel() != new_vals.shape[0]:
         raise RuntimeError("row_idx must have one entry per new row")
+    if ri.numel() == 0:
+        return
     cu = _i32(cu_seqlens)
     _lib.call("dyllm_scatter_update", _ptr(cache), _ptr(new_vals), _row_bytes(cache), _ptr(ri), ri.numel(),
               _ptr(cu), _ptr(seq_starts), _ptr(seq_ids), seq_ids.numel(), _stream())

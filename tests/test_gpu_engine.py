@@ -1,0 +1,53 @@
+"""End-to-end generation on the GPU through ``dLLM.generate`` for the three model families
+(random-initialised shape presets): every step kind runs (full, sparse refresh, sparse
+Q-pruned), every answer position is unmasked, and generation is deterministic."""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(model, prompts, sp, threshold=0.99):
+    from dyllm_amd import dLLM
+
+    eng = dLLM(model, threshold=threshold)
+    out = eng.generate(prompts, sp)
+    torch.cuda.synchronize()
+    return eng, out
+
+
+@pytest.mark.parametrize("model", ["tiny-llada", "tiny-dream", "tiny-llada-moe"])
+def test_generate_all_step_kinds(dev, model):
+    from dyllm_amd import SamplingParams
+
+    print(f"[engine] {model}", flush=True)
+    sp = SamplingParams(max_new_tokens=64, steps=16, num_full_steps=2, block_size=16, temperature=0.0)
+    prompts = [[3, 14, 15, 92, 65], [2, 71, 82, 81, 82, 84, 59], [1] * 12]
+    eng, out = _run(model, prompts, sp)
+    mask = eng.config.mask_id
+    assert len(out) == 3
+    for o, p in zip(out, prompts):
+        ids = o["token_ids"]
+        assert ids[: len(p)] == p
+        assert len(ids) == len(p) + 64
+        # a random-initialised model may itself emit the mask id (the reference does not suppress
+        # it either), so only most answer positions are guaranteed to hold real tokens
+        assert ids[len(p):].count(mask) < 16 or eng.config.eos in ids[len(p):]
+    st = eng.execution_stats
+    assert st["full_forwards"] == 2 and st["sparse_forwards"] >= 6     # refresh and Q-pruned steps ran
+    _, out2 = _run(model, prompts, sp)
+    assert [o["token_ids"] for o in out] == [o["token_ids"] for o in out2]
+
+
+def test_generate_confidence_threshold_and_batches(dev):
+    """Sequences admitted at different times (a new one joins while others are sparse) and the
+    confidence-threshold unmasking rule."""
+    from dyllm_amd import SamplingParams, dLLM
+
+    eng = dLLM("tiny-llada", threshold=0.99, max_num_seqs=2)
+    sp = SamplingParams(max_new_tokens=32, steps=8, num_full_steps=1, block_size=8, temperature=0.0,
+                        confidence_threshold=0.0)      # every candidate qualifies: a block per step
+    out = eng.generate([[5, 6, 7], [8, 9], [10, 11, 12, 13]], sp)
+    for o in out:
+        assert eng.config.mask_id not in o["token_ids"]
+    assert eng.execution_stats["full_forwards"] >= 2
