@@ -103,14 +103,32 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const int32_t* ks_b = a.kslot ? a.kslot + k_beg : nullptr;
   const int nkb = (Lk + kBK - 1) / kBK;
 
-  // register stage of one K/V tile
+  // register stage of one K/V tile. The per-block metadata (salient-key bits, compact dV slot
+  // of each key) is loaded one block before the tile it addresses (into the registers the
+  // previous fetch has just consumed), so the dependent V loads are issued without waiting.
   uint4 kreg[KCH];
   uint4 vreg[VIT][4];
   uint64_t mask_next = ~0ull;
+  uint64_t meta_bm = ~0ull;
+  int meta_slot[VIT][4];
+  auto load_meta = [&](int kb) {
+    if constexpr (MODE != AttnMode::ColSparse) return;
+    if (kb >= nkb) return;
+    const int key0 = kb * kBK;
+    if constexpr (MODE == AttnMode::ColSparse) meta_bm = a.kmask[int64_t(b) * a.nblk + kb];
+#pragma unroll
+    for (int it = 0; it < VIT; ++it) {
+      const int kq = (tid + NT * it) & 15;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = key0 + 4 * kq + j;
+        meta_slot[it][j] = (r >= Lk) ? -1 : (ks_b ? ks_b[r] : r);
+      }
+    }
+  };
   auto fetch = [&](int kb) {
     const int key0 = kb * kBK;
-    uint64_t bm = ~0ull;
-    if constexpr (MODE == AttnMode::ColSparse) bm = a.kmask[int64_t(b) * a.nblk + kb];
+    const uint64_t bm = meta_bm;
     mask_next = bm;
 #pragma unroll
     for (int it = 0; it < KCH; ++it) {
@@ -123,12 +141,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
       for (int it = 0; it < VIT; ++it) {
         const int c = tid + NT * it;
-        const int kq = c & 15, dc = c >> 4;
+        const int dc = c >> 4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          int64_t r = key0 + 4 * kq + j;
-          if (r >= Lk) r = -1;
-          else if (ks_b) r = ks_b[r];
+          int64_t r;
+          if constexpr (MODE == AttnMode::ColSparse) {
+            r = meta_slot[it][j];
+          } else {
+            r = key0 + 4 * ((tid + NT * it) & 15) + j;
+            if (r >= Lk) r = -1;
+          }
           vreg[it][j] = (r >= 0) ? *reinterpret_cast<const uint4*>(Vb + r * ldkv + dc * 8) : make_uint4(0, 0, 0, 0);
         }
       }
@@ -165,13 +187,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
   };
 
+  load_meta(0);
   if (nkb > 0) fetch(0);
+  load_meta(1);
   for (int kb = 0; kb < nkb; ++kb) {
     const int key0 = kb * kBK;
     const uint64_t bmask = mask_next;
     stage();
     __syncthreads();
     if (kb + 1 < nkb) fetch(kb + 1);
+    load_meta(kb + 2);
 
     // ---- S^T = K Q^T for two 32-key tiles --------------------------------------------
     f32x16_t s_acc[2];
