@@ -426,6 +426,87 @@ int launch_seq_row_starts(const int64_t* seq_starts, const int64_t* seq_ids, con
   return check_launch("seq_row_starts_kernel");
 }
 
+// ---- native sparse step: preparation and per-salient-row work -----------------------------
+__global__ __launch_bounds__(256) void step_prep_kernel(StepPrepArgs a) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < a.Tq) a.slot[i] = -1;
+  if (i < a.nmask) a.kmask[i] = 0;
+  if (i < a.Tk) a.kslot[i] = -1;
+  if (i < a.B) {
+    const int64_t sid = a.seq_ids[i];
+    a.v_start[i] = a.v_seq_starts[sid];
+    int64_t c = a.c_seq_starts[sid];
+    if (a.q_pruned) c += int64_t(a.cu_k[i + 1] - a.cu_k[i]) - int64_t(a.cu_q[i + 1] - a.cu_q[i]);
+    a.c_start[i] = c;
+  }
+  if (i == 0) *a.done = 0u;
+}
+
+int launch_step_prep(const StepPrepArgs& a, hipStream_t s) {
+  int64_t n = a.Tq > a.nmask ? a.Tq : a.nmask;
+  if (a.Tk > n) n = a.Tk;
+  if (a.B > n) n = a.B;
+  if (n < 1) n = 1;
+  step_prep_kernel<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(a);
+  return check_launch("step_prep_kernel");
+}
+
+// one wavefront per salient row j: its V-cache row, dV and V-cache update (16-byte lanes), and
+// lane 0 records the row in the slot maps and the salient-key bit of its 64-key block
+__global__ __launch_bounds__(256) void step_salient_kernel(uint16_t* __restrict__ v_cache,
+                                                           const uint16_t* __restrict__ v_new,
+                                                           uint16_t* __restrict__ dv, int64_t row_elems,
+                                                           const int64_t* __restrict__ idx_k64,
+                                                           const int32_t* __restrict__ idx_q32, int n,
+                                                           const int32_t* __restrict__ cu_k, int B, int nblk,
+                                                           const int64_t* __restrict__ v_seq_starts,
+                                                           const int64_t* __restrict__ seq_ids,
+                                                           int32_t* __restrict__ slot,
+                                                           unsigned long long* __restrict__ kmask,
+                                                           int32_t* __restrict__ kslot) {
+  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (j >= n) return;
+  const int64_t k = idx_k64[j];
+  const int bq = find_segment(cu_k, B + 1, k);
+  const int b = bq < B ? bq : B - 1;
+  const int64_t off = k - cu_k[b];
+  const int64_t dest = v_seq_starts[seq_ids[b]] + off;
+  uint4* cr = reinterpret_cast<uint4*>(v_cache + dest * row_elems);
+  const uint4* nr = reinterpret_cast<const uint4*>(v_new + int64_t(j) * row_elems);
+  uint4* dr = reinterpret_cast<uint4*>(dv + int64_t(j) * row_elems);
+  for (int64_t i = lane; i < row_elems / 8; i += 64) {
+    const uint4 o = cr[i], nw = nr[i];
+    const uint32_t ov[4] = {o.x, o.y, o.z, o.w}, nv[4] = {nw.x, nw.y, nw.z, nw.w};
+    uint32_t d[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = __fsub_rn(__uint_as_float(nv[e] << 16), __uint_as_float(ov[e] << 16));
+      const float hi = __fsub_rn(__uint_as_float(nv[e] & 0xffff0000u), __uint_as_float(ov[e] & 0xffff0000u));
+      d[e] = pack_bf16x2(lo, hi);
+    }
+    dr[i] = make_uint4(d[0], d[1], d[2], d[3]);
+    cr[i] = nw;
+  }
+  if (lane == 0) {
+    slot[idx_q32[j]] = j;
+    kslot[k] = j;
+    if (bq < B && off < cu_k[b + 1] - cu_k[b]) atomicOr(&kmask[int64_t(b) * nblk + off / kBK], 1ull << (off % kBK));
+  }
+}
+
+int launch_step_salient(uint16_t* v_cache, const uint16_t* v_new, uint16_t* dv, int64_t row_elems,
+                        const int64_t* idx_k64, const int32_t* idx_q32, int n, const int32_t* cu_k, int B, int nblk,
+                        const int64_t* v_seq_starts, const int64_t* seq_ids, int32_t* slot, uint64_t* kmask,
+                        int32_t* kslot, hipStream_t s) {
+  DYLLM_REQUIRE(row_elems % 8 == 0, "V row width must be a multiple of 8");
+  if (n <= 0) return 0;
+  step_salient_kernel<<<unsigned(cdiv(n, 4)), 256, 0, s>>>(v_cache, v_new, dv, row_elems, idx_k64, idx_q32, n, cu_k,
+                                                            B, nblk, v_seq_starts, seq_ids, slot,
+                                                            reinterpret_cast<unsigned long long*>(kmask), kslot);
+  return check_launch("step_salient_kernel");
+}
+
 template <AttnMode MODE, int NW>
 static void launch_mode(const AttnArgs& a, int max_rows_per_seq, hipStream_t s) {
   AttnArgs g = a;

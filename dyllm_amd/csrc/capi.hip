@@ -49,13 +49,35 @@ size_t dyllm_attention_colsparse_workspace_bytes(int batch, int num_heads, int64
 }
 
 // Shared body of the two column-sparse entry points. kslot_bytes > 0 selects a compact dV.
+// workspace layout of the column-sparse attention: slot map [Tq], salient-key bits [B][nblk],
+// per-head statistics [H][3][Tq], dV slot map [Tk] (compact dV only)
+struct ColsWs {
+  int32_t* slot;
+  uint64_t* kmask;
+  float* part;
+  int32_t* kslot;
+};
+static ColsWs cols_ws(void* workspace, int batch, int num_heads, int64_t total_q, int nblk, bool compact_dv) {
+  char* ws = static_cast<char*>(workspace);
+  ColsWs w{};
+  w.slot = reinterpret_cast<int32_t*>(ws);
+  ws += align256(size_t(total_q) * 4);
+  w.kmask = reinterpret_cast<uint64_t*>(ws);
+  ws += align256(size_t(batch) * nblk * 8);
+  w.part = reinterpret_cast<float*>(ws);
+  ws += align256(size_t(num_heads) * 3 * size_t(total_q) * 4);
+  w.kslot = compact_dv ? reinterpret_cast<int32_t*>(ws) : nullptr;
+  return w;
+}
+
 static int colsparse_impl(const void* q, const void* k, const int64_t* kv_start, const void* v_delta,
                           const void* c, const int64_t* c_start, int c_inplace, const void* o_sal, void* o, int batch,
                           int num_heads, int num_kv_heads, int head_dim, const int32_t* cu_seqlens_q,
                           const int32_t* cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, int64_t total_q,
                           int64_t total_k, int num_salient, const int32_t* idx_salient_q,
                           const int32_t* idx_salient_k, float* cosine_stats, uint8_t* cosine_out, float threshold,
-                          void* workspace, size_t workspace_bytes, bool compact_dv, void* stream) {
+                          void* workspace, size_t workspace_bytes, bool compact_dv, void* stream,
+                          bool maps_ready = false, bool reduce = true) {
   DYLLM_NONNULL(q);
   DYLLM_NONNULL(k);
   DYLLM_NONNULL(c);
@@ -81,18 +103,17 @@ static int colsparse_impl(const void* q, const void* k, const int64_t* kv_start,
   DYLLM_REQUIRE(workspace && workspace_bytes >= need,
                 "workspace too small: need " + std::to_string(need) + " bytes");
   const hipStream_t s = DYLLM_STREAM(stream);
-  char* ws = static_cast<char*>(workspace);
   const int nblk = int(cdiv(max_seqlen_k, 64));
-  int32_t* slot = reinterpret_cast<int32_t*>(ws);
-  ws += align256(size_t(total_q) * 4);
-  uint64_t* kmask = reinterpret_cast<uint64_t*>(ws);
-  ws += align256(size_t(batch) * nblk * 8);
-  float* part = reinterpret_cast<float*>(ws);
-  ws += align256(size_t(num_heads) * 3 * size_t(total_q) * 4);
-  int32_t* kslot = compact_dv ? reinterpret_cast<int32_t*>(ws) : nullptr;
-  if (int rc = launch_colsparse_prep(idx_salient_q, idx_salient_k ? idx_salient_k : idx_salient_q, num_salient,
-                                     cu_seqlens_k, batch, nblk, slot, total_q, kmask, kslot, total_k, s))
-    return rc;
+  const ColsWs cw = cols_ws(workspace, batch, num_heads, total_q, nblk, compact_dv);
+  int32_t* slot = cw.slot;
+  uint64_t* kmask = cw.kmask;
+  float* part = cw.part;
+  int32_t* kslot = cw.kslot;
+  if (!maps_ready) {
+    if (int rc = launch_colsparse_prep(idx_salient_q, idx_salient_k ? idx_salient_k : idx_salient_q, num_salient,
+                                       cu_seqlens_k, batch, nblk, slot, total_q, kmask, kslot, total_k, s))
+      return rc;
+  }
   AttnArgs a{};
   a.Q = static_cast<const uint16_t*>(q);
   a.K = static_cast<const uint16_t*>(k);
@@ -117,6 +138,7 @@ static int colsparse_impl(const void* q, const void* k, const int64_t* kv_start,
   // the reference uses rsqrt(head_dim) here, not the layer's scale (sm80.cu:166-168)
   a.scale_log2 = (1.0f / sqrtf(float(head_dim))) * kLog2e;
   if (int rc = launch_attention(AttnMode::ColSparse, a, max_seqlen_q, s)) return rc;
+  if (!reduce) return 0;
   return launch_saliency_reduce(part, cosine_stats, cosine_out, total_q, num_heads, threshold, s);
 }
 
@@ -153,7 +175,7 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
 size_t dyllm_sparse_step_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim, int64_t total_q,
                                          int64_t total_k, int max_seqlen_k, int64_t num_salient) {
   const size_t n = size_t(num_salient > 0 ? num_salient : 0);
-  return align256(n * 8) + align256(n * num_kv_heads * head_dim * 2) + align256(n * num_heads * head_dim * 2) +
+  return 256 + align256(n * num_kv_heads * head_dim * 2) + align256(n * num_heads * head_dim * 2) +
          2 * align256(size_t(batch) * 8) +
          dyllm_attention_colsparse_workspace_bytes(batch, num_heads, total_q, total_k, max_seqlen_k);
 }
@@ -187,8 +209,8 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
   const hipStream_t s = DYLLM_STREAM(stream);
   const size_t n = size_t(num_salient);
   char* ws = static_cast<char*>(workspace);
-  int64_t* dest = reinterpret_cast<int64_t*>(ws);
-  ws += align256(n * 8);
+  uint32_t* done = reinterpret_cast<uint32_t*>(ws);  // completion counter of the statistics reduction
+  ws += 256;
   uint16_t* dv = reinterpret_cast<uint16_t*>(ws);
   ws += align256(n * num_kv_heads * head_dim * 2);
   uint16_t* o_sal = reinterpret_cast<uint16_t*>(ws);
@@ -200,16 +222,34 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
   const size_t cs_bytes = workspace_bytes - size_t(ws - static_cast<char*>(workspace));
   const bool q_pruned = cu_promptlens != nullptr;
 
+  // reset the maps, first V-cache / context-cache row of every sequence (one launch)
+  const int nblk = int(cdiv(max_seqlen_k, 64));
+  const ColsWs cw = cols_ws(ws, batch, num_heads, total_q, nblk, true);
+  StepPrepArgs pa{};
+  pa.slot = cw.slot;
+  pa.Tq = total_q;
+  pa.kmask = cw.kmask;
+  pa.nmask = int64_t(batch) * nblk;
+  pa.kslot = cw.kslot;
+  pa.Tk = total_k;
+  pa.v_seq_starts = v_seq_starts;
+  pa.c_seq_starts = c_seq_starts;
+  pa.seq_ids = seq_ids;
+  pa.cu_k = cu_seqlens_k;
+  pa.cu_q = cu_seqlens_q;
+  pa.q_pruned = q_pruned ? 1 : 0;
+  pa.B = batch;
+  pa.v_start = v_start;
+  pa.c_start = c_start;
+  pa.done = done;
+  if (int rc = launch_step_prep(pa, s)) return rc;
   if (num_salient > 0) {
-    // dV of the salient keys + V-cache update (attention.py:67-74, 89-96)
-    if (int rc = launch_scatter_dest_rows(idx_k64, num_salient, nullptr, cu_seqlens_k, v_seq_starts, seq_ids, batch,
-                                          dest, s))
-      return rc;
-    if (int rc = launch_v_delta_update(static_cast<uint16_t*>(v_cache), static_cast<const uint16_t*>(v_new), dest,
-                                       num_salient, int64_t(num_kv_heads) * head_dim, dv, s))
+    // dV of the salient keys + V-cache update (attention.py:67-74, 89-96) and the salient maps
+    if (int rc = launch_step_salient(static_cast<uint16_t*>(v_cache), static_cast<const uint16_t*>(v_new), dv,
+                                     int64_t(num_kv_heads) * head_dim, idx_k64, idx_q32, num_salient, cu_seqlens_k,
+                                     batch, nblk, v_seq_starts, seq_ids, cw.slot, cw.kmask, cw.kslot, s))
       return rc;
     // row-sparse attention of the salient queries vs the full cached K/V (attention.py:76-87)
-    if (int rc = launch_seq_row_starts(v_seq_starts, seq_ids, cu_seqlens_k, nullptr, batch, v_start, s)) return rc;
     AttnArgs a{};
     a.Q = static_cast<const uint16_t*>(q);
     a.K = static_cast<const uint16_t*>(k);
@@ -228,18 +268,15 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
       return rc;
   }
   // column-sparse attention + statistics + tau test, context cache updated in place
-  if (int rc = launch_seq_row_starts(c_seq_starts, seq_ids, cu_seqlens_k, q_pruned ? cu_seqlens_q : nullptr, batch,
-                                     c_start, s))
-    return rc;
   if (int rc = colsparse_impl(q, k, k_start, num_salient ? dv : nullptr, c_cache, c_start, 1, o_sal, out, batch,
                               num_heads, num_kv_heads, head_dim, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                               max_seqlen_k, total_q, total_k, num_salient, idx_q32, idx_k32, cosine_stats,
-                              cosine_out, threshold, ws, cs_bytes, true, stream))
+                              cosine_out, threshold, ws, cs_bytes, true, stream, true, false))
     return rc;
-  // compaction of the next salient set (attention.py:147-173)
-  return launch_compact(cosine_out, total_q, cu_seqlens_q, batch, cu_promptlens, next_idx64, next_idx32,
-                        q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr, next_cu_salientlens,
-                        next_count, s);
+  // statistics reduction, tau test and compaction of the next salient set (attention.py:141-173)
+  return launch_reduce_compact(cw.part, cosine_stats, cosine_out, total_q, num_heads, threshold, done, cu_seqlens_q,
+                               batch, cu_promptlens, next_idx64, next_idx32, q_pruned ? next_idx_k64 : nullptr,
+                               q_pruned ? next_idx_k32 : nullptr, next_cu_salientlens, next_count, s);
 }
 
 int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,

@@ -29,6 +29,12 @@ int launch_saliency_reduce(const float* part, float* stats, uint8_t* mask, int64
 int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
                    int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
                    hipStream_t s);
+// statistics reduction + tau test + compaction in one launch (the completion counter must be
+// zero on entry; it is zero again on exit)
+int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
+                          uint32_t* done, const int32_t* cu_q, int B, const int32_t* cu_prompt, int64_t* idx64,
+                          int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
+                          hipStream_t s);
 int launch_fused_offset(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_prompt,
                         const int32_t* cu_sal, int groups, int64_t* out, int64_t cap, hipStream_t s);
 
@@ -61,6 +67,33 @@ int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hip
 int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal, const int32_t* cu_k, int B,
                           int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, int32_t* kslot, int64_t Tk,
                           hipStream_t s);
+// Native sparse step, preparation (one launch): slot / salient-key maps reset, first V-cache
+// and context-cache row of every sequence, completion counter of the reduce kernel zeroed.
+struct StepPrepArgs {
+  int32_t* slot;                // [Tq] -> -1
+  int64_t Tq;
+  uint64_t* kmask;              // [nmask] -> 0
+  int64_t nmask;
+  int32_t* kslot;               // [Tk] -> -1
+  int64_t Tk;
+  const int64_t* v_seq_starts;  // V-cache first row per sequence id
+  const int64_t* c_seq_starts;  // context-cache first row per sequence id
+  const int64_t* seq_ids;       // [B]
+  const int32_t* cu_k;          // [B+1]
+  const int32_t* cu_q;          // [B+1] (Q-pruned: the context rows start at the queried tail block)
+  int q_pruned;
+  int B;
+  int64_t* v_start;             // [B] out
+  int64_t* c_start;             // [B] out
+  uint32_t* done;               // -> 0
+};
+int launch_step_prep(const StepPrepArgs& a, hipStream_t s);
+// Native sparse step, per salient row (one launch): dV = bf16(v_new - v_cache[row]), V-cache
+// update, and the slot / salient-key-bit / dV-slot maps of the column-sparse kernel.
+int launch_step_salient(uint16_t* v_cache, const uint16_t* v_new, uint16_t* dv, int64_t row_elems,
+                        const int64_t* idx_k64, const int32_t* idx_q32, int n, const int32_t* cu_k, int B, int nblk,
+                        const int64_t* v_seq_starts, const int64_t* seq_ids, int32_t* slot, uint64_t* kmask,
+                        int32_t* kslot, hipStream_t s);
 int launch_v_delta_update(uint16_t* v_cache, const uint16_t* v_new, const int64_t* dest_rows, int64_t n,
                           int64_t row_elems, uint16_t* dv, hipStream_t s);
 int launch_seq_row_starts(const int64_t* seq_starts, const int64_t* seq_ids, const int32_t* cu_k,

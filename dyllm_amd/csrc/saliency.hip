@@ -90,6 +90,7 @@ __global__ __launch_bounds__(256) void saliency_reduce_kernel(const float* __res
   const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (t >= T) return;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll 8
   for (int h = 0; h < H; ++h) {
     s0 += part[(int64_t(h) * 3 + 0) * T + t];
     s1 += part[(int64_t(h) * 3 + 1) * T + t];
@@ -116,7 +117,7 @@ int launch_saliency_reduce(const float* part, float* stats, uint8_t* mask, int64
 constexpr int kCompactThreads = 1024;
 constexpr int kCompactItems = 16;
 
-__global__ __launch_bounds__(kCompactThreads) void compact_kernel(
+__device__ __forceinline__ void compact_block(
     const uint8_t* __restrict__ mask, int64_t T, const int32_t* __restrict__ cu_q, int B,
     const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64, int32_t* __restrict__ idx32,
     int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32, int32_t* __restrict__ cu_sal,
@@ -207,6 +208,62 @@ __global__ __launch_bounds__(kCompactThreads) void compact_kernel(
     idx_k[t] = kk;
     if (idx_k32) idx_k32[t] = int32_t(kk);
   }
+}
+
+__global__ __launch_bounds__(kCompactThreads) void compact_kernel(
+    const uint8_t* __restrict__ mask, int64_t T, const int32_t* __restrict__ cu_q, int B,
+    const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64, int32_t* __restrict__ idx32,
+    int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32, int32_t* __restrict__ cu_sal,
+    int32_t* __restrict__ count) {
+  compact_block(mask, T, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count);
+}
+
+// ---- statistics reduction + compaction in one launch ---------------------------------
+// Every workgroup reduces the per-head partial statistics of 1024 rows (heads summed in
+// ascending order) and writes the statistics and the tau decision; the workgroup that finishes
+// last (completion counter, device-scope fences on both sides) then compacts the whole mask.
+// The counter is zeroed by the step's preparation kernel and reset here after use.
+__global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
+    const float* __restrict__ part, float* __restrict__ stats, uint8_t* __restrict__ mask, int64_t T, int H,
+    float tau, uint32_t* __restrict__ done, const int32_t* __restrict__ cu_q, int B,
+    const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64, int32_t* __restrict__ idx32,
+    int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32, int32_t* __restrict__ cu_sal,
+    int32_t* __restrict__ count) {
+  __shared__ int last_sh;
+  const int64_t t = int64_t(blockIdx.x) * kCompactThreads + threadIdx.x;
+  if (t < T) {
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll 8
+    for (int h = 0; h < H; ++h) {
+      s0 += part[(int64_t(h) * 3 + 0) * T + t];
+      s1 += part[(int64_t(h) * 3 + 1) * T + t];
+      s2 += part[(int64_t(h) * 3 + 2) * T + t];
+    }
+    stats[3 * t] = s0;
+    stats[3 * t + 1] = s1;
+    stats[3 * t + 2] = s2;
+    mask[t] = tau_cos(s0, s1, s2) < tau;
+  }
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) last_sh = (atomicAdd(done, 1u) == gridDim.x - 1) ? 1 : 0;
+  __syncthreads();
+  if (!last_sh) return;
+  __threadfence();
+  compact_block(mask, T, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count);
+  if (threadIdx.x == 0) *done = 0u;
+}
+
+int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
+                          uint32_t* done, const int32_t* cu_q, int B, const int32_t* cu_prompt, int64_t* idx64,
+                          int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
+                          hipStream_t s) {
+  DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
+  DYLLM_REQUIRE(T >= 1 && T < (int64_t(1) << 31), "row count out of range");
+  DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
+  reduce_compact_kernel<<<unsigned(cdiv(T, kCompactThreads)), kCompactThreads, 0, s>>>(
+      part, stats, mask, T, H, tau, done, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count);
+  return check_launch("reduce_compact_kernel");
 }
 
 int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
