@@ -190,8 +190,8 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                 const int64_t* idx_k64, const int32_t* idx_k32, float softmax_scale, float threshold,
                                 void* out, float* cosine_stats, uint8_t* cosine_out, int64_t* next_idx64,
                                 int32_t* next_idx32, int64_t* next_idx_k64, int32_t* next_idx_k32,
-                                int32_t* next_cu_salientlens, int32_t* next_count, void* workspace,
-                                size_t workspace_bytes, void* stream) {
+                                int32_t* next_cu_salientlens, int32_t* next_count, int32_t* host_meta,
+                                void* workspace, size_t workspace_bytes, void* stream) {
   DYLLM_NONNULL(v_cache);
   DYLLM_NONNULL(v_seq_starts);
   DYLLM_NONNULL(c_seq_starts);
@@ -207,6 +207,13 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                                         max_seqlen_k, num_salient);
   DYLLM_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need " + std::to_string(need) + " bytes");
   const hipStream_t s = DYLLM_STREAM(stream);
+  int32_t* host_meta_dev = nullptr;
+  if (host_meta) {
+    void* p = nullptr;
+    DYLLM_REQUIRE(hipHostGetDevicePointer(&p, host_meta, 0) == hipSuccess && p != nullptr,
+                  "host_meta must be pinned host memory (hipHostMalloc)");
+    host_meta_dev = static_cast<int32_t*>(p);
+  }
   const size_t n = size_t(num_salient);
   char* ws = static_cast<char*>(workspace);
   uint32_t* done = reinterpret_cast<uint32_t*>(ws);  // completion counter of the statistics reduction
@@ -276,7 +283,7 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
   // statistics reduction, tau test and compaction of the next salient set (attention.py:141-173)
   return launch_reduce_compact(cw.part, cosine_stats, cosine_out, total_q, num_heads, threshold, done, cu_seqlens_q,
                                batch, cu_promptlens, next_idx64, next_idx32, q_pruned ? next_idx_k64 : nullptr,
-                               q_pruned ? next_idx_k32 : nullptr, next_cu_salientlens, next_count, s);
+                               q_pruned ? next_idx_k32 : nullptr, next_cu_salientlens, next_count, host_meta_dev, s);
 }
 
 int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,

@@ -34,7 +34,7 @@ int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, c
 int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
                           uint32_t* done, const int32_t* cu_q, int B, const int32_t* cu_prompt, int64_t* idx64,
                           int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
-                          hipStream_t s);
+                          int32_t* host_meta, hipStream_t s);
 int launch_fused_offset(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_prompt,
                         const int32_t* cu_sal, int groups, int64_t* out, int64_t cap, hipStream_t s);
 

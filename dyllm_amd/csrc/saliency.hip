@@ -228,7 +228,7 @@ __global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
     float tau, uint32_t* __restrict__ done, const int32_t* __restrict__ cu_q, int B,
     const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64, int32_t* __restrict__ idx32,
     int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32, int32_t* __restrict__ cu_sal,
-    int32_t* __restrict__ count) {
+    int32_t* __restrict__ count, int32_t* __restrict__ host_meta) {
   __shared__ int last_sh;
   const int64_t t = int64_t(blockIdx.x) * kCompactThreads + threadIdx.x;
   if (t < T) {
@@ -251,18 +251,26 @@ __global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
   if (!last_sh) return;
   __threadfence();
   compact_block(mask, T, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count);
+  if (host_meta) {
+    // [count, cu_salientlens...] straight into pinned host memory: the host reads the salient
+    // count once this kernel has completed, with no device->host copy behind it
+    __syncthreads();
+    for (int b = threadIdx.x; b <= B; b += kCompactThreads) host_meta[1 + b] = cu_sal[b];
+    if (threadIdx.x == 0) host_meta[0] = count[0];
+    __threadfence_system();
+  }
   if (threadIdx.x == 0) *done = 0u;
 }
 
 int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
                           uint32_t* done, const int32_t* cu_q, int B, const int32_t* cu_prompt, int64_t* idx64,
                           int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
-                          hipStream_t s) {
+                          int32_t* host_meta, hipStream_t s) {
   DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
   DYLLM_REQUIRE(T >= 1 && T < (int64_t(1) << 31), "row count out of range");
   DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
   reduce_compact_kernel<<<unsigned(cdiv(T, kCompactThreads)), kCompactThreads, 0, s>>>(
-      part, stats, mask, T, H, tau, done, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count);
+      part, stats, mask, T, H, tau, done, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count, host_meta);
   return check_launch("reduce_compact_kernel");
 }
 

@@ -209,8 +209,9 @@ class Compacted:
         self.host_meta, self.event = host_meta, event
 
     def host(self):
-        """(count, cu_salientlens as a list): one device->host read for both. With a pinned
-        copy in flight (host_meta + event) only that copy is waited for, not the whole stream."""
+        """(count, cu_salientlens as a list): one device->host read for both. When the producing
+        kernel writes them into pinned host memory (host_meta + event), only that kernel's
+        completion is waited for, not the whole stream."""
         if self.event is not None:
             self.event.synchronize()
             h = self.host_meta.tolist()
@@ -286,9 +287,9 @@ def sparse_attention_step(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_s
               int(total_k), int(n_sal), int(max_salientlen), _ptr(cu_salientlens), _ptr(idx_q32), _ptr(idx_k64),
               _ptr(idx_k32), float(softmax_scale), float(threshold), _ptr(bufs.out), _ptr(bufs.stats),
               _ptr(bufs.mask), _ptr(bufs.idx64), _ptr(bufs.idx32), _ptr(bufs.idx_k64), _ptr(bufs.idx_k32),
-              _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(bufs.ws), bufs.ws_bytes, _stream())
-    # the salient count and per-sequence prefix go to pinned memory right behind the compaction
-    bufs.host_meta.copy_(bufs.meta, non_blocking=True)
+              _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(bufs.host_meta), _ptr(bufs.ws), bufs.ws_bytes, _stream())
+    # the compaction kernel writes the salient count and per-sequence prefix straight into the
+    # pinned host buffer; the event marks when the host may read it
     bufs.event.record()
     return bufs
 

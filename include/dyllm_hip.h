@@ -97,8 +97,8 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
                                      float* cosine_stats, uint8_t* cosine_out, float threshold, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
-/* The whole sparse branch of Attention.forward (attention.py:64-178) in one call, so the
- * ~10 launches of a layer leave the host back to back: dV + V-cache update of the salient keys
+/* The whole sparse branch of Attention.forward (attention.py:64-178) in one call (five
+ * launches that leave the host back to back): dV + V-cache update of the salient keys
  * (v_new rows follow idx_k64), row-sparse attention of the salient queries against the cached
  * K/V, column-sparse attention with statistics and the tau test (context cache updated in place,
  * new rows also written to `out` [total_q, H, D]), and compaction of the next salient set into
@@ -106,7 +106,10 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
  * (k_start == NULL) or read from a cache through per-sequence first rows k_start[b]; the V and
  * context caches are addressed through their seq_start tables (indexed by seq_ids[b]).
  * cu_promptlens != NULL selects a Q-pruned step (Q rows are the response rows; the next set is
- * also produced in K space); otherwise Q space == K space and idx_k* = idx_q*. */
+ * also produced in K space); otherwise Q space == K space and idx_k* = idx_q*.
+ * host_meta (optional, pinned host memory of batch + 2 int32 from hipHostMalloc) receives
+ * [next_count, next_cu_salientlens...] directly from the compaction kernel, so the host can read
+ * the salient count as soon as the call's work has completed without a device->host copy. */
 size_t dyllm_sparse_step_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim, int64_t total_q,
                                          int64_t total_k, int max_seqlen_k, int64_t num_salient);
 int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_start, void* v_cache,
@@ -119,8 +122,8 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                 const int64_t* idx_k64, const int32_t* idx_k32, float softmax_scale, float threshold,
                                 void* out, float* cosine_stats, uint8_t* cosine_out, int64_t* next_idx64,
                                 int32_t* next_idx32, int64_t* next_idx_k64, int32_t* next_idx_k32,
-                                int32_t* next_cu_salientlens, int32_t* next_count, void* workspace,
-                                size_t workspace_bytes, void* stream);
+                                int32_t* next_cu_salientlens, int32_t* next_count, int32_t* host_meta,
+                                void* workspace, size_t workspace_bytes, void* stream);
 
 /* dV and V-cache update of attention.py:67-74 (dv = v_new - v_cache[row]; v_cache[row] = v_new)
  * for compact rows; dest_rows are cache rows (dyllm_scatter_dest_rows). */
