@@ -45,19 +45,21 @@ union Pack4 {
   uint2 d;
 };
 
+__device__ __forceinline__ int xcd_remap(int wg, int nwg) {
+  return ((nwg & 7) == 0) ? (wg & 7) * (nwg >> 3) + (wg >> 3) : wg;
+}
+
+// One (sequence, head, query tile) of NW*32 rows. wg is the tile index after the XCD remap
+// (all query tiles of one (sequence, kv-head) land on the same XCD and share its L2).
 template <AttnMode MODE, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_kernel(AttnArgs a) {
+__device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16_t* __restrict__ k_lds,
+                                               uint16_t* __restrict__ vt_lds) {
   constexpr int NT = NW * 64;              // threads
   constexpr int BQ = NW * 32;              // query rows per workgroup
   constexpr int KCH = kBK * kD / 8 / NT;   // 16-byte K chunks per thread per tile
   constexpr int VIT = (kBK / 4) * (kD / 8) / NT;  // (4 keys x 8 d) V items per thread per tile
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
 
-  // ---- workgroup -> (seq, head, tile), XCD-aware ------------------------------------
-  const int nwg = gridDim.x;
-  int wg = blockIdx.x;
-  if ((nwg & 7) == 0) wg = (wg & 7) * (nwg >> 3) + (wg >> 3);
+  // ---- tile -> (seq, head, query tile) ----------------------------------------------
   const int tile = wg % a.tiles_per_seq;
   const int head = (wg / a.tiles_per_seq) % a.H;
   const int b = wg / (a.tiles_per_seq * a.H);
@@ -282,6 +284,49 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // ---- epilogue ---------------------------------------------------------------------------
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = 1.0f / l_tot;
+  if constexpr (MODE == AttnMode::RowSparse) {
+    if (a.cu_q) {
+      // fused step: the salient row's final output. O[qrow] = bf16(o), the context cache row
+      // rewritten, statistics from the bf16 output vs the cached row (attention_aux_kernels.cu:22-72)
+      float dot = 0.f, nn = 0.f, oo = 0.f;
+      if (row_ok) {
+        const int64_t crow = a.c_start[b] + (qrow - a.cu_q[b]);
+        uint16_t* cp = const_cast<uint16_t*>(a.C) + crow * ldq + head * kD + half * 4;
+        uint16_t* op = a.O + qrow * ldq + head * kD + half * 4;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int off = dt * 32 + g * 8;
+            const uint2 cv = *reinterpret_cast<const uint2*>(cp + off);
+            const float old[4] = {__uint_as_float(cv.x << 16), __uint_as_float(cv.x & 0xffff0000u),
+                                  __uint_as_float(cv.y << 16), __uint_as_float(cv.y & 0xffff0000u)};
+            uint2 st;
+            st.x = pack_bf16x2(o_acc[dt][4 * g] * inv, o_acc[dt][4 * g + 1] * inv);
+            st.y = pack_bf16x2(o_acc[dt][4 * g + 2] * inv, o_acc[dt][4 * g + 3] * inv);
+            const float nw[4] = {__uint_as_float(st.x << 16), __uint_as_float(st.x & 0xffff0000u),
+                                 __uint_as_float(st.y << 16), __uint_as_float(st.y & 0xffff0000u)};
+            *reinterpret_cast<uint2*>(op + off) = st;
+            if (a.c_inplace) *reinterpret_cast<uint2*>(cp + off) = st;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              dot += nw[j] * old[j];
+              nn += nw[j] * nw[j];
+              oo += old[j] * old[j];
+            }
+          }
+      }
+      dot += __shfl_xor(dot, 32, 64);
+      nn += __shfl_xor(nn, 32, 64);
+      oo += __shfl_xor(oo, 32, 64);
+      if (row_ok && half == 0) {
+        a.part[(int64_t(head) * 3 + 0) * a.Tq + qrow] = dot;
+        a.part[(int64_t(head) * 3 + 1) * a.Tq + qrow] = nn;
+        a.part[(int64_t(head) * 3 + 2) * a.Tq + qrow] = oo;
+      }
+      return;
+    }
+  }
   if constexpr (MODE != AttnMode::ColSparse) {
     if (!row_ok) return;
     uint16_t* op = a.O + int64_t(row) * ldq + head * kD + half * 4;
@@ -296,8 +341,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
       }
   } else {
     float dot = 0.f, nn = 0.f, oo = 0.f;
-    if (row_ok) {
-      const int slot = a.sal_slot[row];
+    const int slot = row_ok ? a.sal_slot[row] : -1;
+    // salient rows are finished by the row-sparse tiles of the fused step (every lane stays for
+    // the half-wave reductions below)
+    const bool own = row_ok && !(a.skip_salient && slot >= 0);
+    if (own) {
       const int64_t crow = a.c_start ? a.c_start[b] + (row - row_beg) : int64_t(row);
       uint16_t* cp = const_cast<uint16_t*>(a.C) + crow * ldq + head * kD + half * 4;
       uint16_t* op = a.O + int64_t(row) * ldq + head * kD + half * 4;
@@ -337,11 +385,36 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     dot += __shfl_xor(dot, 32, 64);
     nn += __shfl_xor(nn, 32, 64);
     oo += __shfl_xor(oo, 32, 64);
-    if (row_ok && half == 0) {
+    if (own && half == 0) {
       a.part[(int64_t(head) * 3 + 0) * a.Tq + row] = dot;
       a.part[(int64_t(head) * 3 + 1) * a.Tq + row] = nn;
       a.part[(int64_t(head) * 3 + 2) * a.Tq + row] = oo;
     }
+  }
+}
+
+template <AttnMode MODE, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
+  attention_tile<MODE, NW>(a, xcd_remap(blockIdx.x, gridDim.x), k_lds, vt_lds);
+}
+
+// Fused sparse step: the row-sparse tiles of the salient queries (finishing their rows) and the
+// column-sparse tiles of all other queries in one launch, so the two run concurrently. The
+// row-sparse tiles come first (n_rs_pad of them, a multiple of 8, the excess returning at once),
+// each range remapped XCD-major on its own.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_step_kernel(
+    AttnArgs rs, AttnArgs cs, int n_rs, int n_rs_pad) {
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
+  const int wg = blockIdx.x;
+  if (wg < n_rs_pad) {
+    const int t = xcd_remap(wg, n_rs_pad);
+    if (t < n_rs) attention_tile<AttnMode::RowSparse, NW>(rs, t, k_lds, vt_lds);
+  } else {
+    attention_tile<AttnMode::ColSparse, NW>(cs, xcd_remap(wg - n_rs_pad, int(gridDim.x) - n_rs_pad), k_lds, vt_lds);
   }
 }
 
@@ -537,6 +610,21 @@ int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hip
       break;
   }
   return check_launch("attention_kernel");
+}
+
+int launch_attention_step(const AttnArgs& rs0, int max_rows_rs, const AttnArgs& cs0, int max_rows_cs,
+                          hipStream_t s) {
+  DYLLM_REQUIRE(cs0.B >= 1 && cs0.H >= 1 && cs0.Hkv >= 1 && cs0.H % cs0.Hkv == 0, "bad head counts");
+  AttnArgs rs = rs0, cs = cs0;
+  rs.tiles_per_seq = int(cdiv(max_rows_rs > 0 ? max_rows_rs : 1, 128));
+  cs.tiles_per_seq = int(cdiv(max_rows_cs, 128));
+  const int64_t n_rs = max_rows_rs > 0 ? int64_t(rs.tiles_per_seq) * rs.H * rs.B : 0;
+  const int64_t n_rs_pad = cdiv(n_rs, 8) * 8;
+  const int64_t n_cs = int64_t(cs.tiles_per_seq) * cs.H * cs.B;
+  DYLLM_REQUIRE(n_rs_pad + n_cs < (int64_t(1) << 31), "grid too large");
+  if (n_rs_pad + n_cs == 0) return 0;
+  attention_step_kernel<4><<<unsigned(n_rs_pad + n_cs), 256, 0, s>>>(rs, cs, int(n_rs), int(n_rs_pad));
+  return check_launch("attention_step_kernel");
 }
 
 int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal, const int32_t* cu_k, int B,

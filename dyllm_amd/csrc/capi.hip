@@ -77,7 +77,8 @@ static int colsparse_impl(const void* q, const void* k, const int64_t* kv_start,
                           int64_t total_k, int num_salient, const int32_t* idx_salient_q,
                           const int32_t* idx_salient_k, float* cosine_stats, uint8_t* cosine_out, float threshold,
                           void* workspace, size_t workspace_bytes, bool compact_dv, void* stream,
-                          bool maps_ready = false, bool reduce = true) {
+                          bool maps_ready = false, bool reduce = true, const AttnArgs* fused_rs = nullptr,
+                          int fused_rs_rows = 0) {
   DYLLM_NONNULL(q);
   DYLLM_NONNULL(k);
   DYLLM_NONNULL(c);
@@ -137,7 +138,13 @@ static int colsparse_impl(const void* q, const void* k, const int64_t* kv_start,
   a.Tq = total_q;
   // the reference uses rsqrt(head_dim) here, not the layer's scale (sm80.cu:166-168)
   a.scale_log2 = (1.0f / sqrtf(float(head_dim))) * kLog2e;
-  if (int rc = launch_attention(AttnMode::ColSparse, a, max_seqlen_q, s)) return rc;
+  if (fused_rs) {
+    // salient rows are finished by the row-sparse tiles launched together with these
+    a.skip_salient = 1;
+    if (int rc = launch_attention_step(*fused_rs, fused_rs_rows, a, max_seqlen_q, s)) return rc;
+  } else {
+    if (int rc = launch_attention(AttnMode::ColSparse, a, max_seqlen_q, s)) return rc;
+  }
   if (!reduce) return 0;
   return launch_saliency_reduce(part, cosine_stats, cosine_out, total_q, num_heads, threshold, s);
 }
@@ -256,29 +263,36 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                      int64_t(num_kv_heads) * head_dim, idx_k64, idx_q32, num_salient, cu_seqlens_k,
                                      batch, nblk, v_seq_starts, seq_ids, cw.slot, cw.kmask, cw.kslot, s))
       return rc;
-    // row-sparse attention of the salient queries vs the full cached K/V (attention.py:76-87)
-    AttnArgs a{};
-    a.Q = static_cast<const uint16_t*>(q);
-    a.K = static_cast<const uint16_t*>(k);
-    a.V = static_cast<const uint16_t*>(v_cache);
-    a.O = o_sal;
-    a.cu_rows = cu_salientlens;
-    a.cu_k = cu_seqlens_k;
-    a.kv_start = k_start;
-    a.v_start = v_start;
-    a.q_rows = idx_q32;
-    a.B = batch;
-    a.H = num_heads;
-    a.Hkv = num_kv_heads;
-    a.scale_log2 = softmax_scale * kLog2e;
-    if (int rc = launch_attention(AttnMode::RowSparse, a, max_salientlen > 0 ? max_salientlen : max_seqlen_q, s))
-      return rc;
   }
-  // column-sparse attention + statistics + tau test, context cache updated in place
+  // row-sparse attention of the salient queries vs the full cached K/V (attention.py:76-87),
+  // launched together with the column-sparse attention of the other rows (statistics + tau
+  // inputs, context cache updated in place); each salient row's tile writes its final output,
+  // context row and statistics itself (attention_aux_kernels.cu:22-72)
+  AttnArgs rs{};
+  rs.Q = static_cast<const uint16_t*>(q);
+  rs.K = static_cast<const uint16_t*>(k);
+  rs.V = static_cast<const uint16_t*>(v_cache);
+  rs.C = static_cast<const uint16_t*>(c_cache);
+  rs.O = static_cast<uint16_t*>(out);
+  rs.cu_rows = cu_salientlens;
+  rs.cu_k = cu_seqlens_k;
+  rs.cu_q = cu_seqlens_q;
+  rs.kv_start = k_start;
+  rs.v_start = v_start;
+  rs.c_start = c_start;
+  rs.c_inplace = 1;
+  rs.q_rows = idx_q32;
+  rs.part = cw.part;
+  rs.Tq = total_q;
+  rs.B = batch;
+  rs.H = num_heads;
+  rs.Hkv = num_kv_heads;
+  rs.scale_log2 = softmax_scale * kLog2e;
+  const int rs_rows = num_salient > 0 ? (max_salientlen > 0 ? max_salientlen : max_seqlen_q) : 0;
   if (int rc = colsparse_impl(q, k, k_start, num_salient ? dv : nullptr, c_cache, c_start, 1, o_sal, out, batch,
                               num_heads, num_kv_heads, head_dim, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                               max_seqlen_k, total_q, total_k, num_salient, idx_q32, idx_k32, cosine_stats,
-                              cosine_out, threshold, ws, cs_bytes, true, stream, true, false))
+                              cosine_out, threshold, ws, cs_bytes, true, stream, true, false, &rs, rs_rows))
     return rc;
   // statistics reduction, tau test and compaction of the next salient set (attention.py:141-173)
   return launch_reduce_compact(cw.part, cosine_stats, cosine_out, total_q, num_heads, threshold, done, cu_seqlens_q,

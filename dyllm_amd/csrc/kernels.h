@@ -53,6 +53,9 @@ struct AttnArgs {
   const int64_t* c_start;   // optional [B]: first C row of sequence b (else cu_rows[b])
   int c_inplace;            // ColSparse: also write the new rows back to C
   const int32_t* q_rows;    // RowSparse: Q row of compact row j
+  const int32_t* cu_q;      // RowSparse, fused step: [B+1] Q-space prefix; the tile then writes the
+                            // final output row, the context cache row and the statistics itself
+  int skip_salient;         // ColSparse, fused step: rows with a slot are left to the row-sparse tiles
   const int32_t* sal_slot;  // ColSparse: [Tq] index into o_sal or -1
   const int32_t* kslot;     // ColSparse, optional: [Tk] row of compact dV or -1
   const uint64_t* kmask;    // ColSparse: [B][nblk] salient-key bits per 64-key block
@@ -64,6 +67,8 @@ struct AttnArgs {
   float scale_log2;
 };
 int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s);
+// Row-sparse tiles (fused output) and column-sparse tiles in one launch (4-wave workgroups).
+int launch_attention_step(const AttnArgs& rs, int max_rows_rs, const AttnArgs& cs, int max_rows_cs, hipStream_t s);
 int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal, const int32_t* cu_k, int B,
                           int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, int32_t* kslot, int64_t Tk,
                           hipStream_t s);

@@ -219,10 +219,14 @@ __global__ __launch_bounds__(kCompactThreads) void compact_kernel(
 }
 
 // ---- statistics reduction + compaction in one launch ---------------------------------
-// Every workgroup reduces the per-head partial statistics of 1024 rows (heads summed in
-// ascending order) and writes the statistics and the tau decision; the workgroup that finishes
-// last (completion counter, device-scope fences on both sides) then compacts the whole mask.
-// The counter is zeroed by the step's preparation kernel and reset here after use.
+// Every workgroup reduces the per-head partial statistics of 256 rows: its four 256-thread
+// quarters sum contiguous quarters of the heads (ascending), and the quarter sums are added in
+// quarter order (a fixed order: deterministic). It writes the statistics and the tau decision;
+// the workgroup that finishes last (completion counter, device-scope fences on both sides) then
+// compacts the whole mask. The counter is zeroed by the step's preparation kernel and reset here
+// after use.
+constexpr int kReduceRows = kCompactThreads / 4;
+
 __global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
     const float* __restrict__ part, float* __restrict__ stats, uint8_t* __restrict__ mask, int64_t T, int H,
     float tau, uint32_t* __restrict__ done, const int32_t* __restrict__ cu_q, int B,
@@ -230,15 +234,28 @@ __global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
     int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32, int32_t* __restrict__ cu_sal,
     int32_t* __restrict__ count, int32_t* __restrict__ host_meta) {
   __shared__ int last_sh;
-  const int64_t t = int64_t(blockIdx.x) * kCompactThreads + threadIdx.x;
+  __shared__ float red[4][3][kReduceRows];
+  const int tl = threadIdx.x % kReduceRows, hq = threadIdx.x / kReduceRows;
+  const int64_t t = int64_t(blockIdx.x) * kReduceRows + tl;
+  const int hpq = (H + 3) / 4;
+  const int h0 = hq * hpq, h1 = (h0 + hpq < H) ? h0 + hpq : H;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
   if (t < T) {
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
-#pragma unroll 8
-    for (int h = 0; h < H; ++h) {
+#pragma unroll 4
+    for (int h = h0; h < h1; ++h) {
       s0 += part[(int64_t(h) * 3 + 0) * T + t];
       s1 += part[(int64_t(h) * 3 + 1) * T + t];
       s2 += part[(int64_t(h) * 3 + 2) * T + t];
     }
+  }
+  red[hq][0][tl] = s0;
+  red[hq][1][tl] = s1;
+  red[hq][2][tl] = s2;
+  __syncthreads();
+  if (hq == 0 && t < T) {
+    s0 = ((red[0][0][tl] + red[1][0][tl]) + red[2][0][tl]) + red[3][0][tl];
+    s1 = ((red[0][1][tl] + red[1][1][tl]) + red[2][1][tl]) + red[3][1][tl];
+    s2 = ((red[0][2][tl] + red[1][2][tl]) + red[2][2][tl]) + red[3][2][tl];
     stats[3 * t] = s0;
     stats[3 * t + 1] = s1;
     stats[3 * t + 2] = s2;
@@ -269,7 +286,7 @@ int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_
   DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
   DYLLM_REQUIRE(T >= 1 && T < (int64_t(1) << 31), "row count out of range");
   DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
-  reduce_compact_kernel<<<unsigned(cdiv(T, kCompactThreads)), kCompactThreads, 0, s>>>(
+  reduce_compact_kernel<<<unsigned(cdiv(T, kReduceRows)), kCompactThreads, 0, s>>>(
       part, stats, mask, T, H, tau, done, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count, host_meta);
   return check_launch("reduce_compact_kernel");
 }
