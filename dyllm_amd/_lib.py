@@ -9,7 +9,7 @@ import os
 from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libdyllm_hip.so")
+LIB_PATH = os.environ.get("DYLLM_HIP_LIB") or os.path.join(_HERE, "libdyllm_hip.so")
 
 _P = c_void_p
 _I = c_int

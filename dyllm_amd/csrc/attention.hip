@@ -512,7 +512,6 @@ __global__ __launch_bounds__(256) void step_prep_kernel(StepPrepArgs a) {
     if (a.q_pruned) c += int64_t(a.cu_k[i + 1] - a.cu_k[i]) - int64_t(a.cu_q[i + 1] - a.cu_q[i]);
     a.c_start[i] = c;
   }
-  if (i == 0) *a.done = 0u;
 }
 
 int launch_step_prep(const StepPrepArgs& a, hipStream_t s) {

@@ -182,7 +182,7 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
 size_t dyllm_sparse_step_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim, int64_t total_q,
                                          int64_t total_k, int max_seqlen_k, int64_t num_salient) {
   const size_t n = size_t(num_salient > 0 ? num_salient : 0);
-  return 256 + align256(n * num_kv_heads * head_dim * 2) + align256(n * num_heads * head_dim * 2) +
+  return align256(n * num_kv_heads * head_dim * 2) + align256(n * num_heads * head_dim * 2) +
          2 * align256(size_t(batch) * 8) +
          dyllm_attention_colsparse_workspace_bytes(batch, num_heads, total_q, total_k, max_seqlen_k);
 }
@@ -223,8 +223,6 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
   }
   const size_t n = size_t(num_salient);
   char* ws = static_cast<char*>(workspace);
-  uint32_t* done = reinterpret_cast<uint32_t*>(ws);  // completion counter of the statistics reduction
-  ws += 256;
   uint16_t* dv = reinterpret_cast<uint16_t*>(ws);
   ws += align256(n * num_kv_heads * head_dim * 2);
   uint16_t* o_sal = reinterpret_cast<uint16_t*>(ws);
@@ -255,7 +253,6 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
   pa.B = batch;
   pa.v_start = v_start;
   pa.c_start = c_start;
-  pa.done = done;
   if (int rc = launch_step_prep(pa, s)) return rc;
   if (num_salient > 0) {
     // dV of the salient keys + V-cache update (attention.py:67-74, 89-96) and the salient maps
@@ -295,9 +292,10 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                               cosine_out, threshold, ws, cs_bytes, true, stream, true, false, &rs, rs_rows))
     return rc;
   // statistics reduction, tau test and compaction of the next salient set (attention.py:141-173)
-  return launch_reduce_compact(cw.part, cosine_stats, cosine_out, total_q, num_heads, threshold, done, cu_seqlens_q,
-                               batch, cu_promptlens, next_idx64, next_idx32, q_pruned ? next_idx_k64 : nullptr,
-                               q_pruned ? next_idx_k32 : nullptr, next_cu_salientlens, next_count, host_meta_dev, s);
+  if (int rc = launch_reduce_stats(cw.part, cosine_stats, cosine_out, total_q, num_heads, threshold, s)) return rc;
+  return launch_compact(cosine_out, total_q, cu_seqlens_q, batch, cu_promptlens, next_idx64, next_idx32,
+                        q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr, next_cu_salientlens,
+                        next_count, s, host_meta_dev);
 }
 
 int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,

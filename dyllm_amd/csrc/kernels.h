@@ -28,13 +28,8 @@ int launch_saliency_reduce(const float* part, float* stats, uint8_t* mask, int64
                            hipStream_t s);
 int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
                    int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
-                   hipStream_t s);
-// statistics reduction + tau test + compaction in one launch (the completion counter must be
-// zero on entry; it is zero again on exit)
-int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
-                          uint32_t* done, const int32_t* cu_q, int B, const int32_t* cu_prompt, int64_t* idx64,
-                          int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
-                          int32_t* host_meta, hipStream_t s);
+                   hipStream_t s, int32_t* host_meta = nullptr);
+int launch_reduce_stats(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau, hipStream_t s);
 int launch_fused_offset(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_prompt,
                         const int32_t* cu_sal, int groups, int64_t* out, int64_t cap, hipStream_t s);
 
@@ -73,7 +68,7 @@ int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal,
                           int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, int32_t* kslot, int64_t Tk,
                           hipStream_t s);
 // Native sparse step, preparation (one launch): slot / salient-key maps reset, first V-cache
-// and context-cache row of every sequence, completion counter of the reduce kernel zeroed.
+// and context-cache row of every sequence.
 struct StepPrepArgs {
   int32_t* slot;                // [Tq] -> -1
   int64_t Tq;
@@ -90,7 +85,6 @@ struct StepPrepArgs {
   int B;
   int64_t* v_start;             // [B] out
   int64_t* c_start;             // [B] out
-  uint32_t* done;               // -> 0
 };
 int launch_step_prep(const StepPrepArgs& a, hipStream_t s);
 // Native sparse step, per salient row (one launch): dV = bf16(v_new - v_cache[row]), V-cache

@@ -210,30 +210,36 @@ __device__ __forceinline__ void compact_block(
   }
 }
 
+// [count, cu_salientlens...] straight into pinned host memory (when given): the host reads the
+// salient count once the kernel has completed, with no device->host copy behind it
+__device__ __forceinline__ void write_host_meta(int32_t* host_meta, const int32_t* cu_sal, const int32_t* count,
+                                                int B) {
+  if (!host_meta) return;
+  __syncthreads();
+  for (int b = threadIdx.x; b <= B; b += kCompactThreads) host_meta[1 + b] = cu_sal[b];
+  if (threadIdx.x == 0) host_meta[0] = count[0];
+  __threadfence_system();
+}
+
 __global__ __launch_bounds__(kCompactThreads) void compact_kernel(
     const uint8_t* __restrict__ mask, int64_t T, const int32_t* __restrict__ cu_q, int B,
     const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64, int32_t* __restrict__ idx32,
     int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32, int32_t* __restrict__ cu_sal,
-    int32_t* __restrict__ count) {
+    int32_t* __restrict__ count, int32_t* __restrict__ host_meta) {
   compact_block(mask, T, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count);
+  write_host_meta(host_meta, cu_sal, count, B);
 }
 
-// ---- statistics reduction + compaction in one launch ---------------------------------
+// ---- statistics reduction of the native step ------------------------------------------
 // Every workgroup reduces the per-head partial statistics of 256 rows: its four 256-thread
 // quarters sum contiguous quarters of the heads (ascending), and the quarter sums are added in
-// quarter order (a fixed order: deterministic). It writes the statistics and the tau decision;
-// the workgroup that finishes last (completion counter, device-scope fences on both sides) then
-// compacts the whole mask. The counter is zeroed by the step's preparation kernel and reset here
-// after use.
+// quarter order (a fixed order: deterministic); it writes the statistics and the tau decision.
+// (A variant that let the last workgroup compact the mask in the same launch measured slower:
+// the device-scope fences it needs cost more than the second launch.)
 constexpr int kReduceRows = kCompactThreads / 4;
 
-__global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
-    const float* __restrict__ part, float* __restrict__ stats, uint8_t* __restrict__ mask, int64_t T, int H,
-    float tau, uint32_t* __restrict__ done, const int32_t* __restrict__ cu_q, int B,
-    const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64, int32_t* __restrict__ idx32,
-    int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32, int32_t* __restrict__ cu_sal,
-    int32_t* __restrict__ count, int32_t* __restrict__ host_meta) {
-  __shared__ int last_sh;
+__device__ __forceinline__ void reduce_rows(const float* __restrict__ part, float* __restrict__ stats,
+                                            uint8_t* __restrict__ mask, int64_t T, int H, float tau) {
   __shared__ float red[4][3][kReduceRows];
   const int tl = threadIdx.x % kReduceRows, hq = threadIdx.x / kReduceRows;
   const int64_t t = int64_t(blockIdx.x) * kReduceRows + tl;
@@ -261,44 +267,30 @@ __global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
     stats[3 * t + 2] = s2;
     mask[t] = tau_cos(s0, s1, s2) < tau;
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last_sh = (atomicAdd(done, 1u) == gridDim.x - 1) ? 1 : 0;
-  __syncthreads();
-  if (!last_sh) return;
-  __threadfence();
-  compact_block(mask, T, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count);
-  if (host_meta) {
-    // [count, cu_salientlens...] straight into pinned host memory: the host reads the salient
-    // count once this kernel has completed, with no device->host copy behind it
-    __syncthreads();
-    for (int b = threadIdx.x; b <= B; b += kCompactThreads) host_meta[1 + b] = cu_sal[b];
-    if (threadIdx.x == 0) host_meta[0] = count[0];
-    __threadfence_system();
-  }
-  if (threadIdx.x == 0) *done = 0u;
 }
 
-int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
-                          uint32_t* done, const int32_t* cu_q, int B, const int32_t* cu_prompt, int64_t* idx64,
-                          int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
-                          int32_t* host_meta, hipStream_t s) {
-  DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
-  DYLLM_REQUIRE(T >= 1 && T < (int64_t(1) << 31), "row count out of range");
-  DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
-  reduce_compact_kernel<<<unsigned(cdiv(T, kReduceRows)), kCompactThreads, 0, s>>>(
-      part, stats, mask, T, H, tau, done, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count, host_meta);
-  return check_launch("reduce_compact_kernel");
+__global__ __launch_bounds__(kCompactThreads) void reduce_stats_kernel(const float* __restrict__ part,
+                                                                       float* __restrict__ stats,
+                                                                       uint8_t* __restrict__ mask, int64_t T, int H,
+                                                                       float tau) {
+  reduce_rows(part, stats, mask, T, H, tau);
 }
+
+int launch_reduce_stats(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau, hipStream_t s) {
+  if (T <= 0) return 0;
+  reduce_stats_kernel<<<unsigned(cdiv(T, kReduceRows)), kCompactThreads, 0, s>>>(part, stats, mask, T, H, tau);
+  return check_launch("reduce_stats_kernel");
+}
+
 
 int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
                    int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
-                   hipStream_t s) {
+                   hipStream_t s, int32_t* host_meta) {
   DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
   DYLLM_REQUIRE(T >= 0 && T < (int64_t(1) << 31), "row count out of range");
   DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
   compact_kernel<<<1, kCompactThreads, 0, s>>>(mask, T, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal,
-                                                count);
+                                                count, host_meta);
   return check_launch("compact_kernel");
 }
 
