@@ -271,7 +271,7 @@ def main():
     flops = 2.0 * avg_n * hid * 2 * inter
     avg_gate_ms = sum(gate_ms) / len(gate_ms)
     from dyllm_amd import _lib
-    gate_bm = _lib.load().dyllm_ffn_tile_rows(int(round(avg_n)), 2 * inter, 1)
+    gate_bm = _lib.load().dyllm_ffn_tile_rows(int(round(avg_n)), 2 * inter, hid, 1)
     achieved = flops / (avg_gate_ms * 1e-3) / 1e12
     print(f"[bench] {ms_per_step:.3f} ms/step, avg salient rows per layer {avg_n:.1f}, "
           f"gate_up {avg_gate_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)

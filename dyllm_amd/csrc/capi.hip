@@ -477,16 +477,17 @@ static int64_t hint_or(int64_t hint, int64_t rows) { return (hint > 0 && hint < 
 size_t dyllm_ffn_down_workspace_bytes(int64_t rows, int64_t rows_hint, int hidden, int intermediate) {
   if (rows <= 0) return 0;
   const int64_t h = hint_or(rows_hint, rows);
-  const int tm = gemm_pick_tile(h, hidden, GemmEpi::Store);
-  return align256(gemm_partial_bytes(rows, hidden, tm, gemm_pick_ksplit(h, hidden, intermediate, tm)));
+  const GemmPlan pl = gemm_plan(h, hidden, intermediate, GemmEpi::Store);
+  return align256(gemm_partial_bytes(rows, hidden, pl.tile_m, pl.ksplit));
 }
 
 size_t dyllm_swiglu_ffn_workspace_bytes(int64_t rows, int intermediate) {
   return align256(size_t(rows > 0 ? rows : 0) * size_t(intermediate) * 2);
 }
 
-int dyllm_ffn_tile_rows(int64_t rows, int n, int swiglu) {
-  return gemm_pick_tile(rows, n, swiglu ? GemmEpi::SwiGLU : GemmEpi::Store);
+int dyllm_ffn_tile_rows(int64_t rows, int n, int k, int swiglu) {
+  if (rows <= 0 || n <= 0 || k <= 0) return 0;
+  return gemm_plan(rows, n, k, swiglu ? GemmEpi::SwiGLU : GemmEpi::Store).tile_m;
 }
 
 int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const int32_t* rows_dev,
@@ -513,7 +514,7 @@ int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int6
   g.N = 2 * intermediate;
   g.K = hidden;
   g.half_n = intermediate;
-  const int tm = gemm_pick_tile(hint_or(rows_hint, rows), g.N, GemmEpi::SwiGLU);
+  const int tm = gemm_plan(hint_or(rows_hint, rows), g.N, g.K, GemmEpi::SwiGLU).tile_m;
   return launch_gemm(GemmEpi::SwiGLU, g, rows, tm, 1, DYLLM_STREAM(stream));
 }
 
@@ -541,8 +542,8 @@ int dyllm_ffn_down(const void* h, int64_t rows, const int32_t* rows_dev, int64_t
   d.N = hidden;
   d.K = intermediate;
   const int64_t hr = hint_or(rows_hint, rows);
-  const int tm = gemm_pick_tile(hr, hidden, GemmEpi::Store);
-  const int ks = gemm_pick_ksplit(hr, hidden, intermediate, tm);
+  const GemmPlan pl = gemm_plan(hr, hidden, intermediate, GemmEpi::Store);
+  const int tm = pl.tile_m, ks = pl.ksplit;
   if (ks > 1) {
     const size_t need = gemm_partial_bytes(rows, hidden, tm, ks);
     DYLLM_REQUIRE(workspace && workspace_bytes >= need,

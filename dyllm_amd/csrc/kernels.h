@@ -127,8 +127,12 @@ struct GemmArgs {
 // g.partial with gemm_partial_bytes() bytes and is followed by the reduction kernel.
 int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, int ksplit, hipStream_t s);
 size_t gemm_partial_bytes(int64_t m_bound, int N, int tile_m, int ksplit);
-int gemm_pick_tile(int64_t M, int N, GemmEpi epi);
-int gemm_pick_ksplit(int64_t M, int N, int K, int tile_m);
+struct GemmPlan {
+  int tile_m;   // 128 / 192 / 256
+  int ksplit;   // 1 unless the Store epilogue is split along K
+};
+// tile height and split-K factor for an M x N x K product (measured cost model)
+GemmPlan gemm_plan(int64_t M, int N, int K, GemmEpi epi);
 
 int launch_moe_router(const uint16_t* x, const int32_t* rows, const uint16_t* wr, int64_t T, int Hd, int E, int top_k,
                       int renorm, uint16_t* topk_w, int32_t* topk_ids, hipStream_t s);

@@ -209,8 +209,8 @@ int dyllm_ffn_down(const void* h, int64_t rows, const int32_t* rows_dev, int64_t
                    int hidden, int intermediate, void* out, const int64_t* out_rows, void* workspace,
                    size_t workspace_bytes, void* stream);
 
-/* Tile height (128/192/256) the FFN GEMMs use for `rows` rows and output width n. */
-int dyllm_ffn_tile_rows(int64_t rows, int n, int swiglu);
+/* Tile height (128/192/256) the FFN GEMMs use for `rows` rows, output width n and depth k. */
+int dyllm_ffn_tile_rows(int64_t rows, int n, int k, int swiglu);
 
 /* ---- MoE ------------------------------------------------------------------------------- */
 
