@@ -183,7 +183,7 @@ size_t dyllm_sparse_step_workspace_bytes(int batch, int num_heads, int num_kv_he
                                          int64_t total_k, int max_seqlen_k, int64_t num_salient) {
   const size_t n = size_t(num_salient > 0 ? num_salient : 0);
   return align256(n * num_kv_heads * head_dim * 2) + align256(n * num_heads * head_dim * 2) +
-         2 * align256(size_t(batch) * 8) +
+         2 * align256(size_t(batch) * 8) + align256(size_t(cdiv(total_q, 256)) * 4) +
          dyllm_attention_colsparse_workspace_bytes(batch, num_heads, total_q, total_k, max_seqlen_k);
 }
 
@@ -231,6 +231,8 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
   ws += align256(size_t(batch) * 8);
   int64_t* c_start = reinterpret_cast<int64_t*>(ws);
   ws += align256(size_t(batch) * 8);
+  int32_t* block_counts = reinterpret_cast<int32_t*>(ws);  // salient rows per 256-row block
+  ws += align256(size_t(cdiv(total_q, 256)) * 4);
   const size_t cs_bytes = workspace_bytes - size_t(ws - static_cast<char*>(workspace));
   const bool q_pruned = cu_promptlens != nullptr;
 
@@ -292,10 +294,11 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                               cosine_out, threshold, ws, cs_bytes, true, stream, true, false, &rs, rs_rows))
     return rc;
   // statistics reduction, tau test and compaction of the next salient set (attention.py:141-173)
-  if (int rc = launch_reduce_stats(cw.part, cosine_stats, cosine_out, total_q, num_heads, threshold, s)) return rc;
-  return launch_compact(cosine_out, total_q, cu_seqlens_q, batch, cu_promptlens, next_idx64, next_idx32,
-                        q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr, next_cu_salientlens,
-                        next_count, s, host_meta_dev);
+  if (int rc = launch_reduce_stats(cw.part, cosine_stats, cosine_out, total_q, num_heads, threshold, block_counts, s))
+    return rc;
+  return launch_compact_blocks(cosine_out, total_q, block_counts, cu_seqlens_q, batch, cu_promptlens, next_idx64,
+                               next_idx32, q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr,
+                               next_cu_salientlens, next_count, host_meta_dev, s);
 }
 
 int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,

@@ -29,7 +29,13 @@ int launch_saliency_reduce(const float* part, float* stats, uint8_t* mask, int64
 int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
                    int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
                    hipStream_t s, int32_t* host_meta = nullptr);
-int launch_reduce_stats(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau, hipStream_t s);
+// statistics reduction + tau test of the native step; block_counts (optional) receives the
+// salient rows of every 256-row block for launch_compact_blocks
+int launch_reduce_stats(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
+                        int32_t* block_counts, hipStream_t s);
+int launch_compact_blocks(const uint8_t* mask, int64_t T, const int32_t* block_counts, const int32_t* cu_q, int B,
+                          const int32_t* cu_prompt, int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32,
+                          int32_t* cu_sal, int32_t* count, int32_t* host_meta, hipStream_t s);
 int launch_fused_offset(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_prompt,
                         const int32_t* cu_sal, int groups, int64_t* out, int64_t cap, hipStream_t s);
 

@@ -239,7 +239,8 @@ __global__ __launch_bounds__(kCompactThreads) void compact_kernel(
 constexpr int kReduceRows = kCompactThreads / 4;
 
 __device__ __forceinline__ void reduce_rows(const float* __restrict__ part, float* __restrict__ stats,
-                                            uint8_t* __restrict__ mask, int64_t T, int H, float tau) {
+                                            uint8_t* __restrict__ mask, int64_t T, int H, float tau,
+                                            int32_t* __restrict__ block_counts) {
   __shared__ float red[4][3][kReduceRows];
   const int tl = threadIdx.x % kReduceRows, hq = threadIdx.x / kReduceRows;
   const int64_t t = int64_t(blockIdx.x) * kReduceRows + tl;
@@ -258,6 +259,7 @@ __device__ __forceinline__ void reduce_rows(const float* __restrict__ part, floa
   red[hq][1][tl] = s1;
   red[hq][2][tl] = s2;
   __syncthreads();
+  bool sal = false;
   if (hq == 0 && t < T) {
     s0 = ((red[0][0][tl] + red[1][0][tl]) + red[2][0][tl]) + red[3][0][tl];
     s1 = ((red[0][1][tl] + red[1][1][tl]) + red[2][1][tl]) + red[3][1][tl];
@@ -265,21 +267,117 @@ __device__ __forceinline__ void reduce_rows(const float* __restrict__ part, floa
     stats[3 * t] = s0;
     stats[3 * t + 1] = s1;
     stats[3 * t + 2] = s2;
-    mask[t] = tau_cos(s0, s1, s2) < tau;
+    sal = tau_cos(s0, s1, s2) < tau;
+    mask[t] = sal;
+  }
+  if (block_counts) {
+    // salient rows of this block, for the multi-workgroup compaction (waves of the first
+    // quarter hold the rows)
+    __shared__ int wcnt[kReduceRows / 64];
+    const unsigned long long bal = __ballot(sal);
+    if (hq == 0 && (threadIdx.x & 63) == 0) wcnt[threadIdx.x >> 6] = __popcll(bal);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int c = 0;
+      for (int w = 0; w < kReduceRows / 64; ++w) c += wcnt[w];
+      block_counts[blockIdx.x] = c;
+    }
   }
 }
 
 __global__ __launch_bounds__(kCompactThreads) void reduce_stats_kernel(const float* __restrict__ part,
                                                                        float* __restrict__ stats,
                                                                        uint8_t* __restrict__ mask, int64_t T, int H,
-                                                                       float tau) {
-  reduce_rows(part, stats, mask, T, H, tau);
+                                                                       float tau, int32_t* __restrict__ block_counts) {
+  reduce_rows(part, stats, mask, T, H, tau, block_counts);
 }
 
-int launch_reduce_stats(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau, hipStream_t s) {
+int launch_reduce_stats(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
+                        int32_t* block_counts, hipStream_t s) {
   if (T <= 0) return 0;
-  reduce_stats_kernel<<<unsigned(cdiv(T, kReduceRows)), kCompactThreads, 0, s>>>(part, stats, mask, T, H, tau);
+  reduce_stats_kernel<<<unsigned(cdiv(T, kReduceRows)), kCompactThreads, 0, s>>>(part, stats, mask, T, H, tau,
+                                                                                   block_counts);
   return check_launch("reduce_stats_kernel");
+}
+
+// ---- multi-workgroup compaction (native step) ----------------------------------------
+// Workgroup w owns mask rows [256w, 256w+256); its base is the sum of the salient counts of the
+// workgroups before it (written by reduce_stats_kernel). Rows are emitted in ascending order,
+// cu_salientlens[b] by the workgroup that owns row cu_q[b] (the last one for cu_q[B] = T), the
+// count by the last workgroup; the same values go to pinned host memory when given.
+__global__ __launch_bounds__(kReduceRows) void compact_blocks_kernel(
+    const uint8_t* __restrict__ mask, int64_t T, const int32_t* __restrict__ block_counts,
+    const int32_t* __restrict__ cu_q, int B, const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64,
+    int32_t* __restrict__ idx32, int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32,
+    int32_t* __restrict__ cu_sal, int32_t* __restrict__ count, int32_t* __restrict__ host_meta) {
+  constexpr int NWV = kReduceRows / 64;
+  __shared__ int wtot[NWV];
+  __shared__ int part_sh[NWV];
+  __shared__ int pre[kReduceRows + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int nblk = gridDim.x, blk = blockIdx.x;
+  const int64_t t = int64_t(blk) * kReduceRows + tid;
+  // base = sum of the earlier blocks' counts
+  int acc = 0;
+  for (int w = tid; w < blk; w += kReduceRows) acc += block_counts[w];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane == 0) part_sh[wid] = acc;
+  const bool sal = t < T && mask[t];
+  const unsigned long long bal = __ballot(sal);
+  const int before = __popcll(bal & ((1ull << lane) - 1));
+  if (lane == 0) wtot[wid] = __popcll(bal);
+  __syncthreads();
+  int base = 0, woff = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) {
+    base += part_sh[w];
+    woff += (w < wid) ? wtot[w] : 0;
+    total += wtot[w];
+  }
+  pre[tid] = woff + before;
+  if (tid == 0) pre[kReduceRows] = total;
+  const int pos = base + woff + before;
+  if (sal) {
+    idx64[pos] = t;
+    if (idx32) idx32[pos] = int32_t(t);
+    if (idx_k) {
+      const int seg = find_segment(cu_q, B + 1, t);
+      const int64_t kk = t + cu_prompt[seg + 1];
+      idx_k[pos] = kk;
+      if (idx_k32) idx_k32[pos] = int32_t(kk);
+    }
+  }
+  __syncthreads();
+  bool wrote = false;
+  const int64_t lo = int64_t(blk) * kReduceRows;
+  for (int b = tid; b <= B; b += kReduceRows) {
+    const int64_t p = cu_q[b];
+    const int owner = (p >= T) ? nblk - 1 : int(p / kReduceRows);
+    if (owner != blk) continue;
+    const int64_t local = p - lo;
+    const int v = base + (local >= kReduceRows ? total : pre[local]);
+    cu_sal[b] = v;
+    if (host_meta) host_meta[1 + b] = v;
+    wrote = true;
+  }
+  if (blk == nblk - 1 && tid == 0) {
+    count[0] = base + total;
+    if (host_meta) host_meta[0] = base + total;
+    wrote = true;
+  }
+  if (host_meta && wrote) __threadfence_system();
+}
+
+int launch_compact_blocks(const uint8_t* mask, int64_t T, const int32_t* block_counts, const int32_t* cu_q, int B,
+                          const int32_t* cu_prompt, int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32,
+                          int32_t* cu_sal, int32_t* count, int32_t* host_meta, hipStream_t s) {
+  DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
+  DYLLM_REQUIRE(T >= 1 && T < (int64_t(1) << 31), "row count out of range");
+  DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
+  compact_blocks_kernel<<<unsigned(cdiv(T, kReduceRows)), kReduceRows, 0, s>>>(
+      mask, T, block_counts, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count, host_meta);
+  return check_launch("compact_blocks_kernel");
 }
 
 
