@@ -30,6 +30,17 @@ def test_library_exports_every_declared_symbol():
     assert lib.dyllm_abi_version() == 1
 
 
+def _ctype_of(param):
+    import ctypes
+
+    decl = param.strip()
+    if "*" in decl:
+        return ctypes.c_void_p
+    ty = decl.rsplit(" ", 1)[0].replace("const ", "").strip()
+    return {"int": ctypes.c_int, "int64_t": ctypes.c_int64, "size_t": ctypes.c_size_t,
+            "float": ctypes.c_float, "uint32_t": ctypes.c_uint32}[ty]
+
+
 def test_ctypes_table_matches_header():
     from dyllm_amd import _lib
 
@@ -39,6 +50,11 @@ def test_ctypes_table_matches_header():
         m = re.search(rf"\b{name}\s*\(([^)]*)\)", text)
         params = [p for p in m.group(1).split(",") if p.strip() and p.strip() != "void"]
         assert len(params) == len(args), f"{name}: header has {len(params)} params, ctypes {len(args)}"
+        # every parameter's ctypes type matches its C type: a pointer bound as an int (or the
+        # reverse) truncates addresses and makes kernels write to wild memory
+        for p, a in zip(params, args):
+            want = _ctype_of(p)
+            assert a is want, f"{name}: parameter '{p.strip()}' is bound as {a.__name__}, header type needs {want.__name__}"
 
 
 def test_error_path_reports_message_without_gpu():
