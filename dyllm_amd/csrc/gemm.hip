@@ -19,13 +19,18 @@
 //                               that applies the store epilogue (deterministic).
 //
 // Tiling: workgroup tile BM x 256 x 64, 8 wavefronts (2 per SIMD) in a 2 (M) x 4 (N) grid
-// (WGN = 4; a 2 x 2 grid of 1-wave-per-SIMD tiles measured slower), each wavefront (BM/2) x 64
+// (WGN = 4; a 2 x 2 grid of 1-wave-per-SIMD tiles, and two 4-wave BM x 128 workgroups per CU,
+// both measured slower), each wavefront (BM/2) x 64
 // of v_mfma_f32_32x32x16_bf16 tiles. Operands move global -> LDS with the gfx950 direct
 // LDS-load (global_load_lds_dwordx4), no register staging. Operands are staged through
 // LDS in two buffers of unpadded 128-byte rows whose 16-byte chunks are XOR-swizzled by row
 // (chunk ^ (row & 7)), so the fragment reads are spread over the banks; the next K slice is
 // loaded into the other buffer while the current one is multiplied, and one wait + barrier
-// per K slice separates the buffers. The MFMA is issued as D = W_tile * A_tile^T
+// per K slice separates the buffers (32-wide K stages with 4-5 buffers, i.e. twice the
+// prefetch depth, measured slower). Within a slice the fragment reads of the next 16-wide K
+// substep are interleaved one per MFMA with the current substep, pinned with
+// sched_group_barrier (the compiler's own schedule clusters the reads and stalls on them;
+// 4-8 % with warm caches). The MFMA is issued as D = W_tile * A_tile^T
 // so that each lane owns one output row and four consecutive output columns per register
 // group: 8-byte stores and one row lookup per lane for the scatter. Workgroups are ordered
 // M-fastest and remapped XCD-major so the M tiles sharing a weight slice run on one XCD and
@@ -137,38 +142,56 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  // Fragments are double-buffered in registers (two named sets so every index stays static):
+  // the LDS reads of K-substep ks+1 are issued one by one between the MFMAs of ks.
+  bf16x8_t wf0[TN], af0[TM], wf1[TN], af1[TM];
+  auto fload = [&](const uint16_t* As, int ks, bf16x8_t* wf, bf16x8_t* af) {
+    const uint16_t* Ws = As + BM * kGemmBK;
+    const int ch = 2 * ks + half;
+#pragma unroll
+    for (int i = 0; i < TN; ++i) wf[i] = *reinterpret_cast<const bf16x8_t*>(&Ws[swz(wrow_base(i) + l32, ch)]);
+#pragma unroll
+    for (int j = 0; j < TM; ++j) af[j] = *reinterpret_cast<const bf16x8_t*>(&As[swz(wm * WM + 32 * j + l32, ch)]);
+  };
+  auto mma = [&](const bf16x8_t* wf, const bf16x8_t* af) {
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
+  };
+  // one MFMA, one LDS read, ... for the TN+TM reads, then the remaining MFMAs
+  auto interleave = [&]() {
+#pragma unroll
+    for (int r = 0; r < TN + TM; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int r = TN + TM; r < TN * TM; ++r) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+  };
+
   stage(0, 0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) stage(kt + 1, cur ^ 1);
     const uint16_t* As = gsm + cur * BUF;
-    const uint16_t* Ws = As + BM * kGemmBK;
-    // fragments of K-substep ks+1 are read while the MFMAs of ks run (two named buffers so
-    // every register index stays static)
-    bf16x8_t wf0[TN], af0[TM], wf1[TN], af1[TM];
-#define DYLLM_GEMM_FLOAD(KS, WF, AF)                                                                      \
-  {                                                                                                      \
-    const int ch_ = 2 * (KS) + half;                                                                     \
-    _Pragma("unroll") for (int i = 0; i < TN; ++i) WF[i] =                                               \
-        *reinterpret_cast<const bf16x8_t*>(&Ws[swz(wrow_base(i) + l32, ch_)]);                           \
-    _Pragma("unroll") for (int j = 0; j < TM; ++j) AF[j] =                                               \
-        *reinterpret_cast<const bf16x8_t*>(&As[swz(wm * WM + 32 * j + l32, ch_)]);                       \
-  }
-#define DYLLM_GEMM_MMA(WF, AF)                                                                            \
-  _Pragma("unroll") for (int i = 0; i < TN; ++i) _Pragma("unroll") for (int j = 0; j < TM; ++j) acc[i][j] = \
-      __builtin_amdgcn_mfma_f32_32x32x16_bf16(WF[i], AF[j], acc[i][j], 0, 0, 0);
-    DYLLM_GEMM_FLOAD(0, wf0, af0)
-    DYLLM_GEMM_FLOAD(1, wf1, af1)
-    DYLLM_GEMM_MMA(wf0, af0)
-    DYLLM_GEMM_FLOAD(2, wf0, af0)
-    DYLLM_GEMM_MMA(wf1, af1)
-    DYLLM_GEMM_FLOAD(3, wf1, af1)
-    DYLLM_GEMM_MMA(wf0, af0)
-    DYLLM_GEMM_MMA(wf1, af1)
-#undef DYLLM_GEMM_FLOAD
-#undef DYLLM_GEMM_MMA
+    if (kt + 1 < nk) stage(kt + 1, cur ^ 1);
+    fload(As, 0, wf0, af0);
+    __builtin_amdgcn_sched_barrier(0);
+    fload(As, 1, wf1, af1);
+    mma(wf0, af0);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    fload(As, 2, wf0, af0);
+    mma(wf1, af1);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    fload(As, 3, wf1, af1);
+    mma(wf0, af0);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    mma(wf1, af1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   }
