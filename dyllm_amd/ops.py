@@ -13,6 +13,8 @@ Reference signatures mirrored:
 """
 from __future__ import annotations
 
+import time
+
 import torch
 
 from . import _lib
@@ -200,21 +202,38 @@ def saliency_stats(c_new, c_old, threshold):
     return stats, mask
 
 
+_HOST_META_TIMEOUT_S = 60.0
+
+
 class Compacted:
     """Device results of one compaction; ``count`` stays on the device until asked for."""
 
-    def __init__(self, idx64, idx32, idx_k, cu_salientlens, count, idx_k32=None, host_meta=None, event=None):
+    def __init__(self, idx64, idx32, idx_k, cu_salientlens, count, idx_k32=None, host_meta=None):
         self.idx64, self.idx32, self.idx_k, self.idx_k32 = idx64, idx32, idx_k, idx_k32
         self.cu_salientlens, self.count = cu_salientlens, count
-        self.host_meta, self.event = host_meta, event
+        self.host_meta = host_meta
 
     def host(self):
         """(count, cu_salientlens as a list): one device->host read for both. When the producing
-        kernel writes them into pinned host memory (host_meta + event), only that kernel's
-        completion is waited for, not the whole stream."""
-        if self.event is not None:
-            self.event.synchronize()
-            h = self.host_meta.tolist()
+        kernel writes them into pinned host memory (host_meta, pre-filled with -1 before the
+        launch; every entry is written once, by the block that owns it, and fenced to system
+        scope), the host polls that buffer until no entry is negative: no event, no stream
+        synchronisation, nothing enqueued between the kernel and the next launch."""
+        if self.host_meta is not None:
+            hm = self.host_meta
+            deadline = None
+            while True:
+                h = hm.tolist()
+                if min(h) >= 0:
+                    break
+                now = time.monotonic()
+                if deadline is None:
+                    deadline = now + _HOST_META_TIMEOUT_S
+                elif now > deadline:
+                    # the kernel did not run (an error earlier on the stream): surface it
+                    if torch.cuda.is_available():
+                        torch.cuda.synchronize()
+                    raise RuntimeError("salient count was not written by the compaction kernel")
         else:
             h = torch.cat([self.count, self.cu_salientlens]).cpu().tolist()
         return h[0], h[1:]
@@ -265,13 +284,12 @@ class StepBuffers:
         self.meta = torch.empty(B + 2, **i32)          # [count, cu_salientlens...]
         self.count, self.cu_sal = self.meta[0:1], self.meta[1:]
         self.host_meta = torch.empty(B + 2, dtype=torch.int32, pin_memory=True)
-        self.event = torch.cuda.Event()
         self.ws_bytes = _lib.load().dyllm_sparse_step_workspace_bytes(B, H, Hkv, D, Tq, Tk, max_k, Tq)
         self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
 
     def compacted(self):
         return Compacted(self.idx64, self.idx32, self.idx_k64, self.cu_sal, self.count, self.idx_k32,
-                         self.host_meta, self.event)
+                         self.host_meta)
 
 
 def sparse_attention_step(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_seq_starts, seq_ids, cu_seqlens_q,
@@ -281,6 +299,7 @@ def sparse_attention_step(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_s
     Results land in ``bufs`` (out / stats / mask and the next salient set, left on the device)."""
     Tq, H, D = q.shape
     Hkv = v_new.shape[1] if v_new.dim() == 3 else v_cache.shape[1] // D
+    bufs.host_meta.fill_(-1)   # "not written yet" for Compacted.host()
     _lib.call("dyllm_sparse_attention_step", _ptr(q), _ptr(k), _ptr(k_start), _ptr(v_cache), _ptr(v_seq_starts),
               _ptr(v_new), _ptr(c_cache), _ptr(c_seq_starts), _ptr(seq_ids), seq_ids.numel(), H, Hkv, D,
               _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), _ptr(cu_promptlens), int(max_seqlen_q), int(max_seqlen_k), Tq,
@@ -288,9 +307,6 @@ def sparse_attention_step(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_s
               _ptr(idx_k32), float(softmax_scale), float(threshold), _ptr(bufs.out), _ptr(bufs.stats),
               _ptr(bufs.mask), _ptr(bufs.idx64), _ptr(bufs.idx32), _ptr(bufs.idx_k64), _ptr(bufs.idx_k32),
               _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(bufs.host_meta), _ptr(bufs.ws), bufs.ws_bytes, _stream())
-    # the compaction kernel writes the salient count and per-sequence prefix straight into the
-    # pinned host buffer; the event marks when the host may read it
-    bufs.event.record()
     return bufs
 
 

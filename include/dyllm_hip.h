@@ -109,7 +109,9 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
  * also produced in K space); otherwise Q space == K space and idx_k* = idx_q*.
  * host_meta (optional, pinned host memory of batch + 2 int32 from hipHostMalloc) receives
  * [next_count, next_cu_salientlens...] directly from the compaction kernel, so the host can read
- * the salient count as soon as the call's work has completed without a device->host copy. */
+ * the salient count without a device->host copy: each entry is stored once, by the workgroup
+ * that owns it, and fenced to system scope before the kernel ends. A host that fills the buffer
+ * with -1 before the call can poll it until no entry is negative (no event needed). */
 size_t dyllm_sparse_step_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim, int64_t total_q,
                                          int64_t total_k, int max_seqlen_k, int64_t num_salient);
 int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_start, void* v_cache,

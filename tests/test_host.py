@@ -113,3 +113,18 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_pinned_salient_count_poll(monkeypatch):
+    """Compacted.host() reads the pinned [count, cu_salientlens...] buffer once no entry is
+    negative (-1 = not yet written by the compaction kernel), and gives up with an error if the
+    kernel never writes it."""
+    import torch
+    from dyllm_amd import ops
+
+    comp = ops.Compacted(None, None, None, None, None, host_meta=torch.tensor([5, 0, 2, 5], dtype=torch.int32))
+    assert comp.host() == (5, [0, 2, 5])
+    monkeypatch.setattr(ops, "_HOST_META_TIMEOUT_S", 0.05)
+    stale = ops.Compacted(None, None, None, None, None, host_meta=torch.tensor([5, 0, -1, 5], dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="not written"):
+        stale.host()
