@@ -7,7 +7,8 @@ step. Random-init bf16 weights N(0, 0.02); K/V/Q ~ N(0, 1). The caches hold a de
 the cached context with Gaussian noise of 0.5 x row RMS and get fresh K/V rows, which makes
 ~15% of the rows salient at every layer, as in the reference's synthetic recipe.
 
-One step = for every layer: K-cache scatter of the salient rows, dV + V-cache update,
+One step = for every layer: RoPE + K-cache scatter of the salient rows' projected keys (the
+fused K/V epilogue), dV + V-cache update,
 row-sparse attention of the salient queries vs the full cached K/V, column-sparse attention
 with the saliency statistics and the tau test, compaction of the next salient set (one host
 read of its size, as the reference's torch.nonzero), gathered SwiGLU GEMMs with the
@@ -17,7 +18,9 @@ pre-generated per layer). The caches are restored between steps (untimed) so eve
 step sees the same salient fraction.
 
 value = B * Lq / step time (tokens/s). The roofline object is for the dominant kernel, the
-gathered gate_up SwiGLU GEMM, timed with HIP events on its own launches.
+gathered gate_up SwiGLU GEMM, timed with HIP events on its own launches. The salient-row K/V
+projection GEMM (the step before the path, outside `value`) is timed on its own after the
+steps and reported as `kv_projection`.
 """
 from __future__ import annotations
 
@@ -106,10 +109,19 @@ def build_workload(cfg, layers, device, seed=0):
         k_new = (k_all[resp].float() + 0.1 * randn(Tq, Hkv, D).float()).to(torch.bfloat16)
         v_new = (v_all[resp].float() + 0.1 * randn(Tq, Hkv, D).float()).to(torch.bfloat16)
         del q_all, k_all, v_all
-        state.append(dict(attn=attn, k_cache=k_cache, mlp=mlp, q=q, k_new=k_new.view(Tq, -1),
-                          v_new=v_new.view(Tq, -1), c_saved=attn.context_cache.cache.clone(),
-                          v_saved=attn.v_cache.cache.clone()))
+        # stand-in for the salient-row K/V projection output: kv rows [k | v] of every queried row
+        kv_all = torch.cat([k_new.view(Tq, -1), v_new.view(Tq, -1)], dim=1).contiguous()
+        del k_new, v_new
+        state.append(dict(attn=attn, k_cache=k_cache, mlp=mlp, q=q, kv_all=kv_all,
+                          c_saved=attn.context_cache.cache.clone(), v_saved=attn.v_cache.cache.clone()))
     torch.cuda.synchronize()
+    # RoPE tables (rotary_embedding.py:19-38, theta 500000); every position 0, where the rotation
+    # is the identity, so the fused epilogue does its full work without changing the keys
+    # (and with them the salient fraction the workload is built for)
+    inv = 1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32, device=device) / D))
+    freqs = torch.outer(torch.arange(4096, dtype=torch.float32, device=device), inv)
+    rope_cos, rope_sin = freqs.cos().contiguous(), freqs.sin().contiguous()
+    pos0 = torch.zeros(Tq, dtype=torch.long, device=device)
 
     def set_sparse_context():
         return set_context(False, cu_seqlens_q=cu_q, cu_seqlens_q_cpu=cu_q_cpu, cu_seqlens_k=cu_k,
@@ -129,11 +141,13 @@ def build_workload(cfg, layers, device, seed=0):
             idx = ctx.idx_salient_row
             if n_sal is not None:
                 n_sal.append(idx.numel())
-            k_sal = ops.gather_rows_2D(st["k_new"], idx)
-            v_sal = ops.gather_rows_2D(st["v_new"], idx)
-            st["k_cache"].scatter_update(md.running_seqs_tensor, ctx.idx_salient_row_k, k_sal)
+            # the projection's [k | v] rows of the salient set (stand-in: a gather), then the fused
+            # epilogue: RoPE + K-cache scatter of k, the compact v of the step
+            kv = ops.gather_rows_2D(st["kv_all"], idx)
+            v_sal = st["k_cache"].scatter_kv_rope(md.running_seqs_tensor, ctx.idx_salient_row_k, kv, Hkv, pos0,
+                                                  rope_cos, rope_sin, ctx.idx_salient_row_i32)
             k_full = st["k_cache"].get_seqs(md.running_seqs_tensor, md.running_seqs).view(-1, Hkv, D)
-            o = st["attn"](st["q"], k_full, v_sal.view(-1, Hkv, D))
+            o = st["attn"](st["q"], k_full, v_sal)
             ev = events.get(li) if events is not None else None
             st["mlp"].forward_salient(o.view(Tq, H * D), gate_up_events=ev)
         return ctx
@@ -176,7 +190,10 @@ def cpu_baseline(cfg, n_sal, threads):
     dv[idx_k] = (0.1 * torch.randn(len(idx_k), Hkv, D, generator=g)).to(bf)
     w_gu = (0.02 * torch.randn(2 * inter, hid, generator=g)).to(bf)
     w_d = (0.02 * torch.randn(hid, inter, generator=g)).to(bf)
+    rope_cos, rope_sin = ref.rope_tables(D, 4096, 500000.0)
     t0 = time.perf_counter()
+    k[torch.from_numpy(idx_k)] = ref.rope_neox(k[torch.from_numpy(idx_k)], rope_cos, rope_sin,
+                                               torch.zeros(len(idx_k), dtype=torch.long))
     o_sal = ref.flash_attn_varlen(q[torch.from_numpy(idx_q)], k, v, cu_s, cu_k)
     new_c, _, mask = ref.attention_sparse_varlen(q, k, dv, c, o_sal, cu_q, cu_k, idx_q, cfg["tau"])
     idxs, cu_sal = ref.compact(mask.numpy(), cu_q)
@@ -186,6 +203,40 @@ def cpu_baseline(cfg, n_sal, threads):
     return dict(value=Tq / (t_layer * cfg["layers"]), unit="tokens/s", cores=threads, kind="port",
                 sample=f"1 of {cfg['layers']} layers at full config-1 shape ({n_sal} salient rows), "
                        f"{t_layer:.2f} s, x{cfg['layers']}")
+
+
+def time_kv_projection(cfg, n_sal, reps=24, copies=8):
+    """The salient-row K/V projection (dyllm_linear: kv = hidden[idx] . W_kv^T, llada.py:108) at
+    the bench shape, timed with HIP events on the launching stream, cycling through `copies`
+    weight matrices so the weights come from HBM as they do across 32 layers."""
+    import torch
+
+    from dyllm_amd import _lib, ops
+
+    dev = "cuda"
+    hid, kv_out = cfg["hidden"], 2 * cfg["kv_heads"] * cfg["head_dim"]
+    Tq = cfg["batch"] * cfg["response"]
+    g = torch.Generator(device=dev).manual_seed(1)
+    ws = [torch.empty(kv_out, hid, device=dev).normal_(0, 0.02, generator=g).to(torch.bfloat16)
+          for _ in range(copies)]
+    x = torch.empty(Tq, hid, device=dev).normal_(generator=g).to(torch.bfloat16)
+    rows = torch.sort(torch.randperm(Tq, device=dev, generator=g)[:n_sal]).values.to(torch.int32)
+    for w in ws:
+        ops.linear(x, w, rows_idx=rows)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i, (e0, e1) in enumerate(evs):
+        e0.record()
+        ops.linear(x, ws[i % copies], rows_idx=rows)
+        e1.record()
+    torch.cuda.synchronize()
+    us = sum(e0.elapsed_time(e1) for e0, e1 in evs) / reps * 1e3
+    flops = 2.0 * n_sal * hid * kv_out
+    tf = flops / (us * 1e-6) / 1e12
+    bm = _lib.load().dyllm_ffn_tile_rows(n_sal, kv_out, hid, 0)
+    return {"kernel": f"gemm_kernel<{bm},4,Store> (dyllm_linear: gathered kv_proj of the salient rows)",
+            "rows": n_sal, "avg_launch_us": round(us, 2), "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop_per_launch": flops}
 
 
 def profile_gate_up(cfg, reps=3):
@@ -276,6 +327,10 @@ def main():
     print(f"[bench] {ms_per_step:.3f} ms/step, avg salient rows per layer {avg_n:.1f}, "
           f"gate_up {avg_gate_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
+    kv_proj = time_kv_projection(cfg, int(round(avg_n)))
+    print(f"[bench] kv projection ({kv_proj['rows']} rows): {kv_proj['avg_launch_us']:.1f} us -> "
+          f"{kv_proj['achieved']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu_baseline:
         del wl
@@ -309,6 +364,7 @@ def main():
                      "avg_launch_us": round(avg_gate_ms * 1e3, 2),
                      "flop_per_launch": flops},
         "cpu_baseline": cpu,
+        "kv_projection": kv_proj,
     }
     print(json.dumps(line), flush=True)
 

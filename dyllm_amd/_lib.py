@@ -49,6 +49,10 @@ SIGNATURES = {
     "dyllm_ffn_gate_up": [_P, _L, _P, _L, _P, _L, _P, _I, _I, _P, _P],
     "dyllm_ffn_down": [_P, _L, _P, _L, _P, _I, _I, _P, _P, _P, c_size_t, _P],
     "dyllm_ffn_down_workspace_bytes": [_L, _L, _I, _I],
+    "dyllm_linear_workspace_bytes": [_L, _L, _I, _I],
+    "dyllm_linear": [_P, _L, _P, _L, _P, _L, _P, _I, _I, _P, _P, _P, c_size_t, _P],
+    "dyllm_kv_rope_scatter": [_P, _L, _L, _P, _P, _P, _P, _P, _I, _I, _I, _P, c_float, _P, _P, _P, _P, _P, _I, _P,
+                              _P],
     "dyllm_moe_gate": [_P, _P, _L, _I, _P, _I, _I, _I, _P, _P, _P],
     "dyllm_moe_align_block_size": [_P, _L, _I, _I, _P, _L, _P, _P, _P],
     "dyllm_fused_experts_workspace_bytes": [_L, _I, _I, _I, _I],
@@ -63,6 +67,7 @@ _RET = {
     "dyllm_sparse_step_workspace_bytes": c_size_t,
     "dyllm_swiglu_ffn_workspace_bytes": c_size_t,
     "dyllm_ffn_down_workspace_bytes": c_size_t,
+    "dyllm_linear_workspace_bytes": c_size_t,
     "dyllm_fused_experts_workspace_bytes": c_size_t,
 }
 

@@ -521,6 +521,38 @@ int dyllm_ffn_gate_up(const void* x, int64_t ld_x, const int32_t* rows_idx, int6
   return launch_gemm(GemmEpi::SwiGLU, g, rows, tm, 1, DYLLM_STREAM(stream));
 }
 
+// Store-epilogue GEMM out[out_rows[m] or m] = a(m) . W^T (+ bias), a(m) = A[rows_idx[m] or m],
+// with the tile / split-K plan of the expected row count.
+static int store_gemm(const void* a, int64_t lda, const int32_t* rows_idx, int64_t rows, const int32_t* rows_dev,
+                      int64_t rows_hint, const void* w, int n, int k, const void* bias, void* out, int64_t ldc,
+                      const int64_t* out_rows, void* workspace, size_t workspace_bytes, const char* ws_fn,
+                      hipStream_t s) {
+  GemmArgs d{};
+  d.A = static_cast<const uint16_t*>(a);
+  d.lda = lda;
+  d.a_ids = rows_idx;
+  d.a_div = 1;
+  d.id_limit = INT64_MAX;
+  d.W = static_cast<const uint16_t*>(w);
+  d.ldw = k;
+  d.Cout = static_cast<uint16_t*>(out);
+  d.ldc = ldc;
+  d.c_rows = out_rows;
+  d.bias = static_cast<const uint16_t*>(bias);
+  d.M = rows;
+  d.num_m_dev = rows_dev;
+  d.N = n;
+  d.K = k;
+  const GemmPlan pl = gemm_plan(hint_or(rows_hint, rows), n, k, GemmEpi::Store);
+  if (pl.ksplit > 1) {
+    const size_t need = gemm_partial_bytes(rows, n, pl.tile_m, pl.ksplit);
+    DYLLM_REQUIRE(workspace && workspace_bytes >= need,
+                  "workspace too small: need " + std::to_string(need) + " bytes (" + ws_fn + ")");
+    d.partial = static_cast<float*>(workspace);
+  }
+  return launch_gemm(GemmEpi::Store, d, rows, pl.tile_m, pl.ksplit, s);
+}
+
 int dyllm_ffn_down(const void* h, int64_t rows, const int32_t* rows_dev, int64_t rows_hint, const void* w_down,
                    int hidden, int intermediate, void* out, const int64_t* out_rows, void* workspace,
                    size_t workspace_bytes, void* stream) {
@@ -530,30 +562,75 @@ int dyllm_ffn_down(const void* h, int64_t rows, const int32_t* rows_dev, int64_t
   DYLLM_REQUIRE(hidden > 0 && hidden % 64 == 0, "hidden size must be a positive multiple of 64");
   DYLLM_REQUIRE(intermediate > 0 && intermediate % 64 == 0, "intermediate size must be a positive multiple of 64");
   if (rows <= 0) return 0;
-  GemmArgs d{};
-  d.A = static_cast<const uint16_t*>(h);
-  d.lda = intermediate;
-  d.a_div = 1;
-  d.id_limit = INT64_MAX;
-  d.W = static_cast<const uint16_t*>(w_down);
-  d.ldw = intermediate;
-  d.Cout = static_cast<uint16_t*>(out);
-  d.ldc = hidden;
-  d.c_rows = out_rows;
-  d.M = rows;
-  d.num_m_dev = rows_dev;
-  d.N = hidden;
-  d.K = intermediate;
-  const int64_t hr = hint_or(rows_hint, rows);
-  const GemmPlan pl = gemm_plan(hr, hidden, intermediate, GemmEpi::Store);
-  const int tm = pl.tile_m, ks = pl.ksplit;
-  if (ks > 1) {
-    const size_t need = gemm_partial_bytes(rows, hidden, tm, ks);
-    DYLLM_REQUIRE(workspace && workspace_bytes >= need,
-                  "workspace too small: need " + std::to_string(need) + " bytes (dyllm_ffn_down_workspace_bytes)");
-    d.partial = static_cast<float*>(workspace);
-  }
-  return launch_gemm(GemmEpi::Store, d, rows, tm, ks, DYLLM_STREAM(stream));
+  return store_gemm(h, intermediate, nullptr, rows, rows_dev, rows_hint, w_down, hidden, intermediate, nullptr, out,
+                    hidden, out_rows, workspace, workspace_bytes, "dyllm_ffn_down_workspace_bytes",
+                    DYLLM_STREAM(stream));
+}
+
+int dyllm_kv_rope_scatter(const void* kv, int64_t ld_kv, int64_t rows, const int32_t* rows_dev, const int32_t* pos_idx,
+                          const int64_t* positions, const float* cos_table, const float* sin_table,
+                          int max_position, int num_kv_heads, int head_dim, const void* k_norm_weight, float eps,
+                          void* k_cache, const int64_t* k_rows, const int32_t* cu_seqlens_k,
+                          const int64_t* seq_starts, const int64_t* seq_ids, int batch, void* v_out, void* stream) {
+  DYLLM_REQUIRE(head_dim == 128, "supported head dimension is 128");
+  DYLLM_REQUIRE(num_kv_heads >= 1, "num_kv_heads must be positive");
+  DYLLM_REQUIRE(max_position >= 1, "max_position must be positive");
+  DYLLM_REQUIRE(batch >= 1, "batch must be positive");
+  if (rows <= 0) return 0;
+  DYLLM_NONNULL(kv);
+  DYLLM_NONNULL(positions);
+  DYLLM_NONNULL(cos_table);
+  DYLLM_NONNULL(sin_table);
+  DYLLM_NONNULL(k_cache);
+  DYLLM_NONNULL(k_rows);
+  DYLLM_NONNULL(cu_seqlens_k);
+  DYLLM_NONNULL(seq_starts);
+  DYLLM_NONNULL(seq_ids);
+  DYLLM_NONNULL(v_out);
+  const int64_t kv_size = int64_t(num_kv_heads) * head_dim;
+  DYLLM_REQUIRE(ld_kv >= 2 * kv_size && ld_kv % 8 == 0, "kv row stride must be >= 2 * kv_size and a multiple of 8");
+  KvRopeArgs a{};
+  a.kv = static_cast<const uint16_t*>(kv);
+  a.ld_kv = ld_kv;
+  a.rows = rows;
+  a.rows_dev = rows_dev;
+  a.kv_size = kv_size;
+  a.Hkv = num_kv_heads;
+  a.pos_idx = pos_idx;
+  a.positions = positions;
+  a.cos = cos_table;
+  a.sin = sin_table;
+  a.max_position = max_position;
+  a.k_norm = static_cast<const uint16_t*>(k_norm_weight);
+  a.eps = eps;
+  a.k_cache = static_cast<uint16_t*>(k_cache);
+  a.ld_cache = kv_size;
+  a.k_rows = k_rows;
+  a.cu_k = cu_seqlens_k;
+  a.seq_starts = seq_starts;
+  a.seq_ids = seq_ids;
+  a.B = batch;
+  a.v_out = static_cast<uint16_t*>(v_out);
+  return launch_kv_rope_scatter(a, DYLLM_STREAM(stream));
+}
+
+size_t dyllm_linear_workspace_bytes(int64_t rows, int64_t rows_hint, int out_features, int in_features) {
+  return dyllm_ffn_down_workspace_bytes(rows, rows_hint, out_features, in_features);
+}
+
+int dyllm_linear(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const int32_t* rows_dev,
+                 int64_t rows_hint, const void* w, int out_features, int in_features, const void* bias, void* out,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  DYLLM_NONNULL(x);
+  DYLLM_NONNULL(w);
+  DYLLM_NONNULL(out);
+  DYLLM_REQUIRE(in_features > 0 && in_features % 64 == 0, "in_features must be a positive multiple of 64");
+  DYLLM_REQUIRE(out_features > 0 && out_features % 8 == 0, "out_features must be a positive multiple of 8");
+  DYLLM_REQUIRE(ld_x >= in_features && ld_x % 8 == 0, "x row stride must be >= in_features and a multiple of 8");
+  if (rows <= 0) return 0;
+  return store_gemm(x, ld_x, rows_idx, rows, rows_dev, rows_hint, w, out_features, in_features, bias, out,
+                    out_features, nullptr, workspace, workspace_bytes, "dyllm_linear_workspace_bytes",
+                    DYLLM_STREAM(stream));
 }
 
 int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,

@@ -47,6 +47,12 @@ constexpr int kGemmBN = 256;
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float bf16_rt(float x) { return __uint_as_float(uint32_t(f32_to_bf16(x)) << 16); }
+__device__ __forceinline__ void bf16x4_to_f32(uint2 v, float* f) {
+  f[0] = __uint_as_float(v.x << 16);
+  f[1] = __uint_as_float(v.x & 0xffff0000u);
+  f[2] = __uint_as_float(v.y << 16);
+  f[3] = __uint_as_float(v.y & 0xffff0000u);
+}
 
 // element offset of (row, 16-byte chunk) in a swizzled 64-element-wide tile. gfx950 serves a
 // 16-byte LDS read for 16 lanes at a time over 64 banks (two 128-byte rows): the 16 rows a
@@ -259,9 +265,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
         for (int q = 0; q < 4; ++q) {
           const int n = n0 + q * 8;
           if (n >= g.N) continue;
+          float bv[4] = {0.f, 0.f, 0.f, 0.f};
+          if (g.bias) bf16x4_to_f32(*reinterpret_cast<const uint2*>(g.bias + n), bv);
           uint2 st;
-          st.x = pack_bf16x2(acc[i][j][4 * q] * scale, acc[i][j][4 * q + 1] * scale);
-          st.y = pack_bf16x2(acc[i][j][4 * q + 2] * scale, acc[i][j][4 * q + 3] * scale);
+          st.x = pack_bf16x2(acc[i][j][4 * q] * scale + bv[0], acc[i][j][4 * q + 1] * scale + bv[1]);
+          st.y = pack_bf16x2(acc[i][j][4 * q + 2] * scale + bv[2], acc[i][j][4 * q + 3] * scale + bv[3]);
           *reinterpret_cast<uint2*>(crow + n) = st;
         }
       }
@@ -328,9 +336,11 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs g) {
       s.z += v.z;
       s.w += v.w;
     }
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (g.bias) bf16x4_to_f32(*reinterpret_cast<const uint2*>(g.bias + n), bv);
     uint2 st;
-    st.x = pack_bf16x2(s.x * scale, s.y * scale);
-    st.y = pack_bf16x2(s.z * scale, s.w * scale);
+    st.x = pack_bf16x2(s.x * scale + bv[0], s.y * scale + bv[1]);
+    st.y = pack_bf16x2(s.z * scale + bv[2], s.w * scale + bv[3]);
     *reinterpret_cast<uint2*>(g.Cout + drow * g.ldc + n) = st;
   }
 }

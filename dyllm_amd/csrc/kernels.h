@@ -19,6 +19,31 @@ struct RowMapArgs {
   int B;
 };
 int launch_row_map(RowMap mode, const RowMapArgs& a, hipStream_t stream);
+// Salient-row K/V epilogue: k -> (k_norm) -> rotary -> K-cache row, v -> v_out (rope.hip).
+struct KvRopeArgs {
+  const uint16_t* kv;            // [rows, ld_kv]: k (kv_size) then v (kv_size)
+  int64_t ld_kv;
+  int64_t rows;                  // capacity
+  const int32_t* rows_dev;       // optional device row count (<= rows)
+  int64_t kv_size;               // Hkv * 128
+  int Hkv;
+  const int32_t* pos_idx;        // optional [rows]: index into positions (else row j)
+  const int64_t* positions;
+  const float* cos;              // [max_position, 64]
+  const float* sin;
+  int64_t max_position;
+  const uint16_t* k_norm;        // optional [128] bf16
+  float eps;
+  uint16_t* k_cache;             // rows of ld_cache elements
+  int64_t ld_cache;
+  const int64_t* k_rows;         // [rows] packed K-space row of each salient row
+  const int32_t* cu_k;           // [B+1]
+  const int64_t* seq_starts;
+  const int64_t* seq_ids;        // [B]
+  int B;
+  uint16_t* v_out;               // [rows, kv_size]
+};
+int launch_kv_rope_scatter(const KvRopeArgs& a, hipStream_t s);
 int launch_scatter_dest_rows(const int64_t* row_idx, int64_t M, const int32_t* m_dev, const int32_t* cu,
                              const int64_t* seq_starts, const int64_t* seq_ids, int B, int64_t* dest, hipStream_t s);
 int launch_cosine_mask(const float* stats, uint8_t* mask, int64_t T, float tau, hipStream_t s);
@@ -122,6 +147,7 @@ struct GemmArgs {
   int c_by_id;
   const float* row_scale_f32;
   const uint16_t* row_scale_bf16;
+  const uint16_t* bias;       // Store epilogue, optional: bf16 [N] added in fp32 before rounding
   int64_t M;
   int N, K;
   int half_n;

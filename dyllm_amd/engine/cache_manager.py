@@ -192,6 +192,16 @@ class CacheManager:
         ctx = get_context()
         ops.scatter_update_cuda(self._slab, new, row_idx, ctx.cu_seqlens_k, self.seq_start_gpu, seq_ids)
 
+    def scatter_kv_rope(self, seq_ids: torch.Tensor, row_idx: torch.Tensor, kv: torch.Tensor, num_kv_heads: int,
+                        positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos_idx: torch.Tensor,
+                        k_norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6) -> torch.Tensor:
+        """scatter_update of the salient rows' rotated keys, fused with their k_norm / RoPE
+        (llada.py:108-143): kv = [k | v] rows of the salient-row projection; returns v."""
+        ctx = get_context()
+        return ops.kv_rope_scatter(kv, num_kv_heads, positions, cos, sin, self._slab, row_idx, ctx.cu_seqlens_k,
+                                   self.seq_start_gpu, seq_ids, pos_idx=pos_idx, k_norm_weight=k_norm_weight,
+                                   eps=eps)
+
     def finish(self, finished_seq_ids: List[int]):
         if len(finished_seq_ids) == 0:
             return False

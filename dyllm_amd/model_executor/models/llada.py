@@ -147,16 +147,15 @@ class LLaDAAttention(nn.Module):
             self.k_cache.reset_full(k.flatten(1), md.running_seqs_tensor, seq_ids_list=md.running_seqs)
             o = self.attn(q, k, v)
         else:
-            idx = ctx.idx_salient_row
-            kv = F.linear(ops.gather_rows_2D(hidden, idx), self.kv_proj, self.kv_bias)
-            k, v = kv.split([self.kv_size, self.kv_size], dim=-1)
-            k = k.reshape(-1, self.num_kv_heads, self.head_dim)
-            if self.k_norm is not None:
-                k = self.k_norm(k)
-            k = self.rotary.rotate(positions[idx], k)
-            v = v.reshape(-1, self.num_kv_heads, self.head_dim)
-            kidx = ctx.idx_salient_row_k if ctx.idx_salient_row_k is not None else idx
-            self.k_cache.scatter_update(md.running_seqs_tensor, kidx, k.flatten(1))
+            # salient-row K/V projection as one gathered GEMM, then one epilogue pass: k_norm,
+            # RoPE and the K-cache scatter of k, the compact v of the step (llada.py:108-143)
+            idx = ctx.idx_salient_row_i32
+            kv = ops.linear(hidden, self.kv_proj, self.kv_bias, rows_idx=idx)
+            kidx = ctx.idx_salient_row_k if ctx.idx_salient_row_k is not None else ctx.idx_salient_row
+            kn = self.k_norm
+            v = self.k_cache.scatter_kv_rope(md.running_seqs_tensor, kidx, kv, self.num_kv_heads, positions,
+                                             self.rotary.cos, self.rotary.sin, idx,
+                                             None if kn is None else kn.weight, 1e-6 if kn is None else kn.eps)
             k_full = self.k_cache.get_seqs(md.running_seqs_tensor, md.running_seqs)
             o = self.attn(q, k_full.view(-1, self.num_kv_heads, self.head_dim), v)
         out = F.linear(o.flatten(1), self.o_proj)

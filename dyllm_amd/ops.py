@@ -461,6 +461,73 @@ def ffn_down(h, w_down, out=None, out_rows=None, count=None, hint=0):
     return out
 
 
+def linear(x, w, bias=None, rows_idx=None, count=None, hint=0):
+    """F.linear(x[rows_idx], w, bias) as one gathered GEMM (dyllm_linear): the salient-row
+    kv_proj of llada.py:108 / dream.py:103 / lladamoe.py:204. ``count``/``hint`` as for
+    ffn_gate_up (rows beyond count[0] are left unwritten)."""
+    _check(x, "x", torch.bfloat16, 2)
+    _check(w, "w", torch.bfloat16, 2)
+    n_out, k_in = w.shape
+    if x.shape[1] != k_in:
+        raise RuntimeError("x must be [rows, in_features] with in_features = w.shape[1]")
+    if x.stride(1) != 1:
+        raise RuntimeError("x rows must be contiguous")
+    if bias is not None:
+        _check(bias, "bias", torch.bfloat16, 1)
+        if bias.numel() != n_out or not bias.is_contiguous():
+            raise RuntimeError("bias must be a contiguous [out_features] tensor")
+    ri = _i32(rows_idx) if rows_idx is not None else None
+    M = ri.numel() if ri is not None else x.shape[0]
+    out = torch.empty((M, n_out), dtype=x.dtype, device=x.device)
+    if M:
+        ws_bytes = _lib.load().dyllm_linear_workspace_bytes(M, int(hint), n_out, k_in)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+        _lib.call("dyllm_linear", _ptr(x), x.stride(0), _ptr(ri), M, _ptr(count), int(hint), _ptr(w), n_out, k_in,
+                  _ptr(bias), _ptr(out), _ptr(ws), ws_bytes, _stream())
+    return out
+
+
+def kv_rope_scatter(kv, num_kv_heads, positions, cos, sin, k_cache, k_rows, cu_seqlens_k, seq_starts, seq_ids,
+                    pos_idx=None, k_norm_weight=None, eps=1e-6, count=None):
+    """K/V epilogue of the salient-row projection (dyllm_kv_rope_scatter): for each row j of
+    kv = [k | v], k -> (per-head RMSNorm with k_norm_weight) -> neox RoPE at
+    positions[pos_idx[j] or j] -> K-cache row of packed K row k_rows[j]; returns v
+    [rows, Hkv, 128] (the sparse step's v_new). cos / sin: fp32 [max_position, 64]."""
+    _check(kv, "kv", torch.bfloat16, 2)
+    _check_cache(k_cache, seq_starts, seq_ids)
+    _check(positions, "positions", None, 1)
+    positions = _i64(positions)
+    for t, n in ((cos, "cos"), (sin, "sin")):
+        _check(t, n, torch.float32, 2)
+        if t.shape[1] != 64 or not t.is_contiguous():
+            raise RuntimeError(f"{n} must be a contiguous [max_position, 64] fp32 table")
+    if cos.shape != sin.shape:
+        raise RuntimeError("cos and sin tables must have the same shape")
+    kv_size = num_kv_heads * 128
+    if kv.shape[1] < 2 * kv_size or kv.stride(1) != 1:
+        raise RuntimeError("kv rows must hold k then v (2 * num_kv_heads * 128 contiguous values)")
+    if k_cache.shape[1] != kv_size or k_cache.dtype != torch.bfloat16:
+        raise RuntimeError("k_cache must be bf16 [rows, num_kv_heads * 128]")
+    if k_norm_weight is not None:
+        _check(k_norm_weight, "k_norm_weight", torch.bfloat16, 1)
+        if k_norm_weight.numel() != 128:
+            raise RuntimeError("k_norm_weight must have head_dim (128) entries")
+    rows = kv.shape[0]
+    kr = _i64(k_rows)
+    if kr.numel() < rows:
+        raise RuntimeError("k_rows must have one entry per kv row")
+    pi = _i32(pos_idx) if pos_idx is not None else None
+    if pi is not None and pi.numel() < rows:
+        raise RuntimeError("pos_idx must have one entry per kv row")
+    v_out = torch.empty((rows, num_kv_heads, 128), dtype=kv.dtype, device=kv.device)
+    if rows:
+        _lib.call("dyllm_kv_rope_scatter", _ptr(kv), kv.stride(0), rows, _ptr(count), _ptr(pi), _ptr(positions),
+                  _ptr(cos), _ptr(sin), cos.shape[0], num_kv_heads, 128, _ptr(k_norm_weight), float(eps),
+                  _ptr(k_cache), _ptr(kr), _ptr(_i32(cu_seqlens_k)), _ptr(seq_starts), _ptr(seq_ids),
+                  seq_ids.numel(), _ptr(v_out), _stream())
+    return v_out
+
+
 def swiglu_ffn(x, w_gate_up, w_down, rows_idx=None, out=None, out_rows=None):
     """down(silu(a Wg^T) * (a Wu^T)) for a = x[rows_idx] (or all rows of x). With
     ``out``/``out_rows`` the result rows are written to out[out_rows[m]] (in-place scatter

@@ -214,6 +214,32 @@ int dyllm_ffn_down(const void* h, int64_t rows, const int32_t* rows_dev, int64_t
 /* Tile height (128/192/256) the FFN GEMMs use for `rows` rows, output width n and depth k. */
 int dyllm_ffn_tile_rows(int64_t rows, int n, int k, int swiglu);
 
+/* ---- salient-row K/V projection (the step before the sparse attention) ------------------ */
+
+/* Gathered linear: out[m] = x[rows_idx ? rows_idx[m] : m] . w^T (+ bias), out [rows,
+ * out_features] bf16, fp32 accumulation rounded once (F.linear, linear.py). Replaces
+ * kv_proj(hidden_states[idx_salient_row]) of llada.py:108, dream.py:103, lladamoe.py:204.
+ * w: [out_features, in_features]; bias: optional bf16 [out_features]. rows / rows_dev /
+ * rows_hint as for dyllm_ffn_gate_up; the workspace holds split-K partials. */
+size_t dyllm_linear_workspace_bytes(int64_t rows, int64_t rows_hint, int out_features, int in_features);
+int dyllm_linear(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const int32_t* rows_dev,
+                 int64_t rows_hint, const void* w, int out_features, int in_features, const void* bias, void* out,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* K/V epilogue of that projection for the salient rows j < rows (or < *rows_dev): kv row j holds
+ * k then v ([num_kv_heads * 128] each, row stride ld_kv). k: optional per-head RMSNorm with
+ * k_norm_weight (bf16 [128], lladamoe.py:206-207 / layernorm.py:15-24), then the neox rotary
+ * embedding at positions[pos_idx ? pos_idx[j] : j] clamped to max_position - 1
+ * (rotary_embedding.py:8-16, 40-54; cos/sin tables fp32 [max_position, 64]), written to the
+ * K-cache row of packed K-space row k_rows[j] (the addressing of dyllm_scatter_update,
+ * llada.py:136-143). v: copied to v_out [rows, num_kv_heads * 128]. Replaces the zero-filled
+ * k_temp, the rotary over all rows and the scatter of llada.py:108-143. */
+int dyllm_kv_rope_scatter(const void* kv, int64_t ld_kv, int64_t rows, const int32_t* rows_dev, const int32_t* pos_idx,
+                          const int64_t* positions, const float* cos_table, const float* sin_table,
+                          int max_position, int num_kv_heads, int head_dim, const void* k_norm_weight, float eps,
+                          void* k_cache, const int64_t* k_rows, const int32_t* cu_seqlens_k,
+                          const int64_t* seq_starts, const int64_t* seq_ids, int batch, void* v_out, void* stream);
+
 /* ---- MoE ------------------------------------------------------------------------------- */
 
 /* Router: topk_weights (bf16) / topk_ids (int32) [tokens, top_k] from fp32 softmax of

@@ -21,6 +21,11 @@ index work). Each function cites the reference file:line whose semantics it rest
 * ``swiglu_ffn``                -- textbook F.silu(g) * u composition vs per-row loop.
 * ``moe_gate`` / ``naive_experts`` -- per-token brute-force loop over the top-k experts.
 * ``moe_align_block_size``      -- invariants (permutation, padding, expert ownership).
+* ``rope_neox`` / ``rope_tables`` -- position 0 is the identity, each (d, d+64) pair keeps
+                                   its length, and the result equals the complex product
+                                   (x1 + i x2) e^{i p theta_d} (textbook RoPE).
+* ``rms_norm``                  -- unit RMS before the weight, weight applied per column.
+* ``salient_kv_project``        -- composition of the above with a per-row loop linear.
 """
 from __future__ import annotations
 
@@ -297,6 +302,54 @@ def swiglu_ffn(x, w_gate_up, w_down):
     I = gu.shape[1] // 2
     h = bf16_round(F.silu(gu[:, :I]) * gu[:, I:])
     return h @ w_down.float().t()
+
+
+# ---------------------------------------------------------------------------
+# (next) salient-row K/V projection: linear + k_norm + RoPE + K-cache scatter
+# ---------------------------------------------------------------------------
+def rope_tables(head_dim, max_position, base):
+    """cos / sin tables of RotaryEmbedding.__init__ (rotary_embedding.py:19-38): fp32
+    inv_freq = base^(-2i/D), freqs = positions x inv_freq; [max_position, D/2] each."""
+    inv = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    f = torch.outer(torch.arange(max_position, dtype=torch.float32), inv)
+    return f.cos(), f.sin()
+
+
+def rope_neox(x, cos, sin, positions, max_position=None):
+    """apply_rotary_emb (rotary_embedding.py:8-16) at clamped positions (:47-52): halves
+    x1 | x2 of each head, y1 = x1 cos - x2 sin, y2 = x2 cos + x1 sin in fp32 (each product
+    and sum rounded, no contraction), result rounded to bf16. x: [n, H, D] bf16."""
+    mp = cos.shape[0] if max_position is None else max_position
+    pos = torch.as_tensor(positions, dtype=torch.long).clamp(0, mp - 1)
+    c, s = cos[pos].unsqueeze(1), sin[pos].unsqueeze(1)
+    x1, x2 = x.float().chunk(2, dim=-1)
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(BF16)
+
+
+def rms_norm(x, weight, eps):
+    """RMSNorm.rms_forward (layernorm.py:15-24): fp32 mean of squares over the last dim,
+    x * rsqrt(var + eps) rounded to bf16, then times the bf16 weight (rounded again)."""
+    xf = x.float()
+    y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(BF16)
+    return (y.float() * weight.float()).to(BF16)
+
+
+def salient_kv_project(hidden, idx, w_kv, bias, positions, cos, sin, num_kv_heads, k_norm_weight=None, eps=1e-6):
+    """The salient-row K/V path of the sparse step (llada.py:108-143, lladamoe.py:204-239):
+    kv = kv_proj(hidden[idx]) (bf16 output of an fp32-accumulated product, plus bias),
+    k -> optional per-head k_norm -> RoPE at positions[idx]; returns (k, v) bf16
+    [n, Hkv, 128] -- k is what scatter_update writes into the K cache."""
+    idx = torch.as_tensor(idx, dtype=torch.long)
+    kv = hidden[idx].float() @ w_kv.float().t()
+    if bias is not None:
+        kv = kv + bias.float()
+    kv = kv.to(BF16)
+    kvs = w_kv.shape[0] // 2
+    k = kv[:, :kvs].reshape(-1, num_kv_heads, 128)
+    v = kv[:, kvs:].reshape(-1, num_kv_heads, 128)
+    if k_norm_weight is not None:
+        k = rms_norm(k, k_norm_weight, eps)
+    return rope_neox(k, cos, sin, positions[idx]), v
 
 
 # ---------------------------------------------------------------------------

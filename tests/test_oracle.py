@@ -258,3 +258,61 @@ def test_synthetic_perturbation_known_answer():
     assert torch.nonzero(mask).squeeze(-1).tolist() == pert.tolist()
     cos = ref.cosine_from_stats(st)[pert]
     assert ((cos - 1 / math.sqrt(1.25)).abs() < 0.02).all()
+
+
+def test_rope_pinned_by_identity_norm_and_complex_form():
+    """RoPE restatement: position 0 leaves x unchanged, each (d, d+64) pair keeps its length,
+    and the rotation equals the complex product (x1 + i x2) e^{i p theta_d} with
+    theta_d = base^(-2d/D) (a swapped sin sign or a half-swap fails all three)."""
+    g = torch.Generator().manual_seed(3)
+    cos, sin = ref.rope_tables(128, 4096, 10000.0)
+    x = torch.randn(16, 4, 128, generator=g).to(BF)
+    assert torch.equal(ref.rope_neox(x, cos, sin, torch.zeros(16, dtype=torch.long)), x)
+    pos = torch.randint(0, 4096, (16,), generator=g)
+    y = ref.rope_neox(x, cos, sin, pos).float()
+    n_in = x.float()[..., :64] ** 2 + x.float()[..., 64:] ** 2
+    n_out = y[..., :64] ** 2 + y[..., 64:] ** 2
+    assert torch.allclose(n_out, n_in, rtol=2e-2, atol=1e-3)
+    theta = 10000.0 ** (-torch.arange(0, 128, 2, dtype=torch.float64) / 128)
+    z = torch.complex(x.double()[..., :64], x.double()[..., 64:]) * torch.exp(
+        1j * pos.double()[:, None, None] * theta)
+    want = torch.cat((z.real, z.imag), -1)
+    assert (y.double() - want).abs().max() < 0.02 * want.abs().max()
+    # positions past the table are clamped to its last row
+    assert torch.equal(ref.rope_neox(x, cos, sin, torch.full((16,), 10 ** 6)),
+                       ref.rope_neox(x, cos, sin, torch.full((16,), 4095)))
+
+
+def test_rms_norm_unit_rms_and_weight():
+    g = torch.Generator().manual_seed(4)
+    x = (3.0 * torch.randn(32, 128, generator=g)).to(BF)
+    one = torch.ones(128, dtype=BF)
+    y = ref.rms_norm(x, one, 1e-6).float()
+    assert torch.allclose(y.pow(2).mean(-1), torch.ones(32), rtol=2e-2)
+    w = torch.linspace(0.5, 2.0, 128).to(BF)
+    assert torch.allclose(ref.rms_norm(x, w, 1e-6).float(), (y * w.float()), rtol=1e-2, atol=1e-2)
+
+
+def test_salient_kv_project_per_row_loop():
+    """Composition check: per-row loop of linear (+bias) -> k_norm -> RoPE vs the batched form."""
+    g = torch.Generator().manual_seed(5)
+    Hkv, hid = 2, 64
+    hidden = torch.randn(10, hid, generator=g).to(BF)
+    w = (0.1 * torch.randn(2 * Hkv * 128, hid, generator=g)).to(BF)
+    b = (0.1 * torch.randn(2 * Hkv * 128, generator=g)).to(BF)
+    kn = (1 + 0.1 * torch.randn(128, generator=g)).to(BF)
+    pos = torch.arange(100, 110)
+    cos, sin = ref.rope_tables(128, 512, 10000.0)
+    idx = torch.tensor([7, 2, 5])
+    k, v = ref.salient_kv_project(hidden, idx, w, b, pos, cos, sin, Hkv, kn, 1e-6)
+    for j, r in enumerate(idx.tolist()):
+        kv = (sum(hidden[r].float()[c] * w.float()[:, c] for c in range(hid)) + b.float()).to(BF)
+        kr = kv[:Hkv * 128].view(Hkv, 128)
+        assert torch.allclose(v[j].float(), kv[Hkv * 128:].view(Hkv, 128).float(), atol=1e-2)
+        for h in range(Hkv):
+            xf = kr[h].float()
+            xn = ((xf / torch.sqrt(xf.pow(2).mean() + 1e-6)).to(BF).float() * kn.float()).to(BF).float()
+            p = int(pos[r])
+            c, s_ = cos[p], sin[p]
+            want = torch.cat((xn[:64] * c - xn[64:] * s_, xn[64:] * c + xn[:64] * s_)).to(BF).float()
+            assert (k[j, h].float() - want).abs().max() <= 0.05
