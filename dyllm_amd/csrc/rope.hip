@@ -10,58 +10,93 @@
 // This replaces the reference's zero-filled [T, kv] temporary, the rotary over all T rows and the
 // separate scatter with one pass over the n salient rows.
 //
-// One wavefront per (row, kv head): lane i holds the rotation pair (d = i, d = i + 64) of the
-// 128-wide head, so the rotation and the head RMS reduction stay inside the wavefront.
+// One 256-thread workgroup per salient row: the row's index chain (position, sequence, cache
+// row) is uniform across the workgroup and read once with scalar loads. Thread t works on kv head
+// t / 8 (heads beyond 32 loop) and, inside it, on the 8 rotation pairs (d, d + 64) for
+// d = 8 (t % 8) ... 8 (t % 8) + 7: 16-byte loads of k, cos and sin, the head's RMS reduced over
+// its 8 threads.
 #include "kernels.h"
 
 namespace dyllm {
 
-__global__ __launch_bounds__(256) void kv_rope_scatter_kernel(KvRopeArgs a) {
-  const int64_t wid = (int64_t(blockIdx.x) * 256 + threadIdx.x) >> 6;
-  const int lane = threadIdx.x & 63;
-  const int64_t n = a.rows_dev ? int64_t(a.rows_dev[0]) : a.rows;
-  const int64_t j = wid / a.Hkv;
-  const int h = int(wid - j * a.Hkv);
-  if (j >= n || j >= a.rows) return;
-  constexpr int D = 128, HALF = 64;
-
-  const uint16_t* kr = a.kv + j * a.ld_kv + int64_t(h) * D;
-  float x1 = bf16_to_f32(kr[lane]);
-  float x2 = bf16_to_f32(kr[lane + HALF]);
-  if (a.k_norm) {
-    float ss = x1 * x1 + x2 * x2;
+__device__ __forceinline__ void unpack8(const uint4 v, float* f) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    const float r = rsqrtf(ss / float(D) + a.eps);
-    x1 = __fmul_rn(bf16_to_f32(f32_to_bf16(x1 * r)), bf16_to_f32(a.k_norm[lane]));
-    x2 = __fmul_rn(bf16_to_f32(f32_to_bf16(x2 * r)), bf16_to_f32(a.k_norm[lane + HALF]));
-    x1 = bf16_to_f32(f32_to_bf16(x1));
-    x2 = bf16_to_f32(f32_to_bf16(x2));
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
   }
+}
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                    pack_bf16x2(f[6], f[7]));
+}
+__device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+__global__ __launch_bounds__(256) void kv_rope_scatter_kernel(KvRopeArgs a) {
+  const int64_t j = blockIdx.x;
+  const int64_t n = a.rows_dev ? int64_t(a.rows_dev[0]) : a.rows;
+  if (j >= n) return;
+  constexpr int D = 128, HALF = 64;
+  const int t = threadIdx.x;
+
+  // row-uniform chain
   int64_t pos = a.positions[a.pos_idx ? int64_t(a.pos_idx[j]) : j];
   pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
-  const float c = a.cos[pos * HALF + lane], s = a.sin[pos * HALF + lane];
-  // rounded products and sums in this order (no contraction): the eager fp32 formula
-  const float y1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-  const float y2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
-
   const int64_t kk = a.k_rows[j];
   const int b = find_segment(a.cu_k, a.B + 1, kk);
   const int64_t dest = a.seq_starts[a.seq_ids[b]] + (kk - a.cu_k[b]);
-  uint16_t* kc = a.k_cache + dest * a.ld_cache + int64_t(h) * D;
-  kc[lane] = f32_to_bf16(y1);
-  kc[lane + HALF] = f32_to_bf16(y2);
+  const uint16_t* krow = a.kv + j * a.ld_kv;
+  uint16_t* crow = a.k_cache + dest * a.ld_cache;
 
-  if (lane < D / 8) {
-    const uint4* vr = reinterpret_cast<const uint4*>(a.kv + j * a.ld_kv + a.kv_size + int64_t(h) * D);
-    reinterpret_cast<uint4*>(a.v_out + j * a.kv_size + int64_t(h) * D)[lane] = vr[lane];
+  const int d0 = (t & 7) * 8;
+  float c[8], s[8];
+  *reinterpret_cast<float4*>(c) = *reinterpret_cast<const float4*>(a.cos + pos * HALF + d0);
+  *reinterpret_cast<float4*>(c + 4) = *reinterpret_cast<const float4*>(a.cos + pos * HALF + d0 + 4);
+  *reinterpret_cast<float4*>(s) = *reinterpret_cast<const float4*>(a.sin + pos * HALF + d0);
+  *reinterpret_cast<float4*>(s + 4) = *reinterpret_cast<const float4*>(a.sin + pos * HALF + d0 + 4);
+  float w1[8], w2[8];
+  if (a.k_norm) {
+    unpack8(*reinterpret_cast<const uint4*>(a.k_norm + d0), w1);
+    unpack8(*reinterpret_cast<const uint4*>(a.k_norm + d0 + HALF), w2);
   }
+  for (int h = t >> 3; h < a.Hkv; h += 32) {
+    float x1[8], x2[8];
+    unpack8(*reinterpret_cast<const uint4*>(krow + h * D + d0), x1);
+    unpack8(*reinterpret_cast<const uint4*>(krow + h * D + d0 + HALF), x2);
+    if (a.k_norm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+      ss += __shfl_xor(ss, 1, 64);
+      ss += __shfl_xor(ss, 2, 64);
+      ss += __shfl_xor(ss, 4, 64);
+      const float r = rsqrtf(ss / float(D) + a.eps);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        x1[i] = bf16_round(__fmul_rn(bf16_round(x1[i] * r), w1[i]));
+        x2[i] = bf16_round(__fmul_rn(bf16_round(x2[i] * r), w2[i]));
+      }
+    }
+    float y1[8], y2[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // rounded products and sums in this order (no contraction): the eager fp32 formula
+      y1[i] = __fsub_rn(__fmul_rn(x1[i], c[i]), __fmul_rn(x2[i], s[i]));
+      y2[i] = __fadd_rn(__fmul_rn(x2[i], c[i]), __fmul_rn(x1[i], s[i]));
+    }
+    *reinterpret_cast<uint4*>(crow + h * D + d0) = pack8(y1);
+    *reinterpret_cast<uint4*>(crow + h * D + d0 + HALF) = pack8(y2);
+  }
+  // v: kv_size values -> v_out row j (16 bytes per thread per pass)
+  const uint4* vr = reinterpret_cast<const uint4*>(krow + a.kv_size);
+  uint4* vo = reinterpret_cast<uint4*>(a.v_out + j * a.kv_size);
+  for (int64_t i = t; i < a.kv_size / 8; i += 256) vo[i] = vr[i];
 }
 
 int launch_kv_rope_scatter(const KvRopeArgs& a, hipStream_t s) {
   if (a.rows <= 0) return 0;
-  const int64_t waves = a.rows * a.Hkv;
-  kv_rope_scatter_kernel<<<unsigned(cdiv(waves, 4)), 256, 0, s>>>(a);
+  kv_rope_scatter_kernel<<<unsigned(a.rows), 256, 0, s>>>(a);
   return check_launch("kv_rope_scatter_kernel");
 }
 
