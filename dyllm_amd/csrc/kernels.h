@@ -19,6 +19,22 @@ struct RowMapArgs {
   int B;
 };
 int launch_row_map(RowMap mode, const RowMapArgs& a, hipStream_t stream);
+// RMSNorm with the optional fused residual add (norm.hip).
+struct NormArgs {
+  const uint16_t* x;         // [rows, ld_x]
+  int64_t ld_x;
+  const uint16_t* residual;  // optional [rows, ld_r]
+  int64_t ld_r;
+  const uint16_t* weight;    // [hidden]
+  int64_t rows;
+  int hidden;
+  float eps;
+  uint16_t* out;             // [rows, ld_out] (may alias x)
+  int64_t ld_out;
+  uint16_t* residual_out;    // with residual: [rows, ld_ro] = bf16(x + residual) (may alias residual)
+  int64_t ld_ro;
+};
+int launch_add_rms_norm(const NormArgs& a, hipStream_t s);
 // Salient-row K/V epilogue: k -> (k_norm) -> rotary -> K-cache row, v -> v_out (rope.hip).
 struct KvRopeArgs {
   const uint16_t* kv;            // [rows, ld_kv]: k (kv_size) then v (kv_size)

@@ -37,6 +37,14 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(hidden, dtype=torch.bfloat16, device=device), requires_grad=False)
 
     def forward(self, x, residual=None):
+        hidden = x.shape[-1]
+        if x.is_cuda and x.dtype == torch.bfloat16 and 1024 <= hidden <= 8192 and hidden % 8 == 0:
+            # decoder-layer norms over the hidden size: one native pass per row (dyllm_rms_norm)
+            x2 = x.reshape(-1, hidden).contiguous()
+            if residual is None:
+                return ops.rms_norm(x2, self.weight, self.eps).view(x.shape)
+            y, r = ops.rms_norm(x2, self.weight, self.eps, residual=residual.reshape(-1, hidden).contiguous())
+            return y.view(x.shape), r.view(residual.shape)
         if residual is not None:
             xf = x.float() + residual.float()
             residual = xf.to(x.dtype)

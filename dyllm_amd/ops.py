@@ -528,6 +528,35 @@ def kv_rope_scatter(kv, num_kv_heads, positions, cos, sin, k_cache, k_rows, cu_s
     return v_out
 
 
+def rms_norm(x, weight, eps, residual=None, out=None, residual_out=None):
+    """RMSNorm (layernorm.py:15-24) or, with ``residual``, the fused add + RMSNorm
+    (layernorm.py:29-37) in one pass per row (dyllm_rms_norm). Returns y, or (y, residual_out)
+    with residual_out = bf16(x + residual); ``out`` / ``residual_out`` may be x / residual
+    (in place)."""
+    _check(x, "x", torch.bfloat16, 2)
+    _check(weight, "weight", torch.bfloat16, 1)
+    rows, hidden = x.shape
+    if weight.numel() != hidden or not weight.is_contiguous():
+        raise RuntimeError("weight must be a contiguous [hidden] tensor")
+    if x.stride(1) != 1:
+        raise RuntimeError("x rows must be contiguous")
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out, "out", torch.bfloat16, 2)
+    if residual is not None:
+        _check(residual, "residual", torch.bfloat16, 2)
+        if residual.shape != x.shape or residual.stride(1) != 1:
+            raise RuntimeError("residual must match x with contiguous rows")
+        if residual_out is None:
+            residual_out = torch.empty_like(residual)
+    if rows:
+        _lib.call("dyllm_rms_norm", _ptr(x), x.stride(0), _ptr(residual),
+                  residual.stride(0) if residual is not None else 0, _ptr(weight), rows, hidden, float(eps),
+                  _ptr(out), out.stride(0), _ptr(residual_out),
+                  residual_out.stride(0) if residual_out is not None else 0, _stream())
+    return out if residual is None else (out, residual_out)
+
+
 def swiglu_ffn(x, w_gate_up, w_down, rows_idx=None, out=None, out_rows=None):
     """down(silu(a Wg^T) * (a Wu^T)) for a = x[rows_idx] (or all rows of x). With
     ``out``/``out_rows`` the result rows are written to out[out_rows[m]] (in-place scatter

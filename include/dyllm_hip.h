@@ -240,6 +240,17 @@ int dyllm_kv_rope_scatter(const void* kv, int64_t ld_kv, int64_t rows, const int
                           void* k_cache, const int64_t* k_rows, const int32_t* cu_seqlens_k,
                           const int64_t* seq_starts, const int64_t* seq_ids, int batch, void* v_out, void* stream);
 
+/* ---- decoder-layer RMSNorm (the steps either side of the path) ------------------------------ */
+
+/* RMSNorm.rms_forward / add_rms_forward (layernorm.py:15-37) in one pass per row: with a
+ * residual, s = x + residual in fp32 and residual_out = bf16(s); without, s = x; then
+ * out = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * weight). weight: bf16 [hidden]; hidden a
+ * multiple of 8, at most 8192; out may alias x and residual_out may alias residual. Replaces the
+ * post-attention (and input) layernorm of llada.py:174-186 / dream.py / lladamoe.py on all rows. */
+int dyllm_rms_norm(const void* x, int64_t ld_x, const void* residual, int64_t ld_residual, const void* weight,
+                   int64_t rows, int hidden, float eps, void* out, int64_t ld_out, void* residual_out,
+                   int64_t ld_residual_out, void* stream);
+
 /* ---- MoE ------------------------------------------------------------------------------- */
 
 /* Router: topk_weights (bf16) / topk_ids (int32) [tokens, top_k] from fp32 softmax of

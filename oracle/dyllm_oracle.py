@@ -24,7 +24,9 @@ index work). Each function cites the reference file:line whose semantics it rest
 * ``rope_neox`` / ``rope_tables`` -- position 0 is the identity, each (d, d+64) pair keeps
                                    its length, and the result equals the complex product
                                    (x1 + i x2) e^{i p theta_d} (textbook RoPE).
-* ``rms_norm``                  -- unit RMS before the weight, weight applied per column.
+* ``rms_norm`` / ``add_rms_norm`` -- unit RMS before the weight, weight applied per column;
+                                   the fused form equals rms_norm of the fp32 sum (zero residual:
+                                   identical to rms_norm) and a per-row loop.
 * ``salient_kv_project``        -- composition of the above with a per-row loop linear.
 """
 from __future__ import annotations
@@ -332,6 +334,14 @@ def rms_norm(x, weight, eps):
     xf = x.float()
     y = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(BF16)
     return (y.float() * weight.float()).to(BF16)
+
+
+def add_rms_norm(x, residual, weight, eps):
+    """RMSNorm.add_rms_forward (layernorm.py:29-37): s = x + residual in fp32, residual_out =
+    bf16(s), y = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * weight). Returns (y, residual_out)."""
+    sf = x.float() + residual.float()
+    y = (sf * torch.rsqrt(sf.pow(2).mean(-1, keepdim=True) + eps)).to(BF16)
+    return (y.float() * weight.float()).to(BF16), sf.to(BF16)
 
 
 def salient_kv_project(hidden, idx, w_kv, bias, positions, cos, sin, num_kv_heads, k_norm_weight=None, eps=1e-6):

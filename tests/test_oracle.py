@@ -316,3 +316,20 @@ def test_salient_kv_project_per_row_loop():
             c, s_ = cos[p], sin[p]
             want = torch.cat((xn[:64] * c - xn[64:] * s_, xn[64:] * c + xn[:64] * s_)).to(BF).float()
             assert (k[j, h].float() - want).abs().max() <= 0.05
+
+
+def test_add_rms_norm_consistency_and_loop():
+    """Fused residual form: a zero residual reduces to rms_norm; residual_out is the bf16 sum; y
+    is normalised from the fp32 sum (not from the rounded residual), checked per row."""
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(6, 256, generator=g).to(BF)
+    r = (2 * torch.randn(6, 256, generator=g)).to(BF)
+    w = (1 + 0.1 * torch.randn(256, generator=g)).to(BF)
+    y0, r0 = ref.add_rms_norm(x, torch.zeros_like(x), w, 1e-6)
+    assert torch.equal(y0, ref.rms_norm(x, w, 1e-6)) and torch.equal(r0, x)
+    y, ro = ref.add_rms_norm(x, r, w, 1e-6)
+    for i in range(6):
+        s = x[i].double() + r[i].double()
+        assert torch.equal(ro[i], s.float().to(BF))
+        n = (s / torch.sqrt((s * s).mean() + 1e-6)).float().to(BF).double() * w.double()
+        assert (y[i].double() - n).abs().max() <= 2 ** -7 * n.abs().max()
