@@ -51,6 +51,7 @@ SIGNATURES = {
     "dyllm_ffn_down_workspace_bytes": [_L, _L, _I, _I],
     "dyllm_linear_workspace_bytes": [_L, _L, _I, _I],
     "dyllm_linear": [_P, _L, _P, _L, _P, _L, _P, _I, _I, _P, _P, _P, c_size_t, _P],
+    "dyllm_rope": [_P, _L, _L, _I, _I, _P, _P, _P, _I, _P, c_float, _P],
     "dyllm_kv_rope_scatter": [_P, _L, _L, _P, _P, _P, _P, _P, _I, _I, _I, _P, c_float, _P, _P, _P, _P, _P, _I, _P,
                               _P],
     "dyllm_rms_norm": [_P, _L, _P, _L, _P, _L, _I, c_float, _P, _L, _P, _L, _P],

@@ -368,7 +368,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
             nw[3] = __uint_as_float(st.y & 0xffff0000u);
           } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) nw[j] = __fadd_rn(old[j], __fmul_rn(o_acc[dt][4 * g + j], inv));
+            for (int j = 0; j < 4; ++j) nw[j] = add_mul_rn(old[j], o_acc[dt][4 * g + j], inv);
             st.x = pack_bf16x2(nw[0], nw[1]);
             st.y = pack_bf16x2(nw[2], nw[3]);
           }

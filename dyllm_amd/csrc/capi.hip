@@ -567,6 +567,34 @@ int dyllm_ffn_down(const void* h, int64_t rows, const int32_t* rows_dev, int64_t
                     DYLLM_STREAM(stream));
 }
 
+int dyllm_rope(void* x, int64_t ld_x, int64_t rows, int num_heads, int head_dim, const int64_t* positions,
+               const float* cos_table, const float* sin_table, int max_position, const void* norm_weight, float eps,
+               void* stream) {
+  DYLLM_REQUIRE(head_dim == 128, "supported head dimension is 128");
+  DYLLM_REQUIRE(num_heads >= 1 && max_position >= 1, "num_heads and max_position must be positive");
+  if (rows <= 0) return 0;
+  DYLLM_NONNULL(x);
+  DYLLM_NONNULL(positions);
+  DYLLM_NONNULL(cos_table);
+  DYLLM_NONNULL(sin_table);
+  DYLLM_REQUIRE(ld_x >= int64_t(num_heads) * head_dim && ld_x % 8 == 0, "row stride must be >= heads * 128, a multiple of 8");
+  KvRopeArgs a{};
+  a.kv = static_cast<const uint16_t*>(x);
+  a.ld_kv = ld_x;
+  a.rows = rows;
+  a.kv_size = int64_t(num_heads) * head_dim;
+  a.Hkv = num_heads;
+  a.positions = positions;
+  a.cos = cos_table;
+  a.sin = sin_table;
+  a.max_position = max_position;
+  a.k_norm = static_cast<const uint16_t*>(norm_weight);
+  a.eps = eps;
+  a.k_cache = static_cast<uint16_t*>(x);
+  a.ld_cache = ld_x;
+  return launch_kv_rope_scatter(a, DYLLM_STREAM(stream));
+}
+
 int dyllm_kv_rope_scatter(const void* kv, int64_t ld_kv, int64_t rows, const int32_t* rows_dev, const int32_t* pos_idx,
                           const int64_t* positions, const float* cos_table, const float* sin_table,
                           int max_position, int num_kv_heads, int head_dim, const void* k_norm_weight, float eps,

@@ -19,6 +19,22 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
 
+// Products rounded before the sum, never fused into an FMA. HIP's __fmul_rn / __fadd_rn are
+// plain operators here and would be contracted by the default -ffp-contract; these helpers keep
+// the reference's separately rounded forms.
+__device__ __forceinline__ float add_mul_rn(float c, float a, float b) {  // c + a*b
+#pragma clang fp contract(off)
+  return c + a * b;
+}
+__device__ __forceinline__ float mul_sub_mul_rn(float a, float b, float c, float d) {  // a*b - c*d
+#pragma clang fp contract(off)
+  return a * b - c * d;
+}
+__device__ __forceinline__ float mul_add_mul_rn(float a, float b, float c, float d) {  // a*b + c*d
+#pragma clang fp contract(off)
+  return a * b + c * d;
+}
+
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
 
 // fp32 -> bf16 with the gfx950 hardware conversion (v_cvt_pk_bf16_f32, round to nearest

@@ -50,14 +50,14 @@ struct KvRopeArgs {
   int64_t max_position;
   const uint16_t* k_norm;        // optional [128] bf16
   float eps;
-  uint16_t* k_cache;             // rows of ld_cache elements
+  uint16_t* k_cache;             // rows of ld_cache elements (in-place mode: the output rows)
   int64_t ld_cache;
-  const int64_t* k_rows;         // [rows] packed K-space row of each salient row
+  const int64_t* k_rows;         // [rows] packed K-space row of each salient row; NULL: row j
   const int32_t* cu_k;           // [B+1]
   const int64_t* seq_starts;
   const int64_t* seq_ids;        // [B]
   int B;
-  uint16_t* v_out;               // [rows, kv_size]
+  uint16_t* v_out;               // [rows, kv_size]; NULL: no v part
 };
 int launch_kv_rope_scatter(const KvRopeArgs& a, hipStream_t s);
 int launch_scatter_dest_rows(const int64_t* row_idx, int64_t M, const int32_t* m_dev, const int32_t* cu,

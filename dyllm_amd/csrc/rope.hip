@@ -7,6 +7,8 @@
 //     y1 = x1 cos - x2 sin, y2 = x2 cos + x1 sin, rounded to bf16), written straight into the
 //     row's K-cache row (CacheManager.scatter_update, cache_kernels.cu:388-426);
 //   * v: copied out as the compact v_new the sparse attention step consumes.
+// Without a cache mapping (k_rows == NULL) the rotated rows go to row j of the output and there
+// is no v: the same pass serves the queries (q_norm + RoPE of all queried rows, in place).
 // This replaces the reference's zero-filled [T, kv] temporary, the rotary over all T rows and the
 // separate scatter with one pass over the n salient rows.
 //
@@ -43,9 +45,12 @@ __global__ __launch_bounds__(256) void kv_rope_scatter_kernel(KvRopeArgs a) {
   // row-uniform chain
   int64_t pos = a.positions[a.pos_idx ? int64_t(a.pos_idx[j]) : j];
   pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
-  const int64_t kk = a.k_rows[j];
-  const int b = find_segment(a.cu_k, a.B + 1, kk);
-  const int64_t dest = a.seq_starts[a.seq_ids[b]] + (kk - a.cu_k[b]);
+  int64_t dest = j;   // in-place mode (no cache mapping): row j of the output
+  if (a.k_rows) {
+    const int64_t kk = a.k_rows[j];
+    const int b = find_segment(a.cu_k, a.B + 1, kk);
+    dest = a.seq_starts[a.seq_ids[b]] + (kk - a.cu_k[b]);
+  }
   const uint16_t* krow = a.kv + j * a.ld_kv;
   uint16_t* crow = a.k_cache + dest * a.ld_cache;
 
@@ -81,14 +86,15 @@ __global__ __launch_bounds__(256) void kv_rope_scatter_kernel(KvRopeArgs a) {
     float y1[8], y2[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      // rounded products and sums in this order (no contraction): the eager fp32 formula
-      y1[i] = __fsub_rn(__fmul_rn(x1[i], c[i]), __fmul_rn(x2[i], s[i]));
-      y2[i] = __fadd_rn(__fmul_rn(x2[i], c[i]), __fmul_rn(x1[i], s[i]));
+      // rounded products, then the sum (no contraction): the eager fp32 formula
+      y1[i] = mul_sub_mul_rn(x1[i], c[i], x2[i], s[i]);
+      y2[i] = mul_add_mul_rn(x2[i], c[i], x1[i], s[i]);
     }
     *reinterpret_cast<uint4*>(crow + h * D + d0) = pack8(y1);
     *reinterpret_cast<uint4*>(crow + h * D + d0 + HALF) = pack8(y2);
   }
   // v: kv_size values -> v_out row j (16 bytes per thread per pass)
+  if (!a.v_out) return;
   const uint4* vr = reinterpret_cast<const uint4*>(krow + a.kv_size);
   uint4* vo = reinterpret_cast<uint4*>(a.v_out + j * a.kv_size);
   for (int64_t i = t; i < a.kv_size / 8; i += 256) vo[i] = vr[i];

@@ -55,7 +55,8 @@ class RMSNorm(nn.Module):
 
 
 class RotaryEmbedding(nn.Module):
-    """Neox-style rotary embedding (rotary_embedding.py:8-54)."""
+    """Neox-style rotary embedding tables (rotary_embedding.py:19-38): fp32 cos / sin
+    [max_position, head_dim / 2]; the rotation itself runs in dyllm_rope / dyllm_kv_rope_scatter."""
 
     def __init__(self, head_dim, max_position, base, device="cuda"):
         super().__init__()
@@ -65,11 +66,6 @@ class RotaryEmbedding(nn.Module):
         self.register_buffer("cos", f.cos(), persistent=False)
         self.register_buffer("sin", f.sin(), persistent=False)
 
-    def rotate(self, positions, x):
-        pos = positions.clamp(0, self.cos.shape[0] - 1)
-        c, s = self.cos[pos].unsqueeze(1), self.sin[pos].unsqueeze(1)
-        x1, x2 = x.float().chunk(2, dim=-1)
-        return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
 
 
 class LLaDAMLP(nn.Module):
@@ -140,17 +136,18 @@ class LLaDAAttention(nn.Module):
     def forward(self, positions, hidden):
         ctx = get_context()
         md = get_metadata()
-        q = F.linear(hidden, self.q_proj, self.q_bias).view(-1, self.num_heads, self.head_dim)
-        if self.q_norm is not None:
-            q = self.q_norm(q)
-        q = self.rotary.rotate(positions, q)
+        # q_norm + RoPE of every queried row in place, one native pass (dyllm_rope)
+        q = F.linear(hidden, self.q_proj, self.q_bias)
+        qn, kn = self.q_norm, self.k_norm
+        ops.rope_(q, self.num_heads, positions, self.rotary.cos, self.rotary.sin,
+                  None if qn is None else qn.weight, 1e-6 if qn is None else qn.eps)
+        q = q.view(-1, self.num_heads, self.head_dim)
         if ctx.is_full:
             kv = F.linear(hidden, self.kv_proj, self.kv_bias)
             k, v = kv.split([self.kv_size, self.kv_size], dim=-1)
+            ops.rope_(k, self.num_kv_heads, positions, self.rotary.cos, self.rotary.sin,
+                      None if kn is None else kn.weight, 1e-6 if kn is None else kn.eps)
             k = k.reshape(-1, self.num_kv_heads, self.head_dim)
-            if self.k_norm is not None:
-                k = self.k_norm(k)
-            k = self.rotary.rotate(positions, k)
             v = v.reshape(-1, self.num_kv_heads, self.head_dim)
             self.k_cache.reset_full(k.flatten(1), md.running_seqs_tensor, seq_ids_list=md.running_seqs)
             o = self.attn(q, k, v)
@@ -160,7 +157,6 @@ class LLaDAAttention(nn.Module):
             idx = ctx.idx_salient_row_i32
             kv = ops.linear(hidden, self.kv_proj, self.kv_bias, rows_idx=idx)
             kidx = ctx.idx_salient_row_k if ctx.idx_salient_row_k is not None else ctx.idx_salient_row
-            kn = self.k_norm
             v = self.k_cache.scatter_kv_rope(md.running_seqs_tensor, kidx, kv, self.num_kv_heads, positions,
                                              self.rotary.cos, self.rotary.sin, idx,
                                              None if kn is None else kn.weight, 1e-6 if kn is None else kn.eps)

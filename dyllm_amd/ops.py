@@ -487,6 +487,32 @@ def linear(x, w, bias=None, rows_idx=None, count=None, hint=0):
     return out
 
 
+def rope_(x, num_heads, positions, cos, sin, norm_weight=None, eps=1e-6):
+    """In-place neox RoPE of x [rows, num_heads * 128] at positions[row] (rotary_embedding.py:8-16,
+    47-54), after an optional per-head RMSNorm with norm_weight (q_norm, layernorm.py:15-24)
+    (dyllm_rope). x may be a row-strided view (the k half of a [k | v] projection). Returns x."""
+    if x is None or not x.is_cuda or x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise RuntimeError("x must be a bf16 2D GPU tensor")
+    _check(positions, "positions", None, 1)
+    positions = _i64(positions)
+    for t, n in ((cos, "cos"), (sin, "sin")):
+        _check(t, n, torch.float32, 2)
+        if t.shape[1] != 64 or not t.is_contiguous():
+            raise RuntimeError(f"{n} must be a contiguous [max_position, 64] fp32 table")
+    if x.shape[1] != num_heads * 128 or x.stride(1) != 1:
+        raise RuntimeError("x must be [rows, num_heads * 128] with contiguous rows")
+    if positions.numel() < x.shape[0]:
+        raise RuntimeError("positions must have one entry per row")
+    if norm_weight is not None:
+        _check(norm_weight, "norm_weight", torch.bfloat16, 1)
+        if norm_weight.numel() != 128:
+            raise RuntimeError("norm_weight must have head_dim (128) entries")
+    if x.shape[0]:
+        _lib.call("dyllm_rope", _ptr(x), x.stride(0), x.shape[0], num_heads, 128, _ptr(positions), _ptr(cos),
+                  _ptr(sin), cos.shape[0], _ptr(norm_weight), float(eps), _stream())
+    return x
+
+
 def kv_rope_scatter(kv, num_kv_heads, positions, cos, sin, k_cache, k_rows, cu_seqlens_k, seq_starts, seq_ids,
                     pos_idx=None, k_norm_weight=None, eps=1e-6, count=None):
     """K/V epilogue of the salient-row projection (dyllm_kv_rope_scatter): for each row j of

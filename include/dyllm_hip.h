@@ -234,6 +234,12 @@ int dyllm_linear(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t r
  * K-cache row of packed K-space row k_rows[j] (the addressing of dyllm_scatter_update,
  * llada.py:136-143). v: copied to v_out [rows, num_kv_heads * 128]. Replaces the zero-filled
  * k_temp, the rotary over all rows and the scatter of llada.py:108-143. */
+/* The same epilogue in place for the queries: rows j < rows of x ([rows, num_heads * 128], row
+ * stride ld_x): optional per-head RMSNorm (q_norm, lladamoe.py:194-195), then RoPE at
+ * positions[j] (rotary_embedding.py:47-54), written back to x. */
+int dyllm_rope(void* x, int64_t ld_x, int64_t rows, int num_heads, int head_dim, const int64_t* positions,
+               const float* cos_table, const float* sin_table, int max_position, const void* norm_weight, float eps,
+               void* stream);
 int dyllm_kv_rope_scatter(const void* kv, int64_t ld_kv, int64_t rows, const int32_t* rows_dev, const int32_t* pos_idx,
                           const int64_t* positions, const float* cos_table, const float* sin_table,
                           int max_position, int num_kv_heads, int head_dim, const void* k_norm_weight, float eps,

@@ -181,3 +181,27 @@ def test_salient_kv_projection_end_to_end(dev):
         k_want, v_want = ref.salient_kv_project(hidden, c["idx_q"], w, b, positions, cos, sin, hkv, knw, 1e-6)
         assert_bf16_close(v.cpu(), v_want, what=f"v (hkv={hkv})")
         assert_bf16_close(k_cache.cpu()[_dest_rows(c)].view(-1, hkv, 128), k_want, what=f"k (hkv={hkv})")
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_rope_in_place_matches_oracle(dev, norm):
+    """dyllm_rope on the queries: every row rotated in place at its own position (with q_norm
+    first when given); bit-exact without the norm."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(21)
+    rows, H = 333, 12
+    x = (torch.randn(rows, H * 128, generator=g) * 1.5).to(BF)
+    pos = torch.randint(0, 5000, (rows,), generator=g)
+    cos, sin = ref.rope_tables(128, 4096, 10000.0)
+    w = (1 + 0.1 * torch.randn(128, generator=g)).to(BF) if norm else None
+    xd = x.to(dev)
+    ops.rope_(xd, H, pos.to(dev), cos.to(dev), sin.to(dev), None if w is None else w.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    xin = x.view(rows, H, 128)
+    if w is not None:
+        xin = ref.rms_norm(xin, w, 1e-6)
+    want = ref.rope_neox(xin, cos, sin, pos).view(rows, H * 128)
+    if w is None:
+        assert torch.equal(xd.cpu(), want)
+    else:
+        assert_bf16_close(xd.cpu(), want, what="q_norm + rope")
