@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 BF = torch.bfloat16
 
 
-def _setup(dev, q_pruned, H=4, Hkv=2, lens=((48, 80), (16, 200), (64, 64)), seed=0, tau=None):
+def _setup(dev, q_pruned, H=4, Hkv=2, lens=((48, 80), (16, 200), (64, 64)), seed=0, tau=None, sal_counts=None):
     from dyllm_amd.engine.cache_manager import CacheManager
     from dyllm_amd.model_executor.layers.attention import Attention
     from dyllm_amd.utils.context import set_context
@@ -45,11 +45,12 @@ def _setup(dev, q_pruned, H=4, Hkv=2, lens=((48, 80), (16, 200), (64, 64)), seed
     # salient rows of this step (response rows), new V/K rows
     idx_q, idx_k, cu_s = [], [], [0]
     for b, (p, r) in enumerate(lens):
-        sel = np.sort(rng.choice(r, size=max(1, r // 6), replace=False))
+        n_b = max(1, r // 6) if sal_counts is None else sal_counts[b]
+        sel = np.sort(rng.choice(r, size=n_b, replace=False))
         idx_k += (cu_k[b] + p + sel).tolist()
         idx_q += ((cu_q[b] + sel) if q_pruned else (cu_q[b] + p + sel)).tolist()
         cu_s.append(len(idx_q))
-    idx_k = np.asarray(idx_k)
+    idx_k = np.asarray(idx_k, dtype=np.int64)
     v_new = (v_all[idx_k].float() + 0.5 * torch.randn(len(idx_k), Hkv, D, generator=g)).to(BF)
     k_new = k_all.clone()
     k_new[idx_k] = (k_all[idx_k].float() + 0.5 * torch.randn(len(idx_k), Hkv, D, generator=g)).to(BF)
@@ -57,15 +58,19 @@ def _setup(dev, q_pruned, H=4, Hkv=2, lens=((48, 80), (16, 200), (64, 64)), seed
         else np.arange(Tk)
     q = q_all[resp]
     return dict(attn=attn, q=q, k_new=k_new, v_new=v_new, v_old=v_all, o_full=o_full.cpu(), cu_q=cu_q, cu_k=cu_k,
-                cu_p=cu_p, cu_s=np.asarray(cu_s), idx_q=np.asarray(idx_q), idx_k=idx_k, resp=resp, Tq=Tq, Tk=Tk,
+                cu_p=cu_p, cu_s=np.asarray(cu_s), idx_q=np.asarray(idx_q, dtype=np.int64), idx_k=idx_k, resp=resp, Tq=Tq, Tk=Tk,
                 t=t, md=md, H=H, Hkv=Hkv, Lq=Lq, Lk=Lk)
 
 
-@pytest.mark.parametrize("q_pruned", [True, False])
-def test_attention_forward_sparse_step(dev, q_pruned):
+@pytest.mark.parametrize("q_pruned,sal_counts", [(True, None), (False, None), (True, [0, 7, 64]), (False, [0, 0, 0]),
+                                                  (True, [80, 200, 64]), (True, [1, 0, 1])])
+def test_attention_forward_sparse_step(dev, q_pruned, sal_counts):
+    """Sparse step at layer level; the salient sets include a sequence with no salient row, no
+    salient row at all, every response row salient, and single rows."""
     from dyllm_amd.utils.context import set_context
 
-    s = _setup(dev, q_pruned)
+    print(f"[layer] q_pruned={q_pruned} sal_counts={sal_counts}", flush=True)
+    s = _setup(dev, q_pruned, sal_counts=sal_counts)
     t, md = s["t"], s["md"]
     # oracle inputs: packed caches as the reference's get_seqs / get_seqs_block return them
     c_old = s["o_full"][torch.from_numpy(s["resp"])] if q_pruned else s["o_full"]
