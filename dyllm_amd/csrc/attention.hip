@@ -132,6 +132,30 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     const int key0 = kb * kBK;
     const uint64_t bm = meta_bm;
     mask_next = bm;
+    if (MODE != AttnMode::ColSparse && key0 + kBK <= Lk) {
+      // dense V and a full block (block-uniform branch): no per-row guards or zero fills
+      // (dense -4 %, row-sparse -10 %; the column-sparse tiles keep one path, which measured
+      // faster there)
+#pragma unroll
+      for (int it = 0; it < KCH; ++it) {
+        const int c = tid + NT * it;
+        const int key = c >> 4, dc = c & 15;
+        kreg[it] = *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8);
+      }
+      if (bm != 0) {
+#pragma unroll
+        for (int it = 0; it < VIT; ++it) {
+          const int c = tid + NT * it;
+          const int dc = c >> 4;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int64_t r = key0 + 4 * ((tid + NT * it) & 15) + j;
+            vreg[it][j] = *reinterpret_cast<const uint4*>(Vb + r * ldkv + dc * 8);
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int it = 0; it < KCH; ++it) {
       const int c = tid + NT * it;
