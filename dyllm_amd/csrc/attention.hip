@@ -469,6 +469,19 @@ __global__ __launch_bounds__(256) void colsparse_scatter_kernel(const int32_t* _
   atomicOr(&kmask[int64_t(b) * nblk + off / kBK], 1ull << (off % kBK));
 }
 
+// bf16 x 8 difference new - old, each element rounded once (the dV of attention.py:67-74)
+__device__ __forceinline__ uint4 bf16x8_sub(uint4 nw, uint4 o) {
+  const uint32_t ov[4] = {o.x, o.y, o.z, o.w}, nv[4] = {nw.x, nw.y, nw.z, nw.w};
+  uint32_t d[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = __fsub_rn(__uint_as_float(nv[e] << 16), __uint_as_float(ov[e] << 16));
+    const float hi = __fsub_rn(__uint_as_float(nv[e] & 0xffff0000u), __uint_as_float(ov[e] & 0xffff0000u));
+    d[e] = pack_bf16x2(lo, hi);
+  }
+  return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
 // dV = bf16(v_new - v_cache[row]) then v_cache[row] = v_new (attention.py:67-74, 89-96),
 // one wavefront per salient row, 16-byte lanes.
 __global__ __launch_bounds__(256) void v_delta_update_kernel(uint16_t* __restrict__ v_cache,
@@ -483,15 +496,7 @@ __global__ __launch_bounds__(256) void v_delta_update_kernel(uint16_t* __restric
   uint4* dr = reinterpret_cast<uint4*>(dv + j * row_elems);
   for (int64_t i = lane; i < row_elems / 8; i += 64) {
     const uint4 o = cr[i], nw = nr[i];
-    const uint32_t ov[4] = {o.x, o.y, o.z, o.w}, nv[4] = {nw.x, nw.y, nw.z, nw.w};
-    uint32_t d[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = __fsub_rn(__uint_as_float(nv[e] << 16), __uint_as_float(ov[e] << 16));
-      const float hi = __fsub_rn(__uint_as_float(nv[e] & 0xffff0000u), __uint_as_float(ov[e] & 0xffff0000u));
-      d[e] = pack_bf16x2(lo, hi);
-    }
-    dr[i] = make_uint4(d[0], d[1], d[2], d[3]);
+    dr[i] = bf16x8_sub(nw, o);
     cr[i] = nw;
   }
 }
@@ -547,8 +552,12 @@ int launch_step_prep(const StepPrepArgs& a, hipStream_t s) {
   return check_launch("step_prep_kernel");
 }
 
-// one wavefront per salient row j: its V-cache row, dV and V-cache update (16-byte lanes), and
-// lane 0 records the row in the slot maps and the salient-key bit of its 64-key block
+// dV = bf16(v_new - v_cache[row]), v_cache[row] = v_new for salient row j, spread over kSalQ
+// wavefronts per row (each a contiguous quarter of the row, all of its loads issued before its
+// stores: enough bytes in flight for a few hundred rows); lane 0 of the row's first wavefront
+// records the row in the slot maps and the salient-key bit of its 64-key block.
+constexpr int kSalQ = 4;
+
 __global__ __launch_bounds__(256) void step_salient_kernel(uint16_t* __restrict__ v_cache,
                                                            const uint16_t* __restrict__ v_new,
                                                            uint16_t* __restrict__ dv, int64_t row_elems,
@@ -560,7 +569,8 @@ __global__ __launch_bounds__(256) void step_salient_kernel(uint16_t* __restrict_
                                                            int32_t* __restrict__ slot,
                                                            unsigned long long* __restrict__ kmask,
                                                            int32_t* __restrict__ kslot) {
-  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int j = wid / kSalQ, q = wid % kSalQ;
   const int lane = threadIdx.x & 63;
   if (j >= n) return;
   const int64_t k = idx_k64[j];
@@ -568,23 +578,25 @@ __global__ __launch_bounds__(256) void step_salient_kernel(uint16_t* __restrict_
   const int b = bq < B ? bq : B - 1;
   const int64_t off = k - cu_k[b];
   const int64_t dest = v_seq_starts[seq_ids[b]] + off;
+  const int64_t n16 = row_elems / 8, per = (n16 + kSalQ - 1) / kSalQ;
+  const int64_t beg = q * per, end = beg + per < n16 ? beg + per : n16;
   uint4* cr = reinterpret_cast<uint4*>(v_cache + dest * row_elems);
   const uint4* nr = reinterpret_cast<const uint4*>(v_new + int64_t(j) * row_elems);
   uint4* dr = reinterpret_cast<uint4*>(dv + int64_t(j) * row_elems);
-  for (int64_t i = lane; i < row_elems / 8; i += 64) {
+  int64_t i = beg + lane;
+  for (; i + 64 < end; i += 128) {
+    const uint4 o0 = cr[i], n0 = nr[i], o1 = cr[i + 64], n1 = nr[i + 64];
+    dr[i] = bf16x8_sub(n0, o0);
+    dr[i + 64] = bf16x8_sub(n1, o1);
+    cr[i] = n0;
+    cr[i + 64] = n1;
+  }
+  for (; i < end; i += 64) {
     const uint4 o = cr[i], nw = nr[i];
-    const uint32_t ov[4] = {o.x, o.y, o.z, o.w}, nv[4] = {nw.x, nw.y, nw.z, nw.w};
-    uint32_t d[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = __fsub_rn(__uint_as_float(nv[e] << 16), __uint_as_float(ov[e] << 16));
-      const float hi = __fsub_rn(__uint_as_float(nv[e] & 0xffff0000u), __uint_as_float(ov[e] & 0xffff0000u));
-      d[e] = pack_bf16x2(lo, hi);
-    }
-    dr[i] = make_uint4(d[0], d[1], d[2], d[3]);
+    dr[i] = bf16x8_sub(nw, o);
     cr[i] = nw;
   }
-  if (lane == 0) {
+  if (q == 0 && lane == 0) {
     slot[idx_q32[j]] = j;
     kslot[k] = j;
     if (bq < B && off < cu_k[b + 1] - cu_k[b]) atomicOr(&kmask[int64_t(b) * nblk + off / kBK], 1ull << (off % kBK));
@@ -597,9 +609,9 @@ int launch_step_salient(uint16_t* v_cache, const uint16_t* v_new, uint16_t* dv, 
                         int32_t* kslot, hipStream_t s) {
   DYLLM_REQUIRE(row_elems % 8 == 0, "V row width must be a multiple of 8");
   if (n <= 0) return 0;
-  step_salient_kernel<<<unsigned(cdiv(n, 4)), 256, 0, s>>>(v_cache, v_new, dv, row_elems, idx_k64, idx_q32, n, cu_k,
-                                                            B, nblk, v_seq_starts, seq_ids, slot,
-                                                            reinterpret_cast<unsigned long long*>(kmask), kslot);
+  step_salient_kernel<<<unsigned(cdiv(int64_t(n) * kSalQ, 4)), 256, 0, s>>>(
+      v_cache, v_new, dv, row_elems, idx_k64, idx_q32, n, cu_k, B, nblk, v_seq_starts, seq_ids, slot,
+      reinterpret_cast<unsigned long long*>(kmask), kslot);
   return check_launch("step_salient_kernel");
 }
 
