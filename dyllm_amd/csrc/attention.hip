@@ -623,8 +623,17 @@ static void launch_mode(const AttnArgs& a, int max_rows_per_seq, hipStream_t s) 
   attention_kernel<MODE, NW><<<unsigned(nwg), NW * 64, 0, s>>>(g);
 }
 
+// Q, K, V and the context rows are moved with 16-byte loads / 8-byte stores
+static bool attn_aligned(const AttnArgs& a) {
+  const uintptr_t m = reinterpret_cast<uintptr_t>(a.Q) | reinterpret_cast<uintptr_t>(a.K) |
+                      reinterpret_cast<uintptr_t>(a.V) | reinterpret_cast<uintptr_t>(a.C) |
+                      reinterpret_cast<uintptr_t>(a.o_sal);
+  return (m % 16) == 0 && reinterpret_cast<uintptr_t>(a.O) % 8 == 0;
+}
+
 int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s) {
   DYLLM_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.H % a.Hkv == 0, "bad head counts");
+  DYLLM_REQUIRE(attn_aligned(a), "Q, K, V and context buffers must be 16-byte aligned (output 8-byte)");
   DYLLM_REQUIRE(max_rows_per_seq >= 0, "bad row bound");
   if (max_rows_per_seq == 0) return 0;
   DYLLM_REQUIRE(cdiv(max_rows_per_seq, 64) * a.H * a.B < (int64_t(1) << 31), "grid too large");
@@ -650,6 +659,7 @@ int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hip
 int launch_attention_step(const AttnArgs& rs0, int max_rows_rs, const AttnArgs& cs0, int max_rows_cs,
                           hipStream_t s) {
   DYLLM_REQUIRE(cs0.B >= 1 && cs0.H >= 1 && cs0.Hkv >= 1 && cs0.H % cs0.Hkv == 0, "bad head counts");
+  DYLLM_REQUIRE(attn_aligned(rs0) && attn_aligned(cs0), "Q, K, V and context buffers must be 16-byte aligned (output 8-byte)");
   AttnArgs rs = rs0, cs = cs0;
   rs.tiles_per_seq = int(cdiv(max_rows_rs > 0 ? max_rows_rs : 1, 128));
   cs.tiles_per_seq = int(cdiv(max_rows_cs, 128));

@@ -3,6 +3,8 @@
 #include "../../include/dyllm_hip.h"
 #include "kernels.h"
 
+#include <cstdint>
+#include <initializer_list>
 #include <string>
 
 namespace dyllm {
@@ -21,6 +23,12 @@ int check_launch(const char* what) {
 }
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+// true when every non-null pointer is a multiple of `bytes` (vector loads / stores of that width)
+static inline bool aligned_to(size_t bytes, std::initializer_list<const void*> ptrs) {
+  for (const void* p : ptrs)
+    if (p && reinterpret_cast<uintptr_t>(p) % bytes != 0) return false;
+  return true;
+}
 static const float kLog2e = 1.4426950408889634f;
 constexpr int kMoeBlock = 128;
 
@@ -578,6 +586,8 @@ int dyllm_rope(void* x, int64_t ld_x, int64_t rows, int num_heads, int head_dim,
   DYLLM_NONNULL(cos_table);
   DYLLM_NONNULL(sin_table);
   DYLLM_REQUIRE(ld_x >= int64_t(num_heads) * head_dim && ld_x % 8 == 0, "row stride must be >= heads * 128, a multiple of 8");
+  DYLLM_REQUIRE(aligned_to(16, {x, cos_table, sin_table, norm_weight}),
+                "x, the cos / sin tables and norm_weight must be 16-byte aligned");
   KvRopeArgs a{};
   a.kv = static_cast<const uint16_t*>(x);
   a.ld_kv = ld_x;
@@ -617,6 +627,8 @@ int dyllm_kv_rope_scatter(const void* kv, int64_t ld_kv, int64_t rows, const int
   DYLLM_NONNULL(v_out);
   const int64_t kv_size = int64_t(num_kv_heads) * head_dim;
   DYLLM_REQUIRE(ld_kv >= 2 * kv_size && ld_kv % 8 == 0, "kv row stride must be >= 2 * kv_size and a multiple of 8");
+  DYLLM_REQUIRE(aligned_to(16, {kv, cos_table, sin_table, k_norm_weight, k_cache, v_out}),
+                "kv, the cos / sin tables, k_norm_weight, k_cache and v_out must be 16-byte aligned");
   KvRopeArgs a{};
   a.kv = static_cast<const uint16_t*>(kv);
   a.ld_kv = ld_kv;
@@ -651,6 +663,7 @@ int dyllm_rms_norm(const void* x, int64_t ld_x, const void* residual, int64_t ld
   DYLLM_NONNULL(weight);
   DYLLM_NONNULL(out);
   DYLLM_REQUIRE(residual == nullptr || residual_out != nullptr, "residual_out must be given with a residual");
+  DYLLM_REQUIRE(aligned_to(16, {x, residual, weight, out, residual_out}), "all row buffers and the weight must be 16-byte aligned");
   DYLLM_REQUIRE(ld_x >= hidden && ld_x % 8 == 0 && ld_out >= hidden && ld_out % 8 == 0,
                 "row strides must be >= hidden and multiples of 8");
   DYLLM_REQUIRE(residual == nullptr || (ld_residual >= hidden && ld_residual % 8 == 0 && ld_residual_out >= hidden &&
@@ -685,6 +698,7 @@ int dyllm_linear(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t r
   DYLLM_REQUIRE(in_features > 0 && in_features % 64 == 0, "in_features must be a positive multiple of 64");
   DYLLM_REQUIRE(out_features > 0 && out_features % 8 == 0, "out_features must be a positive multiple of 8");
   DYLLM_REQUIRE(ld_x >= in_features && ld_x % 8 == 0, "x row stride must be >= in_features and a multiple of 8");
+  DYLLM_REQUIRE(aligned_to(16, {x, w}) && aligned_to(8, {bias, out}), "x and w must be 16-byte aligned, bias and out 8-byte aligned");
   if (rows <= 0) return 0;
   return store_gemm(x, ld_x, rows_idx, rows, rows_dev, rows_hint, w, out_features, in_features, bias, out,
                     out_features, nullptr, workspace, workspace_bytes, "dyllm_linear_workspace_bytes",

@@ -433,6 +433,9 @@ int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, int
   DYLLM_REQUIRE(g.K > 0 && g.K % kGemmBK == 0, "GEMM K must be a positive multiple of 64");
   DYLLM_REQUIRE(g.N > 0 && g.N % 8 == 0, "GEMM N must be a positive multiple of 8");
   DYLLM_REQUIRE(g.lda % 8 == 0 && g.ldw % 8 == 0 && g.ldc % 4 == 0, "GEMM leading dimensions must keep 16-byte rows");
+  DYLLM_REQUIRE(reinterpret_cast<uintptr_t>(g.A) % 16 == 0 && reinterpret_cast<uintptr_t>(g.W) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(g.Cout) % 8 == 0 && reinterpret_cast<uintptr_t>(g.bias) % 8 == 0,
+                "GEMM operands must be 16-byte aligned (output and bias 8-byte)");
   if (m_bound <= 0) return 0;
   if (tile_m == 0) tile_m = gemm_plan(m_bound, g.N, g.K, epi).tile_m;
   DYLLM_REQUIRE(tile_m == 128 || tile_m == 192 || tile_m == 256, "tile height must be 128, 192 or 256");

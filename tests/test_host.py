@@ -73,6 +73,14 @@ def test_error_path_reports_message_without_gpu():
         _lib.call("dyllm_ffn_gate_up", 1, 100, None, 10, None, 0, 1, 100, 128, 1, None)
     with pytest.raises(RuntimeError, match="must not be NULL"):
         _lib.call("dyllm_get_seqs", 1, 1, 16, None, 1, 1, 1, 4, None)
+    # misaligned buffers are refused before any launch (the kernels use 16-byte accesses)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        _lib.call("dyllm_rms_norm", 2, 4096, None, 0, 16, 10, 4096, 1e-6, 32, 4096, None, 0, None)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        _lib.call("dyllm_linear", 8, 4096, None, 10, None, 0, 16, 8192, 4096, None, 32, None, 0, None)
+    with pytest.raises(RuntimeError, match="16-byte aligned"):
+        _lib.call("dyllm_kv_rope_scatter", 4, 8192, 10, None, None, 16, 16, 16, 4096, 32, 128, None, 1e-6, 16, 16,
+                  16, 16, 16, 1, 16, None)
     lib = _lib.load()
     assert lib.dyllm_swiglu_ffn_workspace_bytes(920, 12288) >= 920 * 12288 * 2
     assert lib.dyllm_attention_sparse_workspace_bytes(8, 32, 6144, 1024) >= 6144 * 4 + 32 * 3 * 6144 * 4
