@@ -18,7 +18,9 @@ pre-generated per layer). The caches are restored between steps (untimed) so eve
 step sees the same salient fraction.
 
 value = B * Lq / step time (tokens/s). The roofline object is for the dominant kernel, the
-gathered gate_up SwiGLU GEMM, timed with HIP events on its own launches. The salient-row K/V
+fused attention kernel of the step (timed with library-owned HIP events around that launch,
+dyllm_attention_timer); roofline_gate_up is the gathered gate_up SwiGLU GEMM, timed with HIP
+events on its own launches. The salient-row K/V
 projection GEMM (the step before the path, outside `value`) is timed on its own after the
 steps and reported as `kv_projection`.
 """
@@ -42,12 +44,14 @@ PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the gate_up GEMM at this workload, from rocprofv3 FETCH_SIZE / WRITE_SIZE
 # calibrated against a 256 MiB copy (profiles/pmc_gemm_gate_up_config1.md).
 GATE_UP_TRAFFIC_BYTES = 364.0e6
+# HBM bytes per launch of the fused attention kernel, same method (profiles/pmc_attention_step_config1.md)
+ATTN_TRAFFIC_BYTES = 424.0e6
 
 
 def build_workload(cfg, layers, device, seed=0):
     import torch
 
-    from dyllm_amd import ops
+    from dyllm_amd import _lib, ops
     from dyllm_amd.engine.cache_manager import CacheManager
     from dyllm_amd.model_executor.layers.attention import Attention
     from dyllm_amd.model_executor.models.llada import LLaDAMLP
@@ -147,8 +151,12 @@ def build_workload(cfg, layers, device, seed=0):
             v_sal = st["k_cache"].scatter_kv_rope(md.running_seqs_tensor, ctx.idx_salient_row_k, kv, Hkv, pos0,
                                                   rope_cos, rope_sin, ctx.idx_salient_row_i32)
             k_full = st["k_cache"].get_seqs(md.running_seqs_tensor, md.running_seqs).view(-1, Hkv, D)
-            o = st["attn"](st["q"], k_full, v_sal)
             ev = events.get(li) if events is not None else None
+            if ev is not None:   # time the fused attention kernel of this layer's step call
+                _lib.load().dyllm_attention_timer(1)
+            o = st["attn"](st["q"], k_full, v_sal)
+            if ev is not None:
+                _lib.load().dyllm_attention_timer(0)
             st["mlp"].forward_salient(o.view(Tq, H * D), gate_up_events=ev)
         return ctx
 
@@ -402,17 +410,31 @@ def main():
         gate_ms += [a.elapsed_time(b) for a, b in evs.values()]
         n_sals += n_sal
     ms_per_step = total_ms / args.steps
+    import ctypes
+
+    from dyllm_amd import _lib
+    attn_ms, attn_n = ctypes.c_float(), ctypes.c_int()
+    _lib.call("dyllm_attention_timer_read", ctypes.addressof(attn_ms), ctypes.addressof(attn_n))
+    avg_attn_ms = attn_ms.value / max(attn_n.value, 1)
     Tq = wl["Tq"]
     value = Tq / (ms_per_step / 1e3)
 
     hid, inter = cfg["hidden"], cfg["inter"]
     avg_n = sum(n_sals) / len(n_sals)
     flops = 2.0 * avg_n * hid * 2 * inter
+    # fused attention kernel, algorithmic work: row-sparse tiles 4 Lk H D per salient query row;
+    # column-sparse tiles QK^T 2 Lk H D per other row plus PV over its sequence's salient keys only
+    L = cfg["prompt"] + cfg["response"]
+    HD = cfg["heads"] * cfg["head_dim"]
+    attn_flops = (4.0 * L * HD * avg_n + 2.0 * L * HD * (Tq - avg_n)
+                  + 2.0 * (avg_n / cfg["batch"]) * HD * (Tq - avg_n))
+    attn_tf = attn_flops / (avg_attn_ms * 1e-3) / 1e12
     avg_gate_ms = sum(gate_ms) / len(gate_ms)
     from dyllm_amd import _lib
     gate_bm = _lib.load().dyllm_ffn_tile_rows(int(round(avg_n)), 2 * inter, hid, 1)
     achieved = flops / (avg_gate_ms * 1e-3) / 1e12
     print(f"[bench] {ms_per_step:.3f} ms/step, avg salient rows per layer {avg_n:.1f}, "
+          f"attention {avg_attn_ms * 1e3:.1f} us -> {attn_tf:.1f} TFLOP/s, "
           f"gate_up {avg_gate_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
     kv_proj = time_kv_projection(cfg, int(round(avg_n)))
@@ -444,7 +466,14 @@ def main():
                    "layers": layers, "batch": cfg["batch"], "seq_len": cfg["prompt"] + cfg["response"],
                    "response_len": cfg["response"], "hidden": hid, "heads": cfg["heads"], "ffn": inter,
                    "tau": cfg["tau"], "avg_salient_rows_per_layer": round(avg_n, 1)},
-        "roofline": {"kernel": f"gemm_kernel<{gate_bm},4,SwiGLU> (gathered gate_up + SiLU*up, tile {gate_bm}x256)",
+        "roofline": {"kernel": "attention_step_kernel<4> (fused step: row-sparse + column-sparse tiles)",
+                     "bound": "mfma", "achieved": round(attn_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(attn_tf / PEAK_BF16_TFLOPS, 4), "traffic": ATTN_TRAFFIC_BYTES,
+                     "traffic_unit": "bytes per launch (PMC)", "algorithmic_bytes": 345.0e6,
+                     "avg_launch_us": round(avg_attn_ms * 1e3, 2), "flop_per_launch": attn_flops,
+                     "note": "VALU/latency bound (softmax over all query-key pairs); frac counts algorithmic "
+                             "MFMA work only"},
+        "roofline_gate_up": {"kernel": f"gemm_kernel<{gate_bm},4,SwiGLU> (gathered gate_up + SiLU*up, tile {gate_bm}x256)",
                      "bound": "mfma",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,

@@ -19,6 +19,8 @@ _L = c_int64
 SIGNATURES = {
     "dyllm_last_error": [],
     "dyllm_abi_version": [],
+    "dyllm_attention_timer": [_I],
+    "dyllm_attention_timer_read": [_P, _P],
     "dyllm_attention_sparse_workspace_bytes": [_I, _I, _L, _I],
     "dyllm_attention_sparse_varlen": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _L, _I, _P, _P, _P,
                                       _P, _P, c_float, _P, c_size_t, _P],

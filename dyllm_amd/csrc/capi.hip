@@ -6,6 +6,8 @@
 #include <cstdint>
 #include <initializer_list>
 #include <string>
+#include <utility>
+#include <vector>
 
 namespace dyllm {
 
@@ -23,6 +25,16 @@ int check_launch(const char* what) {
 }
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Optional timing of the fused attention kernel of dyllm_sparse_attention_step (for the
+// benchmark's live roofline): while enabled, each call records a library-owned event pair around
+// that one launch on the caller's stream.
+struct AttnTimer {
+  bool enabled = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+  size_t used = 0;
+};
+static thread_local AttnTimer g_attn_timer;
 // true when every non-null pointer is a multiple of `bytes` (vector loads / stores of that width)
 static inline bool aligned_to(size_t bytes, std::initializer_list<const void*> ptrs) {
   for (const void* p : ptrs)
@@ -42,6 +54,29 @@ using namespace dyllm;
 extern "C" {
 
 const char* dyllm_last_error(void) { return g_last_error.c_str(); }
+
+int dyllm_attention_timer(int enable) {
+  g_attn_timer.enabled = enable != 0;
+  return 0;
+}
+
+int dyllm_attention_timer_read(float* total_ms, int* launches) {
+  DYLLM_NONNULL(total_ms);
+  DYLLM_NONNULL(launches);
+  AttnTimer& tm = g_attn_timer;
+  float sum = 0.f;
+  for (size_t i = 0; i < tm.used; ++i) {
+    float ms = 0.f;
+    if (hipEventSynchronize(tm.ev[i].second) != hipSuccess ||
+        hipEventElapsedTime(&ms, tm.ev[i].first, tm.ev[i].second) != hipSuccess)
+      return fail("attention timer: event query failed");
+    sum += ms;
+  }
+  *total_ms = sum;
+  *launches = int(tm.used);
+  tm.used = 0;
+  return 0;
+}
 int dyllm_abi_version(void) { return 1; }
 
 // ---------------------------------------------------------------------------------------
@@ -149,7 +184,21 @@ static int colsparse_impl(const void* q, const void* k, const int64_t* kv_start,
   if (fused_rs) {
     // salient rows are finished by the row-sparse tiles launched together with these
     a.skip_salient = 1;
+    AttnTimer& tm = g_attn_timer;
+    hipEvent_t e1 = nullptr;
+    if (tm.enabled) {
+      if (tm.used == tm.ev.size()) {
+        hipEvent_t a0 = nullptr, a1 = nullptr;
+        if (hipEventCreate(&a0) != hipSuccess || hipEventCreate(&a1) != hipSuccess)
+          return fail("hipEventCreate failed (attention timer)");
+        tm.ev.emplace_back(a0, a1);
+      }
+      if (hipEventRecord(tm.ev[tm.used].first, s) != hipSuccess) return fail("hipEventRecord failed (attention timer)");
+      e1 = tm.ev[tm.used].second;
+      ++tm.used;
+    }
     if (int rc = launch_attention_step(*fused_rs, fused_rs_rows, a, max_seqlen_q, s)) return rc;
+    if (e1 && hipEventRecord(e1, s) != hipSuccess) return fail("hipEventRecord failed (attention timer)");
   } else {
     if (int rc = launch_attention(AttnMode::ColSparse, a, max_seqlen_q, s)) return rc;
   }

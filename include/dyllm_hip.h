@@ -49,6 +49,14 @@ const char* dyllm_last_error(void);
 /* ABI version of this library. */
 int dyllm_abi_version(void);
 
+/* Timing of the fused attention kernel inside dyllm_sparse_attention_step (no counterpart in
+ * the reference; for benchmarks that need that kernel's own duration): while enabled (per host
+ * thread), every step call records a library-owned HIP event pair around the attention launch on
+ * its stream. _read synchronises on the recorded events, returns their summed duration and count
+ * and forgets them. */
+int dyllm_attention_timer(int enable);
+int dyllm_attention_timer_read(float* total_ms, int* launches);
+
 /* ---- attention ------------------------------------------------------------------------ */
 
 /* Workspace for dyllm_attention_sparse_varlen. */
