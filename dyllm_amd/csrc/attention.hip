@@ -34,6 +34,16 @@ constexpr int kBK = 64;              // keys per block (reference block width)
 constexpr int kKStride = kD + 8;     // K tile row stride (elements): 272 B, conflict-free b128 reads
 constexpr int kVStride = kBK + 12;   // V^T tile row stride (elements): 152 B, conflict-free b64 reads
 
+// Two-pass column-sparse path (sequences of at most kMaxBlk2 key blocks): LDS it needs beyond
+// the K / V^T tiles.
+constexpr int kMaxBlk2 = 64;
+struct ColSparseLds {
+  float* m;          // [NW][kMaxBlk2][32] running max of each query row after each key block
+  int16_t* keys;     // [kMaxBlk2 * kBK] salient keys in 16-slot groups, -1 = padding
+  uint8_t* gblk;     // [4 * kMaxBlk2] key block of each group
+  int* ngrp;         // number of groups
+};
+
 union Pack8 {
   bf16x8_t v;
   uint32_t u[4];
@@ -53,7 +63,7 @@ __device__ __forceinline__ int xcd_remap(int wg, int nwg) {
 // (all query tiles of one (sequence, kv-head) land on the same XCD and share its L2).
 template <AttnMode MODE, int NW>
 __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16_t* __restrict__ k_lds,
-                                               uint16_t* __restrict__ vt_lds) {
+                                               uint16_t* __restrict__ vt_lds, const ColSparseLds& sp) {
   constexpr int NT = NW * 64;              // threads
   constexpr int BQ = NW * 32;              // query rows per workgroup
   constexpr int KCH = kBK * kD / 8 / NT;   // 16-byte K chunks per thread per tile
@@ -213,6 +223,224 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     }
   };
 
+  bool two_pass = false;
+  if constexpr (MODE == AttnMode::ColSparse) two_pass = sp.m != nullptr && nkb <= kMaxBlk2;
+  if (two_pass) {
+    // Two passes instead of PV on every 16-key group that holds a salient key.
+    // Pass 1: S = Q K^T over all keys for the running max and row sum only (the same fp32
+    // arithmetic as the single-pass loop), recording each block's running max m_kb.
+    // Pass 2: only the salient keys, grouped 16 per key block: S recomputed with the same MFMA
+    // sequence, P = bf16(exp2(S*c2 - m_kb*c2)) -- the identical bf16 values the single pass
+    // feeds its PV -- and O += P dV with the accumulator rescaled from the previous group's
+    // block max to this one's (the product of the per-block rescales in one factor).
+    if (w == 0) {
+      // salient-key groups of this sequence from the per-block key bits
+      uint64_t word = 0;
+      int grp = 0;
+      if (lane < nkb) {
+        word = a.kmask[int64_t(b) * a.nblk + lane];
+        if (lane == nkb - 1 && (Lk & (kBK - 1))) word &= (1ull << (Lk & (kBK - 1))) - 1;   // keys < Lk only
+        grp = (__popcll(word) + 15) >> 4;
+      }
+      int inc = grp;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += v;
+      }
+      const int g0 = inc - grp;
+      if (lane == 63) *sp.ngrp = inc;
+      int n = 0;
+      while (word) {
+        sp.keys[g0 * 16 + n] = int16_t(lane * kBK + __builtin_ctzll(word));
+        word &= word - 1;
+        ++n;
+      }
+      for (; n < grp * 16; ++n) sp.keys[g0 * 16 + n] = -1;
+      for (int j = 0; j < grp; ++j) sp.gblk[g0 + j] = uint8_t(lane);
+    }
+    __syncthreads();
+    float* m_tab = sp.m + w * (kMaxBlk2 * 32) + ql;
+    auto qk = [&](f32x16_t (&sa)[2], const uint16_t* kt) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sa[t][r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(&kt[(t * 32 + ql) * kKStride + 16 * s + half * 8]);
+          sa[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sa[t], 0, 0, 0);
+        }
+      }
+    };
+    auto fetch_k = [&](int kb) {
+      const int key0 = kb * kBK;
+#pragma unroll
+      for (int it = 0; it < KCH; ++it) {
+        const int c = tid + NT * it;
+        const int key = c >> 4, dc = c & 15;
+        kreg[it] = (key0 + key < Lk) ? *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8)
+                                     : make_uint4(0, 0, 0, 0);
+      }
+    };
+    auto stage_k = [&](uint16_t* kt) {
+#pragma unroll
+      for (int it = 0; it < KCH; ++it) {
+        const int c = tid + NT * it;
+        const int key = c >> 4, dc = c & 15;
+        *reinterpret_cast<uint4*>(&kt[key * kKStride + dc * 8]) = kreg[it];
+      }
+    };
+
+    // ---- pass 1 ----
+    // K double-buffered (the V^T tile, idle in this pass, holds the odd blocks): block kb+1 is
+    // staged while block kb is scored, one barrier per block
+    static_assert(kBK * kKStride <= kD * kVStride, "V^T tile too small for a K tile");
+    if (nkb > 0) {
+      fetch_k(0);
+      stage_k(k_lds);
+    }
+    if (nkb > 1) fetch_k(1);
+    __syncthreads();
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int key0 = kb * kBK;
+      f32x16_t sa[2];
+      qk(sa, (kb & 1) ? vt_lds : k_lds);
+      if (kb + 1 < nkb) stage_k((kb & 1) ? k_lds : vt_lds);
+      if (kb + 2 < nkb) fetch_k(kb + 2);
+      if (key0 + kBK > Lk) {  // ragged last block only
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = key0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+            if (key >= Lk) sa[t][r] = -FLT_MAX;
+          }
+      }
+      float bm = sa[0][0];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sa[t][r]);
+      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+      const float m_new = fmaxf(m_run, bm);
+      const float rescale = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
+      const float m2 = m_new * c2;
+      m_run = m_new;
+      float psum = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[t][r], c2, -m2));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[t][r + 1], c2, -m2));
+          psum += e0 + e1;
+        }
+      l_run = l_run * rescale + psum;
+      if (half == 0) m_tab[kb * 32] = m_new;
+      __syncthreads();
+    }
+    // (the last barrier also ends pass 1's reads of both tiles before pass 2 restages them)
+
+    // ---- pass 2 ----
+    const int ngrp = *sp.ngrp;
+    const int npb = (ngrp + 3) >> 2;
+    // slots past the last group (the tail of the last 64-slot block) were never written
+    auto slot_key = [&](int sl) -> int { return sl < ngrp * 16 ? int(sp.keys[sl]) : -1; };
+    auto load_meta2 = [&](int pb) {
+      if (pb >= npb) return;
+#pragma unroll
+      for (int it = 0; it < VIT; ++it) {
+        const int kq = (tid + NT * it) & 15;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = slot_key(pb * kBK + 4 * kq + j);
+          meta_slot[it][j] = key < 0 ? -1 : (ks_b ? ks_b[key] : key);
+        }
+      }
+    };
+    auto fetch2 = [&](int pb) {
+#pragma unroll
+      for (int it = 0; it < KCH; ++it) {
+        const int c = tid + NT * it;
+        const int key = slot_key(pb * kBK + (c >> 4)), dc = c & 15;
+        kreg[it] = key >= 0 ? *reinterpret_cast<const uint4*>(Kb + int64_t(key) * ldkv + dc * 8) : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int it = 0; it < VIT; ++it) {
+        const int dc = (tid + NT * it) >> 4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t r = meta_slot[it][j];
+          vreg[it][j] = (r >= 0) ? *reinterpret_cast<const uint4*>(Vb + r * ldkv + dc * 8) : make_uint4(0, 0, 0, 0);
+        }
+      }
+    };
+    mask_next = ~0ull;
+    load_meta2(0);
+    if (npb > 0) fetch2(0);
+    load_meta2(1);
+    float m_prev = -FLT_MAX;
+    int blk_prev = -1;
+    for (int pb = 0; pb < npb; ++pb) {
+      stage();
+      __syncthreads();
+      if (pb + 1 < npb) fetch2(pb + 1);
+      load_meta2(pb + 2);
+      f32x16_t sa[2];
+      qk(sa, k_lds);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int g = pb * 4 + t * 2 + u;
+          if (g >= ngrp) continue;
+          const int blk = __builtin_amdgcn_readfirstlane(int(sp.gblk[g]));
+          const float m_g = m_tab[blk * 32];
+          if (blk != blk_prev) {
+            const float f = __builtin_amdgcn_exp2f((m_prev - m_g) * c2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) o_acc[i][r] *= f;
+            m_prev = m_g;
+            blk_prev = blk;
+          }
+          const float m2 = m_g * c2;
+          Pack8 p;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[t][8 * u + 2 * j], c2, -m2));
+            const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[t][8 * u + 2 * j + 1], c2, -m2));
+            p.u[j] = pack_bf16x2(e0, e1);
+          }
+          const int kofs = t * 32 + u * 16 + half * 4;
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const uint16_t* vr = &vt_lds[(dt * 32 + ql) * kVStride + kofs];
+            Pack4 lo, hi;
+            lo.d = *reinterpret_cast<const uint2*>(vr);
+            hi.d = *reinterpret_cast<const uint2*>(vr + 8);
+            Pack8 va;
+            va.u[0] = lo.u[0];
+            va.u[1] = lo.u[1];
+            va.u[2] = hi.u[0];
+            va.u[3] = hi.u[1];
+            o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, p.v, o_acc[dt], 0, 0, 0);
+          }
+        }
+      __syncthreads();
+    }
+    // the blocks after the last salient one rescale the accumulator to the final max
+    {
+      const float f = __builtin_amdgcn_exp2f((m_prev - m_run) * c2);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[i][r] *= f;
+    }
+  }
+  if (!two_pass) {
   load_meta(0);
   if (nkb > 0) fetch(0);
   load_meta(1);
@@ -303,6 +531,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
         }
     }
     __syncthreads();
+  }
   }
 
   // ---- epilogue ---------------------------------------------------------------------------
@@ -421,7 +650,16 @@ template <AttnMode MODE, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
-  attention_tile<MODE, NW>(a, xcd_remap(blockIdx.x, gridDim.x), k_lds, vt_lds);
+  if constexpr (MODE == AttnMode::ColSparse) {
+    __shared__ float m_lds[NW * kMaxBlk2 * 32];
+    __shared__ int16_t key_lds[kMaxBlk2 * kBK];
+    __shared__ uint8_t gblk_lds[4 * kMaxBlk2];
+    __shared__ int ngrp_lds;
+    attention_tile<MODE, NW>(a, xcd_remap(blockIdx.x, gridDim.x), k_lds, vt_lds,
+                             ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds});
+  } else {
+    attention_tile<MODE, NW>(a, xcd_remap(blockIdx.x, gridDim.x), k_lds, vt_lds, ColSparseLds{});
+  }
 }
 
 // Fused sparse step: the row-sparse tiles of the salient queries (finishing their rows) and the
@@ -433,12 +671,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     AttnArgs rs, AttnArgs cs, int n_rs, int n_rs_pad) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
+  __shared__ float m_lds[NW * kMaxBlk2 * 32];
+  __shared__ int16_t key_lds[kMaxBlk2 * kBK];
+  __shared__ uint8_t gblk_lds[4 * kMaxBlk2];
+  __shared__ int ngrp_lds;
   const int wg = blockIdx.x;
   if (wg < n_rs_pad) {
     const int t = xcd_remap(wg, n_rs_pad);
-    if (t < n_rs) attention_tile<AttnMode::RowSparse, NW>(rs, t, k_lds, vt_lds);
+    if (t < n_rs) attention_tile<AttnMode::RowSparse, NW>(rs, t, k_lds, vt_lds, ColSparseLds{});
   } else {
-    attention_tile<AttnMode::ColSparse, NW>(cs, xcd_remap(wg - n_rs_pad, int(gridDim.x) - n_rs_pad), k_lds, vt_lds);
+    attention_tile<AttnMode::ColSparse, NW>(cs, xcd_remap(wg - n_rs_pad, int(gridDim.x) - n_rs_pad), k_lds, vt_lds,
+                                            ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds});
   }
 }
 

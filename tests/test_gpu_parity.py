@@ -237,6 +237,39 @@ def test_attention_sparse_varlen(dev, q_pruned, H, Hkv):
     assert excluded < Tq // 20
 
 
+@pytest.mark.parametrize("lens,sal_frac,H,Hkv", [
+    # most keys salient: up to 4 sixteen-key groups per 64-key block, ragged last blocks
+    ([(30, 290), (100, 157), (5, 60)], 0.6, 4, 2),
+    # 4096 keys (the largest two-pass sequence) next to 4200 (the single-pass path) in one launch
+    ([(64, 4032), (200, 4000)], 0.05, 2, 1),
+])
+def test_attention_sparse_varlen_shapes(dev, lens, sal_frac, H, Hkv):
+    """Column-sparse attention where the salient keys fill several groups per key block, and
+    across the sequence length where the kernel switches from the two-pass to the single-pass
+    path."""
+    ops = _ops()
+    print(f"[colsparse shapes] lens={lens} sal_frac={sal_frac}", flush=True)
+    cs = _colsparse_case(5, H, Hkv, True, lens=lens, sal_frac=sal_frac)
+    Tq = cs["q"].shape[0]
+    _, st0, _ = ref.attention_sparse_varlen(cs["q"], cs["k"], cs["dv"], cs["c"], cs["o_sal"], cs["cu_q"],
+                                            cs["cu_k"], cs["idx_q"], 0.99)
+    cos = ref.cosine_from_stats(st0).numpy()
+    tau = float(np.median(cos))
+    want_o, want_st, want_m = ref.attention_sparse_varlen(cs["q"], cs["k"], cs["dv"], cs["c"], cs["o_sal"],
+                                                          cs["cu_q"], cs["cu_k"], cs["idx_q"], tau)
+    t = lambda a: torch.as_tensor(a).to(dev)
+    stats = torch.zeros(Tq, 3, dtype=torch.float32, device=dev)
+    mask = torch.empty(Tq, dtype=torch.bool, device=dev)
+    o = ops.attention_sparse_varlen(t(cs["q"]), t(cs["k"]), t(cs["dv"]), t(cs["c"]), t(cs["o_sal"]), t(cs["cu_q"]),
+                                    t(cs["cu_k"]), cs["maxq"], cs["maxk"], Tq, t(cs["cu_s"]), t(cs["idx_q"]), stats,
+                                    mask, tau, True, t(cs["idx_k"]))
+    assert_bf16_close(o, want_o, what="column-sparse output")
+    assert torch.equal(o.cpu()[torch.from_numpy(cs["idx_q"]).long()], cs["o_sal"])
+    torch.testing.assert_close(stats.cpu(), want_st, rtol=1e-4, atol=1e-2)
+    excluded = assert_mask_equal(mask.cpu().numpy(), want_m.numpy(), cos, tau)
+    assert excluded < Tq // 20
+
+
 # ---------------------------------------------------------------------------------------
 # FFN / MoE
 # ---------------------------------------------------------------------------------------
