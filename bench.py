@@ -45,7 +45,7 @@ PEAK_HBM_GBS = 8000.0
 # calibrated against a 256 MiB copy (profiles/pmc_gemm_gate_up_config1.md).
 GATE_UP_TRAFFIC_BYTES = 364.0e6
 # HBM bytes per launch of the fused attention kernel, same method (profiles/pmc_attention_step_config1.md)
-ATTN_TRAFFIC_BYTES = 424.0e6
+ATTN_TRAFFIC_BYTES = 423.2e6
 
 
 def build_workload(cfg, layers, device, seed=0):
@@ -449,6 +449,26 @@ def main():
         print(f"[bench] CPU baseline on {threads} threads", file=sys.stderr, flush=True)
         cpu = cpu_baseline(cfg, int(round(avg_n)), threads)
 
+    rf_attn = {"kernel": "attention_step_kernel<4> (fused step: row-sparse + column-sparse tiles)",
+               "bound": "mfma", "achieved": round(attn_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+               "frac": round(attn_tf / PEAK_BF16_TFLOPS, 4), "traffic": ATTN_TRAFFIC_BYTES,
+               "traffic_unit": "bytes per launch (PMC)", "algorithmic_bytes": 345.0e6,
+               "avg_launch_us": round(avg_attn_ms * 1e3, 2), "flop_per_launch": attn_flops,
+               "note": "VALU/latency bound (softmax over all query-key pairs); frac counts algorithmic "
+                       "MFMA work only"}
+    rf_gate = {"kernel": f"gemm_kernel<{gate_bm},4,SwiGLU> (gathered gate_up + SiLU*up, tile {gate_bm}x256)",
+               "bound": "mfma",
+               "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+               "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
+               "traffic_unit": "bytes per launch (PMC)", "algorithmic_bytes": 231.4e6,
+               "avg_launch_us": round(avg_gate_ms * 1e3, 2),
+               "flop_per_launch": flops}
+    # the dominant kernel (longest mean launch) carries "roofline", the other one rides along
+    if avg_attn_ms >= avg_gate_ms:
+        rf_main, rf_other_key, rf_other = rf_attn, "roofline_gate_up", rf_gate
+    else:
+        rf_main, rf_other_key, rf_other = rf_gate, "roofline_attention", rf_attn
+
     line = {
         "metric": "salient-path tokens/s per denoise step, LLaDA-8B shape bf16; % HBM/MFMA roofline",
         "value": round(value, 1),
@@ -466,20 +486,8 @@ def main():
                    "layers": layers, "batch": cfg["batch"], "seq_len": cfg["prompt"] + cfg["response"],
                    "response_len": cfg["response"], "hidden": hid, "heads": cfg["heads"], "ffn": inter,
                    "tau": cfg["tau"], "avg_salient_rows_per_layer": round(avg_n, 1)},
-        "roofline": {"kernel": "attention_step_kernel<4> (fused step: row-sparse + column-sparse tiles)",
-                     "bound": "mfma", "achieved": round(attn_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(attn_tf / PEAK_BF16_TFLOPS, 4), "traffic": ATTN_TRAFFIC_BYTES,
-                     "traffic_unit": "bytes per launch (PMC)", "algorithmic_bytes": 345.0e6,
-                     "avg_launch_us": round(avg_attn_ms * 1e3, 2), "flop_per_launch": attn_flops,
-                     "note": "VALU/latency bound (softmax over all query-key pairs); frac counts algorithmic "
-                             "MFMA work only"},
-        "roofline_gate_up": {"kernel": f"gemm_kernel<{gate_bm},4,SwiGLU> (gathered gate_up + SiLU*up, tile {gate_bm}x256)",
-                     "bound": "mfma",
-                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
-                     "traffic_unit": "bytes per launch (PMC)", "algorithmic_bytes": 231.4e6,
-                     "avg_launch_us": round(avg_gate_ms * 1e3, 2),
-                     "flop_per_launch": flops},
+        "roofline": rf_main,
+        rf_other_key: rf_other,
         "cpu_baseline": cpu,
         "kv_projection": kv_proj,
     }
