@@ -23,11 +23,12 @@
 // both measured slower), each wavefront (BM/2) x 64
 // of v_mfma_f32_32x32x16_bf16 tiles. Operands move global -> LDS with the gfx950 direct
 // LDS-load (global_load_lds_dwordx4), no register staging. Operands are staged through
-// LDS in two buffers of unpadded 128-byte rows whose 16-byte chunks are XOR-swizzled by row
-// (chunk ^ (row & 7)), so the fragment reads are spread over the banks; the next K slice is
-// loaded into the other buffer while the current one is multiplied, and one wait + barrier
-// per K slice separates the buffers (32-wide K stages with 4-5 buffers, i.e. twice the
-// prefetch depth, measured slower). Within a slice the fragment reads of the next 16-wide K
+// LDS in unpadded 128-byte rows whose 16-byte chunks are XOR-swizzled by row
+// (chunk ^ (row & 7)), so the fragment reads are spread over the banks. A slices (the gathered
+// rows, L2-resident) are double-buffered and loaded one slice ahead; W slices (streamed from
+// HBM) are triple-buffered and loaded two slices ahead (2*BM*64 + 3*256*64 elements: 144 KB at
+// BM = 192, the full 160 KB at 256). One wait + barrier per K slice: vmcnt(4) leaves only the
+// newest W loads in flight (32-wide K stages with 4-5 buffers of both operands measured slower). Within a slice the fragment reads of the next 16-wide K
 // substep are interleaved one per MFMA with the current substep, pinned with
 // sched_group_barrier (the compiler's own schedule clusters the reads and stalls on them;
 // 4-8 % with warm caches). The MFMA is issued as D = W_tile * A_tile^T
@@ -69,7 +70,6 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   constexpr int NW = 2 * WGN;                 // wavefronts: 2 along M x WGN along N
   constexpr int WM = BM / 2, WN = BN / WGN;   // wave tile (rows of A, rows of W)
   constexpr int TM = WM / 32, TN = WN / 32;   // 32x32 MFMA tiles per wave
-  constexpr int BUF = (BM + BN) * kGemmBK;
   const int64_t m0 = int64_t(mt) * BM;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -118,14 +118,21 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   }
   typedef __attribute__((address_space(3))) void lds_void;
   typedef const __attribute__((address_space(1))) void glb_void;
-  auto stage = [&](int kt, int buf) {
+  // LDS: A slices double-buffered, W slices (streamed from HBM) triple-buffered so their loads
+  // are issued two slices ahead: [A0 | A1 | W0 | W1 | W2]
+  uint16_t* const a_lds = gsm;
+  uint16_t* const w_lds = gsm + 2 * BM * kGemmBK;
+  auto stage_a = [&](int kt, int buf) {
     const int64_t ko = int64_t(kt) * kGemmBK;
-    uint16_t* As = gsm + buf * BUF;
-    uint16_t* Ws = As + BM * kGemmBK;
+    uint16_t* As = a_lds + buf * (BM * kGemmBK);
 #pragma unroll
     for (int i = 0; i < CA; ++i)
       __builtin_amdgcn_global_load_lds((glb_void*)(a_src[i] + ko),
                                        (lds_void*)(As + (w + NW * i) * 8 * kGemmBK), 16, 0, 0);
+  };
+  auto stage_w = [&](int kt, int buf) {
+    const int64_t ko = int64_t(kt) * kGemmBK;
+    uint16_t* Ws = w_lds + buf * (BN * kGemmBK);
 #pragma unroll
     for (int i = 0; i < CW; ++i)
       __builtin_amdgcn_global_load_lds((glb_void*)(w_src[i] + ko),
@@ -151,8 +158,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   // Fragments are double-buffered in registers (two named sets so every index stays static):
   // the LDS reads of K-substep ks+1 are issued one by one between the MFMAs of ks.
   bf16x8_t wf0[TN], af0[TM], wf1[TN], af1[TM];
-  auto fload = [&](const uint16_t* As, int ks, bf16x8_t* wf, bf16x8_t* af) {
-    const uint16_t* Ws = As + BM * kGemmBK;
+  auto fload = [&](const uint16_t* As, const uint16_t* Ws, int ks, bf16x8_t* wf, bf16x8_t* af) {
     const int ch = 2 * ks + half;
 #pragma unroll
     for (int i = 0; i < TN; ++i) wf[i] = *reinterpret_cast<const bf16x8_t*>(&Ws[swz(wrow_base(i) + l32, ch)]);
@@ -181,32 +187,49 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   // (lgkmcnt, so no wave refills a buffer still being read) and for its own direct-to-LDS loads of
   // the next slice (vmcnt, so the slice is complete for every wave after the barrier). That is all
   // the LDS ping-pong needs; the workgroup-scope fences of __syncthreads() cost 2-4 % of the step.
-  stage(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const uint16_t* As = gsm + cur * BUF;
-    if (kt + 1 < nk) stage(kt + 1, cur ^ 1);
-    fload(As, 0, wf0, af0);
-    __builtin_amdgcn_sched_barrier(0);
-    fload(As, 1, wf1, af1);
-    mma(wf0, af0);
-    interleave();
-    __builtin_amdgcn_sched_barrier(0);
-    fload(As, 2, wf0, af0);
-    mma(wf1, af1);
-    interleave();
-    __builtin_amdgcn_sched_barrier(0);
-    fload(As, 3, wf1, af1);
-    mma(wf0, af0);
-    interleave();
-    __builtin_amdgcn_sched_barrier(0);
-    mma(wf1, af1);
-    // this wave's LDS reads of stage `cur` are done before any wave refills it
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  // Loads complete in issue order, so vmcnt(CW) at the end of slice kt leaves only the W loads
+  // of slice kt+2 (issued last) in flight: A and W of slice kt+1 have landed.
+  static_assert(CW == 4, "vmcnt immediate below assumes 4 W blocks per wavefront");
+  stage_a(0, 0);
+  stage_w(0, 0);
+  if (nk > 1) {
+    stage_w(1, 1);
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  } else {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  __builtin_amdgcn_s_barrier();
+  int wcur = 0;   // kt % 3
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint16_t* As = a_lds + (kt & 1) * (BM * kGemmBK);
+    const uint16_t* Ws = w_lds + wcur * (BN * kGemmBK);
+    const int wnext2 = wcur == 0 ? 2 : wcur - 1;   // (kt + 2) % 3
+    if (kt + 1 < nk) stage_a(kt + 1, (kt & 1) ^ 1);
+    if (kt + 2 < nk) stage_w(kt + 2, wnext2);
+    fload(As, Ws, 0, wf0, af0);
+    __builtin_amdgcn_sched_barrier(0);
+    fload(As, Ws, 1, wf1, af1);
+    mma(wf0, af0);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    fload(As, Ws, 2, wf0, af0);
+    mma(wf1, af1);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    fload(As, Ws, 3, wf1, af1);
+    mma(wf0, af0);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    mma(wf1, af1);
+    // this wave's LDS reads of the current slice are done before any wave refills its buffers
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (kt + 2 < nk) {
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __builtin_amdgcn_s_barrier();
+    wcur = wcur == 2 ? 0 : wcur + 1;
   }
 
   // ---- epilogue: lane owns row m = m0 + wm*WM + 32j + l32 -------------------------------
@@ -362,7 +385,7 @@ static int num_cus() {
   return n;
 }
 
-static constexpr size_t lds_bytes(int bm) { return size_t(2) * (bm + kGemmBN) * kGemmBK * sizeof(uint16_t); }
+static constexpr size_t lds_bytes(int bm) { return size_t(2 * bm + 3 * kGemmBN) * kGemmBK * sizeof(uint16_t); }
 
 template <int BM, int WGN, GemmEpi EPI>
 static int launch_gemm_cfg(const GemmArgs& g0, int64_t m_tiles, int ksplit, hipStream_t s) {
