@@ -43,7 +43,7 @@ EVENT_STRIDE = 8
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the gate_up GEMM at this workload, from rocprofv3 FETCH_SIZE / WRITE_SIZE
 # calibrated against a 256 MiB copy (profiles/pmc_gemm_gate_up_config1.md).
-GATE_UP_TRAFFIC_BYTES = 364.0e6
+GATE_UP_TRAFFIC_BYTES = 361.7e6
 # HBM bytes per launch of the fused attention kernel, same method (profiles/pmc_attention_step_config1.md)
 ATTN_TRAFFIC_BYTES = 423.2e6
 
