@@ -19,6 +19,7 @@ from __future__ import annotations
 
 from typing import List, Optional
 
+import numpy as np
 import torch
 
 from ..config import Config
@@ -43,6 +44,48 @@ def build_model(config: Config, device="cuda"):
     return model
 
 
+_NP_DTYPE = {torch.int32: np.int32, torch.long: np.int64, torch.float32: np.float32}
+
+
+class _HostStaging:
+    """One host-to-device transfer per step for all of its index / offset metadata (the reference
+    issues one small copy per tensor, model_runner.py:140-298). Fields are packed 16-byte aligned
+    into a reusable pinned buffer and copied with one non-blocking copy into a fresh device block;
+    each field comes back as a typed view of that block. The pinned buffer is rewritten only after
+    the previous copy out of it has completed."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.fields = []
+        self.pinned = None
+        self.copied = None   # event recorded after the last copy out of `pinned`
+
+    def add(self, name: str, data, dtype) -> None:
+        self.fields.append((name, np.ascontiguousarray(np.asarray(data, dtype=_NP_DTYPE[dtype])), dtype))
+
+    def flush(self) -> dict:
+        offs, n = [], 0
+        for _, arr, _ in self.fields:
+            offs.append(n)
+            n += (arr.nbytes + 15) // 16 * 16
+        fields, self.fields = self.fields, []
+        if self.device.type != "cuda":
+            return {name: torch.from_numpy(arr.copy()).to(self.device) for name, arr, _ in fields}
+        if self.copied is not None:
+            self.copied.synchronize()
+        if self.pinned is None or self.pinned.numel() < n:
+            cap = max(n, 2 * self.pinned.numel() if self.pinned is not None else 1 << 16)
+            self.pinned = torch.empty(cap, dtype=torch.uint8, pin_memory=True)
+        host = self.pinned.numpy()
+        for (_, arr, _), o in zip(fields, offs):
+            host[o:o + arr.nbytes] = arr.view(np.uint8).reshape(-1)
+        dev = torch.empty(max(n, 16), dtype=torch.uint8, device=self.device)
+        dev[:n].copy_(self.pinned[:n], non_blocking=True)
+        self.copied = torch.cuda.Event()
+        self.copied.record()
+        return {name: dev[o:o + arr.nbytes].view(dt) for (name, arr, dt), o in zip(fields, offs)}
+
+
 def q_pruned_step(seq: Sequence) -> bool:
     """Sparse step that queries only the response rows (model_runner.py:205)."""
     return seq.processed_steps > 4 and seq.processed_steps % 4 != 0
@@ -59,6 +102,7 @@ class ModelRunner:
         hf = config.hf_config
         self.model = model if model is not None else build_model(config, device)
         self.sampler = DreamSampler("entropy") if hf.model_type == "Dream" else LLaDASampler("confidence")
+        self.staging = _HostStaging(self.device)
 
     def _dev(self, data, dtype):
         t = torch.tensor(data, dtype=dtype)
@@ -77,14 +121,23 @@ class ModelRunner:
             cu.append(cu[-1] + L)
             lens.append(L)
             ids.append(seq.seq_id)
-        i32 = torch.int32
-        cu_dev = self._dev(cu, i32)
-        md.running_seqs = ids
-        md.running_seqs_tensor = self._dev(ids, torch.long)
-        set_context(True, cu_seqlens_q=cu_dev, cu_seqlens_q_cpu=cu, cu_seqlens_k=cu_dev, cu_seqlens_k_cpu=cu,
-                    max_seqlen_q=max(lens), max_seqlen_k=max(lens), context_lens=self._dev(lens, i32),
-                    context_lens_cpu=lens, total_seqlen=cu[-1], total_seqlen_k=cu[-1])
-        return self._dev(input_ids, torch.long), self._dev(positions, torch.long)
+        i32, i64 = torch.int32, torch.long
+        st = self.staging
+        st.add("cu", cu, i32)
+        st.add("ids", ids, i64)
+        st.add("lens", lens, i32)
+        st.add("input_ids", input_ids, i64)
+        st.add("positions", positions, i64)
+
+        def finish(d):
+            md.running_seqs = ids
+            md.running_seqs_tensor = d["ids"]
+            set_context(True, cu_seqlens_q=d["cu"], cu_seqlens_q_cpu=cu, cu_seqlens_k=d["cu"], cu_seqlens_k_cpu=cu,
+                        max_seqlen_q=max(lens), max_seqlen_k=max(lens), context_lens=d["lens"],
+                        context_lens_cpu=lens, total_seqlen=cu[-1], total_seqlen_k=cu[-1])
+            return d["input_ids"], d["positions"]
+
+        return finish
 
     def prepare_sparse(self, seqs: List[Sequence]):
         md = get_metadata()
@@ -116,25 +169,32 @@ class ModelRunner:
             lens.append(L)
             ids.append(seq.seq_id)
         i32, i64 = torch.int32, torch.long
-        cu_s_dev = self._dev(cu_s, i32)
-        md.running_seqs = ids
-        md.running_seqs_tensor = self._dev(ids, i64)
-        idx_q_dev = self._dev(idx_q, i64)
-        set_context(False, cu_seqlens_q=self._dev(cu_q, i32), cu_seqlens_q_cpu=cu_q, cu_seqlens_k=self._dev(cu_k, i32),
-                    cu_seqlens_k_cpu=cu_k, cu_promptlens=self._dev(cu_p, i32), cu_updatedlens=cu_s_dev,
-                    cu_salientlens=cu_s_dev, max_seqlen_q=max(cu_q[i + 1] - cu_q[i] for i in range(len(seqs))),
-                    max_seqlen_k=max(lens), idx_updated_row=self._dev(idx_upd, i32), idx_salient_row=idx_q_dev,
-                    idx_salient_row_k=self._dev(idx_k, i64) if pruned else None,
-                    max_salientlen=max(cu_s[i + 1] - cu_s[i] for i in range(len(seqs))),
-                    context_lens=self._dev(lens, i32), context_lens_cpu=lens, total_seqlen_k=cu_k[-1],
-                    total_seqlen=cu_q[-1], positions_k=self._dev(positions_k, i64))
-        return self._dev(input_ids, i64), self._dev(positions, i64)
+        st = self.staging
+        for name, data, dt in (("cu_s", cu_s, i32), ("ids", ids, i64), ("idx_q", idx_q, i64), ("cu_q", cu_q, i32),
+                               ("cu_k", cu_k, i32), ("cu_p", cu_p, i32), ("idx_upd", idx_upd, i32),
+                               ("idx_k", idx_k, i64), ("lens", lens, i32), ("positions_k", positions_k, i64),
+                               ("input_ids", input_ids, i64), ("positions", positions, i64)):
+            st.add(name, data, dt)
 
-    def prepare_sample(self, seqs: List[Sequence]):
+        def finish(d):
+            md.running_seqs = ids
+            md.running_seqs_tensor = d["ids"]
+            set_context(False, cu_seqlens_q=d["cu_q"], cu_seqlens_q_cpu=cu_q, cu_seqlens_k=d["cu_k"],
+                        cu_seqlens_k_cpu=cu_k, cu_promptlens=d["cu_p"], cu_updatedlens=d["cu_s"],
+                        cu_salientlens=d["cu_s"], max_seqlen_q=max(cu_q[i + 1] - cu_q[i] for i in range(len(seqs))),
+                        max_seqlen_k=max(lens), idx_updated_row=d["idx_upd"], idx_salient_row=d["idx_q"],
+                        idx_salient_row_k=d["idx_k"] if pruned else None,
+                        max_salientlen=max(cu_s[i + 1] - cu_s[i] for i in range(len(seqs))),
+                        context_lens=d["lens"], context_lens_cpu=lens, total_seqlen_k=cu_k[-1],
+                        total_seqlen=cu_q[-1], positions_k=d["positions_k"])
+            return d["input_ids"], d["positions"]
+
+        return finish
+
+    def prepare_sample(self, seqs: List[Sequence], pruned: bool):
         """Candidate rows of the current block and the per-sequence sampling knobs
-        (model_runner.py:300-372)."""
+        (model_runner.py:300-372); staged with the step's other metadata."""
         mask = self.config.mask_id
-        pruned = get_context().idx_salient_row_k is not None
         rels, counts, temps, transfers, top_ps, top_ks, thrs, offsets = [], [], [], [], [], [], [], []
         has_t = has_p = has_k = has_thr = False
         for seq in seqs:
@@ -161,14 +221,26 @@ class ModelRunner:
         cu = [0]
         for c in counts:
             cu.append(cu[-1] + c)
-        f32 = torch.float32
-        params = (self._dev(temps, f32) if has_t else None,
-                  self._dev(top_ks, torch.int32) if has_k else None,
-                  self._dev(top_ps, f32) if has_p else None,
-                  block,
-                  self._dev(thrs, f32) if has_thr else None)
-        indices = (self._dev(rels, torch.long), self._dev(offsets, torch.long), self._dev(cu, torch.int32))
-        return params, indices, self._dev(transfers, torch.int32)
+        f32, i32, i64 = torch.float32, torch.int32, torch.long
+        st = self.staging
+        if has_t:
+            st.add("s_temps", temps, f32)
+        if has_k:
+            st.add("s_top_ks", top_ks, i32)
+        if has_p:
+            st.add("s_top_ps", top_ps, f32)
+        if has_thr:
+            st.add("s_thrs", thrs, f32)
+        st.add("s_rels", rels, i64)
+        st.add("s_offsets", offsets, i64)
+        st.add("s_cu", cu, i32)
+        st.add("s_transfers", transfers, i32)
+
+        def finish(d):
+            params = (d.get("s_temps"), d.get("s_top_ks"), d.get("s_top_ps"), block, d.get("s_thrs"))
+            return params, (d["s_rels"], d["s_offsets"], d["s_cu"]), d["s_transfers"]
+
+        return finish
 
     # -- execution ------------------------------------------------------------------------
     @torch.inference_mode()
@@ -181,9 +253,14 @@ class ModelRunner:
         else:
             self.num_sparse_forwards += 1
         get_metadata().finished_seqs = list(finished_seqs or [])
-        input_ids, positions = self.prepare_full(seqs) if is_full else self.prepare_sparse(seqs)
+        # all host-built metadata of the step (batch layout and sampling inputs) in one transfer
+        finish_batch = self.prepare_full(seqs) if is_full else self.prepare_sparse(seqs)
+        pruned = not is_full and all(q_pruned_step(s) for s in seqs)
+        finish_sample = self.prepare_sample(seqs, pruned)
+        staged = self.staging.flush()
+        input_ids, positions = finish_batch(staged)
+        params, indices, transfers = finish_sample(staged)
         logits = self.run_model(input_ids, positions, is_full)
-        params, indices, transfers = self.prepare_sample(seqs)
         with torch.inference_mode():
             pos, tok, cnt = self.sampler(input_logits=logits, ctx=get_context(), input_indices=indices,
                                          temperatures=params[0], num_transfer=transfers, top_k=params[1],

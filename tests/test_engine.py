@@ -150,18 +150,20 @@ def test_prepare_sparse_indices():
     a.last_token_pos, b.last_token_pos = [4, 1, 9], [5, 12]     # position 1 is in a's prompt
     for s in (a, b):
         s.processed_steps = 8                                       # refresh step (multiple of 4)
-    r.prepare_sparse([a, b])
+    r.prepare_sparse([a, b])(r.staging.flush())
     ctx = get_context()
     assert ctx.cu_seqlens_q_cpu == [0, 11, 24] and ctx.idx_salient_row_k is None
     assert ctx.idx_salient_row.tolist() == [4, 9, 11 + 5, 11 + 12]
     assert ctx.cu_salientlens.tolist() == [0, 2, 4] and ctx.max_salientlen == 2
     for s in (a, b):
         s.processed_steps = 6                                       # Q-pruned step
-    r.prepare_sparse([a, b])
+    ids, pos = r.prepare_sparse([a, b])(r.staging.flush())
+    assert pos.tolist() == list(range(3, 11)) + list(range(5, 13)) and ids.dtype == torch.long
     ctx = get_context()
     assert ctx.cu_seqlens_q_cpu == [0, 8, 16] and ctx.cu_promptlens.tolist() == [0, 3, 8]
     assert ctx.idx_salient_row.tolist() == [1, 6, 8 + 0, 8 + 7]
     assert ctx.idx_salient_row_k.tolist() == [4, 9, 11 + 5, 11 + 12]
+    assert ctx.cu_seqlens_k.dtype == torch.int32 and ctx.idx_salient_row.dtype == torch.long
     reset_context()
 
 

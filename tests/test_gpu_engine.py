@@ -51,3 +51,28 @@ def test_generate_confidence_threshold_and_batches(dev):
     for o in out:
         assert eng.config.mask_id not in o["token_ids"]
     assert eng.execution_stats["full_forwards"] >= 2
+
+
+def test_host_staging_single_transfer(dev):
+    """The step metadata travels in one pinned transfer; every field comes back with its dtype and
+    values, also when the pinned buffer is reused by the next step while the device block of the
+    previous one is still referenced."""
+    from dyllm_amd.engine.model_runner import _HostStaging
+
+    st = _HostStaging(torch.device(dev))
+    rng = torch.Generator().manual_seed(3)
+    kept = []
+    for step in range(3):
+        fields = {"a": (torch.randint(-2**40, 2**40, (1000 + step,), generator=rng), torch.long),
+                  "b": (torch.randint(-2**30, 2**30, (7,), generator=rng).to(torch.int32), torch.int32),
+                  "e": (torch.zeros(0, dtype=torch.long), torch.long),
+                  "c": (torch.randn(33, generator=rng), torch.float32)}
+        for name, (t, dt) in fields.items():
+            st.add(name, t.tolist(), dt)
+        out = st.flush()
+        kept.append((fields, out))
+    torch.cuda.synchronize()
+    for fields, out in kept:
+        for name, (t, dt) in fields.items():
+            assert out[name].dtype == dt and out[name].device.type == "cuda"
+            assert torch.equal(out[name].cpu(), t.to(dt)), name
