@@ -646,8 +646,15 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
   }
 }
 
+// The 2-wavefront column-sparse kernel (small grids only) holds the two-pass state and the larger
+// per-thread staging of its 128-thread workgroup in 1 wavefront per SIMD (its accumulators go to
+// AGPRs); it measured within ±5 % of the single-pass variant, which spills at 2 per SIMD.
 template <AttnMode MODE, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_kernel(AttnArgs a) {
+constexpr int kAttnWaves = (MODE == AttnMode::ColSparse && NW == 2) ? 1 : 2;
+
+template <AttnMode MODE, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(kAttnWaves<MODE, NW>, 2))) void
+attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
   if constexpr (MODE == AttnMode::ColSparse) {
