@@ -233,33 +233,6 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     // sequence, P = bf16(exp2(S*c2 - m_kb*c2)) -- the identical bf16 values the single pass
     // feeds its PV -- and O += P dV with the accumulator rescaled from the previous group's
     // block max to this one's (the product of the per-block rescales in one factor).
-    if (w == 0) {
-      // salient-key groups of this sequence from the per-block key bits
-      uint64_t word = 0;
-      int grp = 0;
-      if (lane < nkb) {
-        word = a.kmask[int64_t(b) * a.nblk + lane];
-        if (lane == nkb - 1 && (Lk & (kBK - 1))) word &= (1ull << (Lk & (kBK - 1))) - 1;   // keys < Lk only
-        grp = (__popcll(word) + 15) >> 4;
-      }
-      int inc = grp;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int v = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += v;
-      }
-      const int g0 = inc - grp;
-      if (lane == 63) *sp.ngrp = inc;
-      int n = 0;
-      while (word) {
-        sp.keys[g0 * 16 + n] = int16_t(lane * kBK + __builtin_ctzll(word));
-        word &= word - 1;
-        ++n;
-      }
-      for (; n < grp * 16; ++n) sp.keys[g0 * 16 + n] = -1;
-      for (int j = 0; j < grp; ++j) sp.gblk[g0 + j] = uint8_t(lane);
-    }
-    __syncthreads();
     float* m_tab = sp.m + w * (kMaxBlk2 * 32) + ql;
     auto qk = [&](f32x16_t (&sa)[2], const uint16_t* kt) {
 #pragma unroll
@@ -296,12 +269,36 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     // K double-buffered (the V^T tile, idle in this pass, holds the odd blocks): block kb+1 is
     // staged while block kb is scored, one barrier per block
     static_assert(kBK * kKStride <= kD * kVStride, "V^T tile too small for a K tile");
-    if (nkb > 0) {
-      fetch_k(0);
-      stage_k(k_lds);
+    if (nkb > 0) fetch_k(0);   // in flight while the group list is built
+    if (w == 0) {
+      // salient-key groups of this sequence from the per-block key bits
+      uint64_t word = 0;
+      int grp = 0;
+      if (lane < nkb) {
+        word = a.kmask[int64_t(b) * a.nblk + lane];
+        if (lane == nkb - 1 && (Lk & (kBK - 1))) word &= (1ull << (Lk & (kBK - 1))) - 1;   // keys < Lk only
+        grp = (__popcll(word) + 15) >> 4;
+      }
+      int inc = grp;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += v;
+      }
+      const int g0 = inc - grp;
+      if (lane == 63) *sp.ngrp = inc;
+      int n = 0;
+      while (word) {
+        sp.keys[g0 * 16 + n] = int16_t(lane * kBK + __builtin_ctzll(word));
+        word &= word - 1;
+        ++n;
+      }
+      for (; n < grp * 16; ++n) sp.keys[g0 * 16 + n] = -1;
+      for (int j = 0; j < grp; ++j) sp.gblk[g0 + j] = uint8_t(lane);
     }
+    if (nkb > 0) stage_k(k_lds);
     if (nkb > 1) fetch_k(1);
-    __syncthreads();
+    __syncthreads();   // the group list and K tile 0 are complete
     for (int kb = 0; kb < nkb; ++kb) {
       const int key0 = kb * kBK;
       f32x16_t sa[2];
