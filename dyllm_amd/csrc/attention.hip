@@ -37,11 +37,15 @@ constexpr int kVStride = kBK + 12;   // V^T tile row stride (elements): 152 B, c
 // Two-pass column-sparse path (sequences of at most kMaxBlk2 key blocks): LDS it needs beyond
 // the K / V^T tiles.
 constexpr int kMaxBlk2 = 64;
+#ifndef DYLLM_P1_PAIR
+#define DYLLM_P1_PAIR 1
+#endif
 struct ColSparseLds {
   float* m;          // [NW][kMaxBlk2][32] running max of each query row after each key block
   int16_t* keys;     // [kMaxBlk2 * kBK] salient keys in 16-slot groups, -1 = padding
   uint8_t* gblk;     // [4 * kMaxBlk2] key block of each group
   int* ngrp;         // number of groups
+  float* xch;        // [NW][96] pass-1 partials exchanged between the waves of a pair (64 sums, 32 maxima)
 };
 
 union Pack8 {
@@ -296,6 +300,125 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       for (; n < grp * 16; ++n) sp.keys[g0 * 16 + n] = -1;
       for (int j = 0; j < grp; ++j) sp.gblk[g0 + j] = uint8_t(lane);
     }
+#if DYLLM_P1_PAIR
+    // Wavefronts pair up (w, w^1) over the pair's two 32-row groups, and wave w scores the key
+    // blocks of parity w & 1 for both groups: every K fragment read from LDS feeds two MFMAs (half
+    // the LDS reads per row, four independent accumulation chains). Each wave keeps a partial
+    // (max, sum) per group over its blocks and records each block's own maximum; afterwards the
+    // partner's partial is merged through LDS (fp32-rounding-level difference from the
+    // sequential sum) and the block maxima are turned into the exact running maxima pass 2 needs.
+    // K: blocks 2j and 2j+1 are staged together (K tile and the idle V^T tile), one barrier each.
+    const int pg = w ^ 1, par = w & 1;
+    bf16x8_t qf2[8];   // the partner group's Q fragments
+    {
+      const int prow = row_beg + tile * BQ + pg * 32 + ql;
+      const uint16_t* qp = a.Q + int64_t(prow) * ldq + head * kD + half * 8;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        Pack8 p;
+        p.q = prow < row_end ? *reinterpret_cast<const uint4*>(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+        qf2[s] = p.v;
+      }
+    }
+    float* const mt_par = sp.m + pg * (kMaxBlk2 * 32) + ql;
+    float pm[2] = {-FLT_MAX, -FLT_MAX}, pl[2] = {0.f, 0.f};   // [own group, partner group]
+    uint4 kreg1[KCH];
+    auto fetch_k1 = [&](int kb) {
+      const int key0 = kb * kBK;
+#pragma unroll
+      for (int it = 0; it < KCH; ++it) {
+        const int c = tid + NT * it;
+        const int key = c >> 4, dc = c & 15;
+        kreg1[it] = (key0 + key < Lk) ? *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8)
+                                      : make_uint4(0, 0, 0, 0);
+      }
+    };
+    auto stage_k1 = [&]() {
+#pragma unroll
+      for (int it = 0; it < KCH; ++it) {
+        const int c = tid + NT * it;
+        const int key = c >> 4, dc = c & 15;
+        *reinterpret_cast<uint4*>(&vt_lds[key * kKStride + dc * 8]) = kreg1[it];
+      }
+    };
+    if (nkb > 1) fetch_k1(1);
+    for (int j = 0; 2 * j < nkb; ++j) {
+      stage_k(k_lds);
+      if (2 * j + 1 < nkb) stage_k1();
+      __syncthreads();
+      if (2 * j + 2 < nkb) fetch_k(2 * j + 2);
+      if (2 * j + 3 < nkb) fetch_k1(2 * j + 3);
+      const int kb = 2 * j + par;
+      if (kb < nkb) {
+        const uint16_t* kt = par ? vt_lds : k_lds;
+        f32x16_t sa[2][2];   // [group][32-key half]
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sa[0][t][r] = sa[1][t][r] = 0.f;
+#pragma unroll
+          for (int s = 0; s < 8; ++s) {
+            const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(&kt[(t * 32 + ql) * kKStride + 16 * s + half * 8]);
+            sa[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sa[0][t], 0, 0, 0);
+            sa[1][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf2[s], sa[1][t], 0, 0, 0);
+          }
+        }
+        const int key0 = kb * kBK;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          if (key0 + kBK > Lk) {  // ragged last block only
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int key = key0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                if (key >= Lk) sa[g][t][r] = -FLT_MAX;
+              }
+          }
+          float bm = sa[g][0][0];
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sa[g][t][r]);
+          bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+          const float m_new = fmaxf(pm[g], bm);
+          const float rescale = __builtin_amdgcn_exp2f((pm[g] - m_new) * c2);
+          const float m2 = m_new * c2;
+          pm[g] = m_new;
+          float psum = 0.f;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) {
+              const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[g][t][r], c2, -m2));
+              const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[g][t][r + 1], c2, -m2));
+              psum += e0 + e1;
+            }
+          pl[g] = pl[g] * rescale + psum;
+          if (half == 0) (g == 0 ? m_tab : mt_par)[kb * 32] = bm;   // the block's own maximum
+        }
+      }
+      __syncthreads();
+    }
+    // merge the partner's partial for this wave's group; running maxima of the group's blocks
+    // (the maximum is shared by both half-waves, the sum is per lane: each half holds other keys)
+    sp.xch[pg * 96 + lane] = pl[1];
+    if (half == 0) sp.xch[pg * 96 + 64 + ql] = pm[1];
+    __syncthreads();
+    {
+      const float mb = sp.xch[w * 96 + 64 + ql], lb = sp.xch[w * 96 + lane];
+      m_run = fmaxf(pm[0], mb);
+      l_run = pl[0] * __builtin_amdgcn_exp2f((pm[0] - m_run) * c2) + lb * __builtin_amdgcn_exp2f((mb - m_run) * c2);
+      if (half == 0) {
+        float run = -FLT_MAX;
+        for (int kb = 0; kb < nkb; ++kb) {
+          run = fmaxf(run, m_tab[kb * 32]);
+          m_tab[kb * 32] = run;
+        }
+      }
+    }
+    __syncthreads();
+#else
     if (nkb > 0) stage_k(k_lds);
     if (nkb > 1) fetch_k(1);
     __syncthreads();   // the group list and K tile 0 are complete
@@ -337,6 +460,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       if (half == 0) m_tab[kb * 32] = m_new;
       __syncthreads();
     }
+#endif
     // (the last barrier also ends pass 1's reads of both tiles before pass 2 restages them)
 
     // ---- pass 2 ----
@@ -659,8 +783,9 @@ attention_kernel(AttnArgs a) {
     __shared__ int16_t key_lds[kMaxBlk2 * kBK];
     __shared__ uint8_t gblk_lds[4 * kMaxBlk2];
     __shared__ int ngrp_lds;
+    __shared__ float xch_lds[NW * 96];
     attention_tile<MODE, NW>(a, xcd_remap(blockIdx.x, gridDim.x), k_lds, vt_lds,
-                             ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds});
+                             ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds, xch_lds});
   } else {
     attention_tile<MODE, NW>(a, xcd_remap(blockIdx.x, gridDim.x), k_lds, vt_lds, ColSparseLds{});
   }
@@ -679,13 +804,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   __shared__ int16_t key_lds[kMaxBlk2 * kBK];
   __shared__ uint8_t gblk_lds[4 * kMaxBlk2];
   __shared__ int ngrp_lds;
+  __shared__ float xch_lds[NW * 96];
   const int wg = blockIdx.x;
   if (wg < n_rs_pad) {
     const int t = xcd_remap(wg, n_rs_pad);
     if (t < n_rs) attention_tile<AttnMode::RowSparse, NW>(rs, t, k_lds, vt_lds, ColSparseLds{});
   } else {
     attention_tile<AttnMode::ColSparse, NW>(cs, xcd_remap(wg - n_rs_pad, int(gridDim.x) - n_rs_pad), k_lds, vt_lds,
-                                            ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds});
+                                            ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds, xch_lds});
   }
 }
 
