@@ -370,7 +370,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU; the hot path is not sharded across GPUs "
-              "(see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+              "(sequences would split across data-parallel ranks with no exchange). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch

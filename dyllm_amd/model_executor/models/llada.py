@@ -2,9 +2,10 @@
 (dyllm/model_executor/models/llada.py:26-260), random-initialised from shape fields only.
 
 The hot path (attention saliency / compaction / gathered SwiGLU + scatter) runs on the HIP
-kernels; the dense ops on either side of it (embeddings, RMSNorm, RoPE, the Q/K/V/O
-projections, the LM head) use PyTorch-ROCm, as SURVEY's scope table places them outside the
-path. MLP and Dream/MoE variants share this structure.
+kernels, as do the salient-row K/V projection with its RoPE / K-cache epilogue, the query RoPE
+and the decoder-layer RMSNorms; the remaining dense ops on either side of the path (embeddings,
+the Q and O projections, the LM head) use PyTorch-ROCm. MLP and Dream/MoE variants share this
+structure.
 """
 from __future__ import annotations
 
