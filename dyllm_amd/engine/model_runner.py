@@ -104,12 +104,6 @@ class ModelRunner:
         self.sampler = DreamSampler("entropy") if hf.model_type == "Dream" else LLaDASampler("confidence")
         self.staging = _HostStaging(self.device)
 
-    def _dev(self, data, dtype):
-        t = torch.tensor(data, dtype=dtype)
-        if self.device.type == "cuda":
-            return t.pin_memory().to(self.device, non_blocking=True)
-        return t.to(self.device)
-
     # -- batch preparation -------------------------------------------------------------
     def prepare_full(self, seqs: List[Sequence]):
         md = get_metadata()
