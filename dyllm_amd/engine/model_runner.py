@@ -107,14 +107,14 @@ class ModelRunner:
     # -- batch preparation -------------------------------------------------------------
     def prepare_full(self, seqs: List[Sequence]):
         md = get_metadata()
-        input_ids, positions, cu, lens, ids = [], [], [0], [], []
+        cu, lens, ids = [0], [], []
         for seq in seqs:
             L = len(seq)
-            input_ids.extend(seq.token_ids)
-            positions.extend(range(L))
             cu.append(cu[-1] + L)
             lens.append(L)
             ids.append(seq.seq_id)
+        input_ids = np.concatenate([seq.token_arr for seq in seqs])
+        positions = np.concatenate([np.arange(L, dtype=np.int64) for L in lens])
         i32, i64 = torch.int32, torch.long
         st = self.staging
         st.add("cu", cu, i32)
@@ -144,14 +144,14 @@ class ModelRunner:
             start = seq.answer_start
             kept = [p for p in seq.last_token_pos if p >= start]
             if pruned:
-                input_ids.extend(seq.token_ids[start:])
-                positions.extend(range(start, L))
+                input_ids.append(seq.token_arr[start:])
+                positions.append(np.arange(start, L, dtype=np.int64))
                 idx_q.extend(p - seq.num_prompt_tokens + cu_q[-1] for p in kept)
                 idx_k.extend(p + cu_k[-1] for p in kept)
                 lq = L - start
             else:
-                input_ids.extend(seq.token_ids)
-                positions.extend(range(L))
+                input_ids.append(seq.token_arr)
+                positions.append(np.arange(L, dtype=np.int64))
                 idx_q.extend(p + cu_q[-1] for p in kept)
                 lq = L
             positions_k.extend(kept)
@@ -167,7 +167,8 @@ class ModelRunner:
         for name, data, dt in (("cu_s", cu_s, i32), ("ids", ids, i64), ("idx_q", idx_q, i64), ("cu_q", cu_q, i32),
                                ("cu_k", cu_k, i32), ("cu_p", cu_p, i32), ("idx_upd", idx_upd, i32),
                                ("idx_k", idx_k, i64), ("lens", lens, i32), ("positions_k", positions_k, i64),
-                               ("input_ids", input_ids, i64), ("positions", positions, i64)):
+                               ("input_ids", np.concatenate(input_ids), i64),
+                               ("positions", np.concatenate(positions), i64)):
             st.add(name, data, dt)
 
         def finish(d):
@@ -193,20 +194,21 @@ class ModelRunner:
         has_t = has_p = has_k = has_thr = False
         for seq in seqs:
             limit = min(len(seq), seq.block_size * (seq.block_idx + 1) + seq.num_prompt_tokens)
-            mpos = [i for i in range(limit) if seq.token_ids[i] == mask]
+            mpos = np.flatnonzero(seq.token_arr[:limit] == mask)
             off = seq.answer_start if pruned else 0
             if pruned:
-                mpos = [p - off for p in mpos if p >= off]
-            rels.extend(mpos)
+                mpos = mpos[mpos >= off] - off
+            n = len(mpos)
+            rels.append(mpos)
             offsets.append(off)
-            counts.append(len(mpos))
+            counts.append(n)
             t_on = seq.temperature is not None and seq.temperature > 1e-6
             has_t |= t_on
             # sequences without a temperature are left unscaled in a batch that has one
-            temps.extend([seq.temperature if t_on else 1.0] * len(mpos))
+            temps.append(np.full(n, seq.temperature if t_on else 1.0))
             transfers.append(1 if seq.confidence_threshold is not None else seq.num_transfer_tokens)
-            top_ps.extend([seq.top_p if seq.top_p is not None else 1.0] * len(mpos))
-            top_ks.extend([seq.top_k if seq.top_k is not None else 1 << 30] * len(mpos))
+            top_ps.append(np.full(n, seq.top_p if seq.top_p is not None else 1.0))
+            top_ks.append(np.full(n, seq.top_k if seq.top_k is not None else 1 << 30))
             thrs.append(seq.confidence_threshold if seq.confidence_threshold is not None else float("inf"))
             has_p |= seq.top_p is not None
             has_k |= seq.top_k is not None
@@ -218,14 +220,14 @@ class ModelRunner:
         f32, i32, i64 = torch.float32, torch.int32, torch.long
         st = self.staging
         if has_t:
-            st.add("s_temps", temps, f32)
+            st.add("s_temps", np.concatenate(temps), f32)
         if has_k:
-            st.add("s_top_ks", top_ks, i32)
+            st.add("s_top_ks", np.concatenate(top_ks), i32)
         if has_p:
-            st.add("s_top_ps", top_ps, f32)
+            st.add("s_top_ps", np.concatenate(top_ps), f32)
         if has_thr:
             st.add("s_thrs", thrs, f32)
-        st.add("s_rels", rels, i64)
+        st.add("s_rels", np.concatenate(rels), i64)
         st.add("s_offsets", offsets, i64)
         st.add("s_cu", cu, i32)
         st.add("s_transfers", transfers, i32)

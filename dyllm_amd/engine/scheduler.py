@@ -78,7 +78,7 @@ class Scheduler:
 
     def eos_and_done(self, seq: Sequence, pos: int) -> bool:
         """True when no mask token precedes ``pos`` (scheduler.py:83-87)."""
-        return all(seq[p] != self.mask for p in range(pos))
+        return not bool((seq.token_arr[:pos] == self.mask).any())
 
     def _finish(self, seq: Sequence, finished: List[int]):
         seq.status = SequenceStatus.FINISHED

@@ -6,6 +6,8 @@ from enum import Enum, auto
 from itertools import count
 from typing import List
 
+import numpy as np
+
 from ..sampling_params import SamplingParams
 
 
@@ -23,6 +25,8 @@ class Sequence:
         self.seq_id = next(Sequence.counter)
         self.status = SequenceStatus.FULL
         self.token_ids = list(token_ids)
+        # int64 copy of token_ids for the per-step index building (update_token writes both)
+        self.token_arr = np.asarray(self.token_ids, dtype=np.int64)
         self.mask_id = sp.mask_id
         # tokens written by the last step and their positions: the first layer's salient rows
         # of the next sparse step (model_runner.py:207-214)
@@ -81,6 +85,7 @@ class Sequence:
             if self.token_ids[p] == self.mask_id and t != self.mask_id:
                 self.num_tokens += 1
             self.token_ids[p] = t
+            self.token_arr[p] = t
         self.last_tokens = list(token_id)
         self.last_token_pos = list(pos)
 
