@@ -150,3 +150,33 @@ def test_fused_ffn_scatter_matches_reference_mlp(dev):
     # untouched rows are bit-identical to the previous step's cache
     keep = np.setdiff1d(np.arange(B * R), idx_q)
     assert torch.equal(out[torch.from_numpy(keep)], want[torch.from_numpy(keep)])
+
+
+@pytest.mark.parametrize("L", [100, 700])
+def test_mlp_full_step_dense_rows(dev, L):
+    """Full-step FFN over all rows (3 x 100 and 3 x 700 rows) through LLaDAMLP.forward: matches
+    the fp32 oracle when read back from the FFN cache, as the full step returns it."""
+    from dyllm_amd.model_executor.models.llada import LLaDAMLP
+    from dyllm_amd.utils.context import set_context
+    from dyllm_amd.utils.metadata import get_metadata
+
+    print(f"[mlp full] rows={3 * L}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(5)
+    B, hid, inter = 3, 256, 384
+    T = B * L
+    md = get_metadata()
+    md.running_seqs = [0, 1, 2]
+    md.running_seqs_tensor = torch.arange(3, device=dev)
+    md.finished_seqs = []
+    cu = [i * L for i in range(B + 1)]
+    i32 = lambda a: torch.tensor(a, dtype=torch.int32, device=dev)
+    set_context(True, cu_seqlens_q=i32(cu), cu_seqlens_q_cpu=cu, cu_seqlens_k=i32(cu), cu_seqlens_k_cpu=cu,
+                max_seqlen_q=L, max_seqlen_k=L, context_lens_cpu=[L] * B, total_seqlen=T, total_seqlen_k=T)
+    mlp = LLaDAMLP(hid, inter, device=dev, gen=g)
+    with torch.no_grad():
+        mlp.gate_up_proj.data = (torch.randn(2 * inter, hid, device=dev, generator=g) * hid ** -0.5).to(BF)
+        mlp.down_proj.data = (torch.randn(hid, inter, device=dev, generator=g) * inter ** -0.5).to(BF)
+    x = torch.randn(T, hid, device=dev, generator=g).to(BF)
+    y = mlp(x).cpu()
+    want = ref.swiglu_ffn(x.cpu(), mlp.gate_up_proj.cpu(), mlp.down_proj.cpu()).to(BF)
+    assert_bf16_close(y, want, what="full-step FFN")
