@@ -208,6 +208,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     if (kt + 2 < nk) stage_w(kt + 2, wnext2);
     fload(As, Ws, 0, wf0, af0);
     __builtin_amdgcn_sched_barrier(0);
+    // raised wave priority from the first MFMA of the slice to its end: the SIMD's arbiter then
+    // favours a wave in its MFMA stretch over its partner wave issuing the next slice's loads
+    __builtin_amdgcn_s_setprio(1);
     fload(As, Ws, 1, wf1, af1);
     mma(wf0, af0);
     interleave();
@@ -221,6 +224,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     interleave();
     __builtin_amdgcn_sched_barrier(0);
     mma(wf1, af1);
+    __builtin_amdgcn_s_setprio(0);
     // this wave's LDS reads of the current slice are done before any wave refills its buffers
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (kt + 2 < nk) {
