@@ -28,6 +28,13 @@ index work). Each function cites the reference file:line whose semantics it rest
                                    the fused form equals rms_norm of the fp32 sum (zero residual:
                                    identical to rms_norm) and a per-row loop.
 * ``salient_kv_project``        -- composition of the above with a per-row loop linear.
+* ``sparse_attention_step``     -- every queried row equals exact SDPA attn(Q, K, V_new) to bf16
+                                   rounding, the V cache changes exactly at the salient K rows,
+                                   the next set equals {cos(exact, C_old) < tau}, each K-space
+                                   index is the same token as its Q-space index; composition
+                                   mistakes (o_sal from the old V cache, dV at Q rows, a wrong
+                                   prompt offset) are shown to fail; and the config-0 known
+                                   answer (salient set == perturbed rows) through the whole step.
 """
 from __future__ import annotations
 

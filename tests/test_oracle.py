@@ -333,3 +333,193 @@ def test_add_rms_norm_consistency_and_loop():
         assert torch.equal(ro[i], s.float().to(BF))
         n = (s / torch.sqrt((s * s).mean() + 1e-6)).float().to(BF).double() * w.double()
         assert (y[i].double() - n).abs().max() <= 2 ** -7 * n.abs().max()
+
+
+# ---------------------------------------------------------------------------
+# sparse_attention_step (attention.py:64-178), pinned end to end by what the mathematics fixes
+# ---------------------------------------------------------------------------
+def _dense_attn(q, k, v, cu_q, cu_k):
+    """Exact fp32 softmax(QK^T/sqrt(D))V per sequence via torch SDPA (GQA expanded); the
+    textbook operation the whole sparse step approximates."""
+    Tq, H, D = q.shape
+    g = H // k.shape[1]
+    out = torch.zeros(Tq, H, D)
+    for b in range(len(cu_q) - 1):
+        qs, qe, ks, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        if qe == qs:
+            continue
+        qb = q[qs:qe].float().transpose(0, 1)
+        kb = k[ks:ke].float().transpose(0, 1).repeat_interleave(g, 0)
+        vb = v[ks:ke].float().transpose(0, 1).repeat_interleave(g, 0)
+        out[qs:qe] = F.scaled_dot_product_attention(qb, kb, vb).transpose(0, 1)
+    return out
+
+
+def _step_case(seed, lens, q_pruned, n_sal_per_seq, H=4, Hkv=2, D=128, sigma=1.0):
+    """Ragged batch: lens = [(prompt, response)]. Q-pruned: the queried rows are the
+    responses; refresh: every row. The previous salient set is drawn per sequence from the
+    response rows; its V rows get a fresh value (v_new)."""
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    cu_k = np.concatenate([[0], np.cumsum([p + r for p, r in lens])]).astype(np.int64)
+    cu_p = np.concatenate([[0], np.cumsum([p for p, _ in lens])]).astype(np.int64)
+    cu_q = (np.concatenate([[0], np.cumsum([r for _, r in lens])]) if q_pruned else cu_k).astype(np.int64)
+    Tq, Tk = int(cu_q[-1]), int(cu_k[-1])
+    q = torch.randn(Tq, H, D, generator=g).to(BF)
+    k = torch.randn(Tk, Hkv, D, generator=g).to(BF)
+    v_old = torch.randn(Tk, Hkv, D, generator=g).to(BF)
+    sidx, kidx, cu_s = [], [], [0]
+    for b, (p, r) in enumerate(lens):
+        sel = np.sort(rng.choice(r, size=min(r, n_sal_per_seq[b]), replace=False))
+        sidx += ((cu_q[b] + sel) if q_pruned else (cu_k[b] + p + sel)).tolist()
+        kidx += (cu_k[b] + p + sel).tolist()
+        cu_s.append(len(sidx))
+    sidx, kidx, cu_s = (np.asarray(a, np.int64) for a in (sidx, kidx, cu_s))
+    v_new = (v_old[kidx].float() + sigma * torch.randn(len(kidx), Hkv, D, generator=g)).to(BF)
+    return dict(q=q, k=k, v_old=v_old, v_new=v_new, cu_q=cu_q, cu_k=cu_k, cu_p=cu_p, sidx=sidx, kidx=kidx,
+                cu_s=cu_s, q_pruned=q_pruned)
+
+
+def _run_step(c, c_old, tau=0.99):
+    return ref.sparse_attention_step(c["q"], c["k"], c["v_new"], c["v_old"], c_old, c["cu_q"], c["cu_k"], c["cu_s"],
+                                     c["sidx"], c["kidx"] if c["q_pruned"] else None, c["cu_p"], tau)
+
+
+def _check_step(c, c_old, res, tau=0.99):
+    """The properties a correct sparse step has, independent of how it is composed:
+    (1) the V cache changes exactly at the salient K rows and holds v_new there;
+    (2) every queried row's new context equals exact attn(Q, K, V_new) to bf16 rounding --
+        salient rows because they are recomputed, the others by linearity of P.V;
+    (3) the next salient set is {rows : cos(new, C_old) < tau} of those exact rows (outside
+        the tau band), ascending, with cu_salientlens its per-sequence split;
+    (4) Q-pruned: idx_salient_row_k is each index plus its sequence's prompt length
+        (a per-row loop); refresh: it is None."""
+    q, k, cu_q, cu_k = c["q"], c["k"], c["cu_q"], c["cu_k"]
+    v_upd = c["v_old"].clone()
+    v_upd[torch.as_tensor(c["kidx"])] = c["v_new"]
+    assert torch.equal(res["v_cache"], v_upd), "V cache"
+    changed = (res["v_cache"] != c["v_old"]).flatten(1).any(1).nonzero().squeeze(-1).numpy()
+    assert set(changed.tolist()) <= set(c["kidx"].tolist())
+    exact = _dense_attn(q, k, v_upd, cu_q, cu_k)
+    sal = torch.as_tensor(c["sidx"])
+    from tests._tol import assert_bf16_close
+    # against the exact product the step carries two bf16 roundings (P before P.V and the
+    # output) -> mean relative 3e-3 here; every composition mistake below moves rows by >10%
+    assert_bf16_close(res["new_c"][sal], exact[sal], mean_rel=3e-3, what="salient rows")
+    keep = torch.ones(len(q), dtype=torch.bool)
+    keep[sal] = False
+    assert_bf16_close(res["new_c"][keep], exact[keep], mean_rel=3e-3, what="non-salient rows")
+    cos = F.cosine_similarity(exact.flatten(1).double(), c_old.float().flatten(1).double(), dim=-1).numpy()
+    want = cos < tau
+    band = np.abs(cos - tau) <= 1e-4  # fp32 paths vs the exact cosine: stay clear of the edge
+    got = res["mask"].numpy()
+    assert ((got == want) | band).all(), "salient set"
+    idxs = res["idx_salient_row"]
+    assert np.array_equal(idxs, np.nonzero(got)[0]) and np.all(np.diff(idxs) > 0)
+    for b in range(len(cu_q) - 1):
+        lo, hi = res["cu_salientlens"][b], res["cu_salientlens"][b + 1]
+        assert np.all((idxs[lo:hi] >= cu_q[b]) & (idxs[lo:hi] < cu_q[b + 1]))
+        assert hi - lo == got[cu_q[b]:cu_q[b + 1]].sum()
+    if c["q_pruned"]:
+        # the K-space row of each salient query row is the same token: same sequence, and the
+        # same offset into its response (K rows of a sequence are prompt then response)
+        got_k = np.asarray(res["idx_salient_row_k"])
+        assert got_k.shape == idxs.shape
+        for i, j in zip(idxs, got_k):
+            b = int(np.searchsorted(cu_q, i, side="right")) - 1
+            assert cu_k[b] <= j < cu_k[b + 1]
+            plen = (cu_k[b + 1] - cu_k[b]) - (cu_q[b + 1] - cu_q[b])
+            assert j - cu_k[b] - plen == i - cu_q[b]
+    else:
+        assert res["idx_salient_row_k"] is None
+
+
+STEP_CASES = [
+    ("qpruned_ragged", [(40, 96), (16, 48), (64, 130)], True, [9, 5, 20]),
+    ("refresh_ragged", [(40, 96), (16, 48), (64, 130)], False, [9, 5, 20]),
+    ("qpruned_empty_seq", [(32, 64), (8, 40)], True, [0, 6]),
+    ("qpruned_no_salient", [(32, 64), (8, 40)], True, [0, 0]),
+    ("refresh_all_salient", [(16, 24), (8, 16)], False, [24, 16]),
+    ("qpruned_single_rows", [(20, 33), (5, 1)], True, [1, 1]),
+]
+
+
+@pytest.mark.parametrize("name,lens,q_pruned,nsal", STEP_CASES, ids=[s[0] for s in STEP_CASES])
+def test_sparse_step_pinned_by_exact_attention(name, lens, q_pruned, nsal):
+    c = _step_case(11, lens, q_pruned, nsal)
+    # C_old: the exact fp32 context of the previous step (attn with the pre-update V)
+    c_old = _dense_attn(c["q"], c["k"], c["v_old"], c["cu_q"], c["cu_k"])
+    res = _run_step(c, c_old)
+    _check_step(c, c_old, res)
+    if nsal and sum(nsal):
+        assert res["mask"].any()  # sigma = 1 on V rows moves the contexts past tau somewhere
+
+
+def _step_mutant(c, c_old, kind, tau=0.99):
+    """Plausible composition mistakes of attention.py:64-178, built from the oracle's own
+    pieces: the pins above must reject each of them."""
+    q, k = c["q"], c["k"]
+    sidx = torch.as_tensor(c["sidx"])
+    kidx = torch.as_tensor(c["kidx"] if c["q_pruned"] else c["sidx"])
+    if kind == "dv_at_q_rows":  # Q-pruned: scatter dV at the Q-space indices
+        kidx_dv = sidx
+    else:
+        kidx_dv = kidx
+    v_cache = c["v_old"].clone()
+    dv = ref.bf16_round(c["v_new"].float() - v_cache[kidx].float())
+    v_cache[kidx] = c["v_new"]
+    v_for_osal = c["v_old"] if kind == "o_sal_old_cache" else v_cache
+    o_sal = ref.flash_attn_varlen(q[sidx], k, v_for_osal, c["cu_s"], c["cu_k"])
+    vd = torch.zeros_like(k, dtype=torch.float32)
+    vd[kidx_dv] = dv
+    newc, stats, mask = ref.attention_sparse_varlen(q, k, vd.to(BF), c_old, o_sal, c["cu_q"], c["cu_k"], sidx, tau)
+    idxs, cu_sal = ref.compact(mask.numpy(), c["cu_q"])
+    if kind == "offset_own_prompt":  # fused offset with the sequence's start instead of its end
+        seg = np.searchsorted(cu_sal[1:], np.arange(len(idxs)), side="right")
+        idx_k = idxs + c["cu_p"][seg]
+    else:
+        idx_k = ref.fused_offset(idxs, c["cu_p"], cu_sal) if c["q_pruned"] else None
+    return dict(new_c=newc, v_cache=v_cache, stats=stats, mask=mask, idx_salient_row=idxs, cu_salientlens=cu_sal,
+                idx_salient_row_k=idx_k)
+
+
+@pytest.mark.parametrize("kind", ["o_sal_old_cache", "dv_at_q_rows", "offset_own_prompt"])
+def test_sparse_step_pins_reject_composition_mistakes(kind):
+    c = _step_case(12, [(40, 96), (16, 48), (64, 130)], True, [9, 5, 20])
+    c_old = _dense_attn(c["q"], c["k"], c["v_old"], c["cu_q"], c["cu_k"])
+    _check_step(c, c_old, _step_mutant(c, c_old, "none"))  # the faithful composition passes
+    with pytest.raises(AssertionError):
+        _check_step(c, c_old, _step_mutant(c, c_old, kind))
+
+
+def test_config0_known_answer_through_the_step():
+    """Config 0 (B=1, 128 prompt + 384 response, 32 heads x 128, tau = 0.99) run through the
+    whole Q-pruned step. Each response query is a scaled copy of its own key row, so its
+    attention is one-hot on that row to within e^-30; the previous salient set holds 20% of the
+    response rows, and the V rows of half of them (10% of the responses) move by
+    sigma = 0.5 x row RMS while the rest keep their value. Known answer: the new salient set
+    is exactly the perturbed rows (cos ~ 1/sqrt(1.25) = 0.894), and its K-space rows are those
+    rows + 128."""
+    P, R, H, D = 128, 384, 32, 128
+    g = torch.Generator().manual_seed(2024)
+    rng = np.random.default_rng(2024)
+    k = torch.randn(P + R, H, D, generator=g).to(BF)
+    q = (4.0 * k[P:].float()).to(BF)
+    v_old = torch.randn(P + R, H, D, generator=g).to(BF)
+    sal = np.sort(rng.choice(R, size=77, replace=False))
+    pert = np.sort(rng.choice(sal, size=38, replace=False))
+    v_new = v_old[P + sal].float()
+    rms = v_new.flatten(1).pow(2).mean(-1).sqrt()[:, None, None]
+    is_p = torch.as_tensor(np.isin(sal, pert))
+    v_new[is_p] += 0.5 * rms[is_p] * torch.randn(int(is_p.sum()), H, D, generator=g)
+    v_new = v_new.to(BF)
+    cu_q = np.array([0, R]); cu_k = np.array([0, P + R]); cu_p = np.array([0, P])
+    c_old = ref.flash_attn_varlen(q, k, v_old, cu_q, cu_k)  # the bf16 context cache
+    res = ref.sparse_attention_step(q, k, v_new, v_old, c_old, cu_q, cu_k, np.array([0, len(sal)]), sal, P + sal,
+                                    cu_p, 0.99)
+    assert res["idx_salient_row"].tolist() == pert.tolist()
+    assert res["cu_salientlens"].tolist() == [0, len(pert)]
+    assert res["idx_salient_row_k"].tolist() == (P + pert).tolist()
+    cos = ref.cosine_from_stats(res["stats"]).numpy()
+    assert np.all(np.abs(cos[pert] - 1 / math.sqrt(1.25)) < 0.03)
+    assert np.all(np.delete(cos, pert) > 0.999)
