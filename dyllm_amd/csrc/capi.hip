@@ -5,6 +5,7 @@
 
 #include <cstdint>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -42,6 +43,31 @@ static inline bool aligned_to(size_t bytes, std::initializer_list<const void*> p
   return true;
 }
 static const float kLog2e = 1.4426950408889634f;
+
+// Workspace of dyllm_sparse_attention_step_noalloc: one library-owned device array per GPU,
+// resolved to its device address once per device with hipGetSymbolAddress (the host-side name
+// is not a device address). Every call on a GPU shares that GPU's array; calls that overlap on
+// one GPU race. Nothing in it has to start at zero: the step's first launch resets its maps.
+constexpr size_t kStepScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kStepScratchBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kMaxDevices] = {};
+
+static int step_scratch_ptr(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return fail("no current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return 0;
+}
 constexpr int kMoeBlock = 128;
 
 }  // namespace dyllm
@@ -357,6 +383,41 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                next_idx32, q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr,
                                next_cu_salientlens, next_count, host_meta_dev, s);
 }
+
+// ---------------------------------------------------------------------------------------
+// dyllm_sparse_attention_step_noalloc: the same step with its workspace carved from a
+// library-owned device array instead of a caller buffer, for callers that cannot allocate.
+int dyllm_sparse_attention_step_noalloc(const void* q, const void* k, const int64_t* k_start, void* v_cache,
+                                        const int64_t* v_seq_starts, const void* v_new, void* c_cache,
+                                        const int64_t* c_seq_starts, const int64_t* seq_ids, int batch,
+                                        int num_heads, int num_kv_heads, int head_dim,
+                                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                        const int32_t* cu_promptlens, int max_seqlen_q, int max_seqlen_k,
+                                        int64_t total_q, int64_t total_k, int num_salient, int max_salientlen,
+                                        const int32_t* cu_salientlens, const int32_t* idx_q32,
+                                        const int64_t* idx_k64, const int32_t* idx_k32, float softmax_scale,
+                                        float threshold, void* out, float* cosine_stats, uint8_t* cosine_out,
+                                        int64_t* next_idx64, int32_t* next_idx32, int64_t* next_idx_k64,
+                                        int32_t* next_idx_k32, int32_t* next_cu_salientlens, int32_t* next_count,
+                                        int32_t* host_meta, void* stream) {
+  DYLLM_REQUIRE(num_salient >= 0 && batch >= 1 && total_q >= 0 && total_k >= 0, "bad sizes");
+  const size_t need = dyllm_sparse_step_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, total_q, total_k,
+                                                        max_seqlen_k, num_salient);
+  DYLLM_REQUIRE(need <= kStepScratchBytes, "step needs " + std::to_string(need) +
+                                               " bytes of scratch; the no-allocation entry point holds " +
+                                               std::to_string(kStepScratchBytes) + " (use dyllm_sparse_attention_step)");
+  void* ws = nullptr;
+  if (int rc = step_scratch_ptr(&ws)) return rc;
+  return dyllm_sparse_attention_step(q, k, k_start, v_cache, v_seq_starts, v_new, c_cache, c_seq_starts, seq_ids,
+                                     batch, num_heads, num_kv_heads, head_dim, cu_seqlens_q, cu_seqlens_k,
+                                     cu_promptlens, max_seqlen_q, max_seqlen_k, total_q, total_k, num_salient,
+                                     max_salientlen, cu_salientlens, idx_q32, idx_k64, idx_k32, softmax_scale,
+                                     threshold, out, cosine_stats, cosine_out, next_idx64, next_idx32, next_idx_k64,
+                                     next_idx_k32, next_cu_salientlens, next_count, host_meta, ws, kStepScratchBytes,
+                                     stream);
+}
+
+size_t dyllm_sparse_step_scratch_bytes(void) { return kStepScratchBytes; }
 
 int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,
                          int64_t row_elems, void* dv_out, void* stream) {

@@ -310,6 +310,25 @@ def sparse_attention_step(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_s
     return bufs
 
 
+def sparse_attention_step_noalloc(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_seq_starts, seq_ids,
+                                  cu_seqlens_q, cu_seqlens_k, cu_promptlens, max_seqlen_q, max_seqlen_k, total_k,
+                                  n_sal, max_salientlen, cu_salientlens, idx_q32, idx_k64, idx_k32, softmax_scale,
+                                  threshold, k_start=None):
+    """``sparse_attention_step`` through dyllm_sparse_attention_step_noalloc: the workspace is the
+    library's own per-GPU scratch array (``bufs.ws`` is not used), so the call allocates nothing."""
+    Tq, H, D = q.shape
+    Hkv = v_new.shape[1] if v_new.dim() == 3 else v_cache.shape[1] // D
+    bufs.host_meta.fill_(-1)
+    _lib.call("dyllm_sparse_attention_step_noalloc", _ptr(q), _ptr(k), _ptr(k_start), _ptr(v_cache),
+              _ptr(v_seq_starts), _ptr(v_new), _ptr(c_cache), _ptr(c_seq_starts), _ptr(seq_ids), seq_ids.numel(), H,
+              Hkv, D, _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), _ptr(cu_promptlens), int(max_seqlen_q),
+              int(max_seqlen_k), Tq, int(total_k), int(n_sal), int(max_salientlen), _ptr(cu_salientlens),
+              _ptr(idx_q32), _ptr(idx_k64), _ptr(idx_k32), float(softmax_scale), float(threshold), _ptr(bufs.out),
+              _ptr(bufs.stats), _ptr(bufs.mask), _ptr(bufs.idx64), _ptr(bufs.idx32), _ptr(bufs.idx_k64),
+              _ptr(bufs.idx_k32), _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(bufs.host_meta), _stream())
+    return bufs
+
+
 def fused_offset_launch(idxs, num_idxs, cu_promptlens, cu_salientlens, out_tensor, max_threads):
     """attention_aux_kernels.cu:173-200 (same argument checks)."""
     dev = idxs.device

@@ -135,6 +135,29 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                 int32_t* next_cu_salientlens, int32_t* next_count, int32_t* host_meta,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same step as dyllm_sparse_attention_step without the workspace arguments: no counterpart
+ * in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): the workspace is a library-owned device
+ * array of dyllm_sparse_step_scratch_bytes() (64 MiB) per GPU, held until the process ends.
+ * Calls whose dyllm_sparse_step_workspace_bytes(...) exceeds it fail with an error (config 1,
+ * 920 salient rows, needs about 18 MiB). The array keeps the last call's contents; every call on
+ * one GPU shares it, so calls that overlap on one GPU (concurrent streams or threads) race.
+ * Allocates nothing: no hipMalloc / hipFree, no library allocation. */
+size_t dyllm_sparse_step_scratch_bytes(void);
+int dyllm_sparse_attention_step_noalloc(const void* q, const void* k, const int64_t* k_start, void* v_cache,
+                                        const int64_t* v_seq_starts, const void* v_new, void* c_cache,
+                                        const int64_t* c_seq_starts, const int64_t* seq_ids, int batch,
+                                        int num_heads, int num_kv_heads, int head_dim,
+                                        const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                        const int32_t* cu_promptlens, int max_seqlen_q, int max_seqlen_k,
+                                        int64_t total_q, int64_t total_k, int num_salient, int max_salientlen,
+                                        const int32_t* cu_salientlens, const int32_t* idx_q32,
+                                        const int64_t* idx_k64, const int32_t* idx_k32, float softmax_scale,
+                                        float threshold, void* out, float* cosine_stats, uint8_t* cosine_out,
+                                        int64_t* next_idx64, int32_t* next_idx32, int64_t* next_idx_k64,
+                                        int32_t* next_idx_k32, int32_t* next_cu_salientlens, int32_t* next_count,
+                                        int32_t* host_meta, void* stream);
+
 /* dV and V-cache update of attention.py:67-74 (dv = v_new - v_cache[row]; v_cache[row] = v_new)
  * for compact rows; dest_rows are cache rows (dyllm_scatter_dest_rows). */
 int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,
