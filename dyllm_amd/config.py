@@ -139,6 +139,13 @@ class Config:
     dist_port: Optional[int] = None
     dtype: str = "bfloat16"
     seed: int = 0                      # random-initialisation seed when no weights are loaded
+    # Sparse-step cadence: after `refresh_period` processed steps, a step queries only the response
+    # rows (Q-pruned) except every `refresh_period`-th, which queries all rows (model_runner.py:211,
+    # where the period is the constant 4).
+    refresh_period: int = 4
+    # Overrides the checkpoint's max_position_embeddings (the RoPE table length and the cap on
+    # max_model_len, config.py:51-58) for contexts longer than the checkpoint was trained on.
+    max_position_embeddings: Optional[int] = None
 
     def __post_init__(self):
         if self.tensor_parallel_size != 1 or self.expert_parallel_size != 1:
@@ -148,6 +155,12 @@ class Config:
             raise ValueError("the HIP kernels compute in bfloat16 only")
         if self.hf_config is None:
             self.hf_config = load_model_config(self.model)
+        if self.refresh_period < 1:
+            raise ValueError("refresh_period must be at least 1")
+        if self.max_position_embeddings is not None:
+            if self.max_position_embeddings < 1:
+                raise ValueError("max_position_embeddings must be positive")
+            self.hf_config = replace(self.hf_config, max_position_embeddings=int(self.max_position_embeddings))
         self.mask_id = self.hf_config.mask_token_id
         if self.hf_config.eos_token_id is not None:
             self.eos = self.hf_config.eos_token_id

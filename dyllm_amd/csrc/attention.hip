@@ -37,9 +37,6 @@ constexpr int kVStride = kBK + 12;   // V^T tile row stride (elements): 152 B, c
 // Two-pass column-sparse path (sequences of at most kMaxBlk2 key blocks): LDS it needs beyond
 // the K / V^T tiles.
 constexpr int kMaxBlk2 = 64;
-#ifndef DYLLM_P1_PAIR
-#define DYLLM_P1_PAIR 1
-#endif
 struct ColSparseLds {
   float* m;          // [NW][kMaxBlk2][32] running max of each query row after each key block
   int16_t* keys;     // [kMaxBlk2 * kBK] salient keys in 16-slot groups, -1 = padding
@@ -70,6 +67,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
                                                uint16_t* __restrict__ vt_lds, const ColSparseLds& sp) {
   constexpr int NT = NW * 64;              // threads
   constexpr int BQ = NW * 32;              // query rows per workgroup
+  static_assert(MODE != AttnMode::ColSparse || NW % 2 == 0, "the paired pass 1 needs an even number of wavefronts");
   constexpr int KCH = kBK * kD / 8 / NT;   // 16-byte K chunks per thread per tile
   constexpr int VIT = (kBK / 4) * (kD / 8) / NT;  // (4 keys x 8 d) V items per thread per tile
 
@@ -300,7 +298,6 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       for (; n < grp * 16; ++n) sp.keys[g0 * 16 + n] = -1;
       for (int j = 0; j < grp; ++j) sp.gblk[g0 + j] = uint8_t(lane);
     }
-#if DYLLM_P1_PAIR
     // Wavefronts pair up (w, w^1) over the pair's two 32-row groups, and wave w scores the key
     // blocks of parity w & 1 for both groups: every K fragment read from LDS feeds two MFMAs (half
     // the LDS reads per row, four independent accumulation chains). Each wave keeps a partial
@@ -418,49 +415,6 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       }
     }
     __syncthreads();
-#else
-    if (nkb > 0) stage_k(k_lds);
-    if (nkb > 1) fetch_k(1);
-    __syncthreads();   // the group list and K tile 0 are complete
-    for (int kb = 0; kb < nkb; ++kb) {
-      const int key0 = kb * kBK;
-      f32x16_t sa[2];
-      qk(sa, (kb & 1) ? vt_lds : k_lds);
-      if (kb + 1 < nkb) stage_k((kb & 1) ? k_lds : vt_lds);
-      if (kb + 2 < nkb) fetch_k(kb + 2);
-      if (key0 + kBK > Lk) {  // ragged last block only
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = key0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-            if (key >= Lk) sa[t][r] = -FLT_MAX;
-          }
-      }
-      float bm = sa[0][0];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sa[t][r]);
-      bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-      const float m_new = fmaxf(m_run, bm);
-      const float rescale = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
-      const float m2 = m_new * c2;
-      m_run = m_new;
-      float psum = 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[t][r], c2, -m2));
-          const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[t][r + 1], c2, -m2));
-          psum += e0 + e1;
-        }
-      l_run = l_run * rescale + psum;
-      if (half == 0) m_tab[kb * 32] = m_new;
-      __syncthreads();
-    }
-#endif
     // (the last barrier also ends pass 1's reads of both tiles before pass 2 restages them)
 
     // ---- pass 2 ----

@@ -318,7 +318,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
 // M tiles that share a weight slice run together on one XCD and read it from HBM once.
 template <int BM, int WGN, GemmEpi EPI>
 __global__ __launch_bounds__(128 * WGN) void gemm_kernel(GemmArgs g) {
-  const int64_t M = g.num_m_dev ? int64_t(g.num_m_dev[0]) : g.M;
+  const int64_t M = g.num_m_dev ? min(int64_t(g.num_m_dev[0]), g.M) : g.M;   // never past the host capacity
   const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (kGemmBN / 2)) : int(cdiv(g.N, kGemmBN));
   const int mtr = int(cdiv(M, BM));
   const int64_t total = int64_t(mtr) * n_tiles * g.ksplit;
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(128 * WGN) void gemm_kernel(GemmArgs g) {
 // Sum of the split-K slices in slice order, then the store epilogue (row remap, row scale,
 // bf16). One thread per 4 output columns.
 __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs g) {
-  const int64_t M = g.num_m_dev ? int64_t(g.num_m_dev[0]) : g.M;
+  const int64_t M = g.num_m_dev ? min(int64_t(g.num_m_dev[0]), g.M) : g.M;
   const int nq = g.N / 4;
   for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < M * nq; t += int64_t(gridDim.x) * 256) {
     const int64_t m = t / nq;

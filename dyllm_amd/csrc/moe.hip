@@ -103,7 +103,10 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int32_t* __restri
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   if (tid < 64) cnt[tid] = 0;
   __syncthreads();
-  for (int64_t i = tid; i < S; i += 1024) atomicAdd(&cnt[ids[i]], 1);
+  // expert ids are clamped to [0, E): an out-of-range id from a caller can never index past the
+  // 64-entry LDS tables (its slot is then routed to the nearest valid expert)
+  auto expert_of = [&](int64_t i) { return min(max(int(ids[i]), 0), E - 1); };
+  for (int64_t i = tid; i < S; i += 1024) atomicAdd(&cnt[expert_of(i)], 1);
   __syncthreads();
   if (tid == 0) {
     int acc = 0;
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int32_t* __restri
   for (int64_t r0 = 0; r0 < S; r0 += 1024) {
     const int64_t i = r0 + tid;
     const bool ok = i < S;
-    const int e = ok ? ids[i] : 63;
+    const int e = ok ? expert_of(i) : 63;
     unsigned long long same = __ballot(ok);
 #pragma unroll
     for (int bit = 0; bit < 6; ++bit) {

@@ -6,9 +6,9 @@ Step kinds (model_runner.py:140-298):
 * full      -- every row of every sequence is queried; the layers run dense attention and the
                FFN over all rows and rewrite their caches;
 * sparse    -- the first layer's salient rows are the positions the previous step unmasked;
-               each layer's attention decides the next layer's salient rows. After four
-               processed steps a sparse step queries only the response rows (Q-pruned), except
-               every fourth step, which queries all rows (refresh).
+               each layer's attention decides the next layer's salient rows. After
+               `refresh_period` (4) processed steps a sparse step queries only the response rows
+               (Q-pruned), except every `refresh_period`-th step, which queries all rows (refresh).
 
 A batch is Q-pruned only when all its sequences are (the reference decides per sequence but
 then drops the K-space index list as soon as one sequence refreshes, model_runner.py:213-220,
@@ -86,9 +86,10 @@ class _HostStaging:
         return {name: dev[o:o + arr.nbytes].view(dt) for (name, arr, dt), o in zip(fields, offs)}
 
 
-def q_pruned_step(seq: Sequence) -> bool:
-    """Sparse step that queries only the response rows (model_runner.py:205)."""
-    return seq.processed_steps > 4 and seq.processed_steps % 4 != 0
+def q_pruned_step(seq: Sequence, period: int = 4) -> bool:
+    """Sparse step that queries only the response rows (model_runner.py:211, period 4 there):
+    after `period` processed steps, all but every `period`-th step."""
+    return seq.processed_steps > period and seq.processed_steps % period != 0
 
 
 class ModelRunner:
@@ -99,6 +100,7 @@ class ModelRunner:
         self.device = torch.device(device)
         self.num_full_forwards = 0
         self.num_sparse_forwards = 0
+        self.num_q_pruned_forwards = 0     # sparse steps that queried only the response rows
         hf = config.hf_config
         self.model = model if model is not None else build_model(config, device)
         self.sampler = DreamSampler("entropy") if hf.model_type == "Dream" else LLaDASampler("confidence")
@@ -135,7 +137,7 @@ class ModelRunner:
 
     def prepare_sparse(self, seqs: List[Sequence]):
         md = get_metadata()
-        pruned = all(q_pruned_step(s) for s in seqs)
+        pruned = all(q_pruned_step(s, self.config.refresh_period) for s in seqs)
         input_ids, positions, positions_k = [], [], []
         idx_q, idx_k, idx_upd = [], [], []
         cu_q, cu_k, cu_p, cu_s, lens, ids = [0], [0], [0], [0], [], []
@@ -251,7 +253,8 @@ class ModelRunner:
         get_metadata().finished_seqs = list(finished_seqs or [])
         # all host-built metadata of the step (batch layout and sampling inputs) in one transfer
         finish_batch = self.prepare_full(seqs) if is_full else self.prepare_sparse(seqs)
-        pruned = not is_full and all(q_pruned_step(s) for s in seqs)
+        pruned = not is_full and all(q_pruned_step(s, self.config.refresh_period) for s in seqs)
+        self.num_q_pruned_forwards += int(pruned)
         finish_sample = self.prepare_sample(seqs, pruned)
         staged = self.staging.flush()
         input_ids, positions = finish_batch(staged)

@@ -295,7 +295,9 @@ int dyllm_rms_norm(const void* x, int64_t ld_x, const void* residual, int64_t ld
 int dyllm_moe_gate(const void* x, const int32_t* rows_idx, int64_t tokens, int hidden, const void* router_w,
                    int num_experts, int top_k, int renormalize, void* topk_weights, int32_t* topk_ids, void* stream);
 
-/* moe_align_block_size on the device. capacity >= tokens*top_k + E*(block-1), multiple of block. */
+/* moe_align_block_size on the device. capacity >= tokens*top_k + E*(block-1), multiple of block.
+ * Expert ids outside [0, num_experts) are clamped into that range on the device (the ids are
+ * device data: validating them on the host would need a synchronisation). */
 int dyllm_moe_align_block_size(const int32_t* topk_ids, int64_t slots, int num_experts, int block,
                                int32_t* sorted_token_ids, int64_t capacity, int32_t* tile_expert,
                                int32_t* num_post_pad, void* stream);

@@ -30,3 +30,18 @@ def assert_mask_equal(got_mask, want_mask, cos_ref, tau, band=TAU_BAND, what="sa
     bad = np.nonzero((g != w) & keep)[0]
     assert bad.size == 0, f"{what}: {bad.size} rows differ outside the tau band, e.g. {bad[:8]} cos={c[bad[:8]]}"
     return int((~keep).sum())
+
+
+def assert_routing_weights(got, want, what="routing weights"):
+    """Router weights are bf16 roundings of one fp32 softmax probability: the device's fp32
+    (dot-product order, exp) may differ from torch's by a few fp32 ulps, which can move the bf16
+    rounding by at most one bf16 ulp of the value. Bar: every weight within one bf16 ulp, and the
+    normwise mean relative error within MEAN_REL (1e-3)."""
+    g = got.detach().float().cpu()
+    w = want.detach().float().cpu()
+    assert g.shape == w.shape
+    ulp = torch.exp2(torch.floor(torch.log2(w.abs().clamp_min(1e-30))) - 7)
+    bad = ((g - w).abs() > ulp).nonzero()
+    assert bad.numel() == 0, f"{what}: {bad.shape[0]} weights differ by more than one bf16 ulp"
+    rel = ((g - w).abs().mean() / w.abs().mean()).item()
+    assert rel <= MEAN_REL, f"{what}: mean rel err {rel:.3e} > {MEAN_REL}"

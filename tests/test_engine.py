@@ -278,3 +278,30 @@ def test_weight_loader_moe_experts():
     load_weights(dst, ws)
     for (n, a), (_, b) in zip(src.named_parameters(), dst.named_parameters()):
         assert torch.equal(a.data, b.data), n
+
+
+def test_config_refresh_period_and_long_context():
+    """Config 4: refresh every 8 steps and an 8192-row context on the LLaDA-8B shape, whose
+    checkpoint caps positions at 4096 (config.py:51-58 clips max_model_len to it)."""
+    from dyllm_amd.engine.model_runner import q_pruned_step
+
+    assert Config("llada-8b", max_model_len=8192).max_model_len == 4096   # the reference's clip
+    c = Config("llada-8b", max_model_len=8192, max_position_embeddings=8192, refresh_period=8)
+    assert c.max_model_len == 8192 and c.hf_config.max_position_embeddings == 8192
+    assert PRESETS["llada-8b"].max_position_embeddings == 4096            # the preset is not mutated
+    with pytest.raises(ValueError, match="refresh_period"):
+        Config("llada-8b", refresh_period=0)
+
+    class _S:
+        processed_steps = 0
+
+    def kinds(period):
+        out = []
+        for n in range(1, 25):
+            _S.processed_steps = n
+            out.append("q" if q_pruned_step(_S, period) else "r")
+        return "".join(out)
+
+    # period 4 is the reference's cadence (model_runner.py:211)
+    assert kinds(4) == "rrrr" + "qqqr" * 5
+    assert kinds(8) == "rrrrrrrr" + "qqqqqqqr" * 2

@@ -76,3 +76,29 @@ def test_host_staging_single_transfer(dev):
         for name, (t, dt) in fields.items():
             assert out[name].dtype == dt and out[name].device.type == "cuda"
             assert torch.equal(out[name].cpu(), t.to(dt)), name
+
+
+def test_generate_config4_long_context(dev):
+    """Config 4 through dLLM.generate: the LLaDA-8B shape (32 layers, random-init bf16), batch 2,
+    2048 prompt + 6144 response tokens (an 8192-row context, past the checkpoint's 4096 positions,
+    so the RoPE tables are raised to 8192), tau = 0.995, a full-attention refresh every 8 steps."""
+    from dyllm_amd import SamplingParams, dLLM
+
+    print("[engine] config4 long context", flush=True)
+    eng = dLLM("llada-8b", threshold=0.995, max_model_len=8192, max_position_embeddings=8192, refresh_period=8)
+    assert eng.config.max_model_len == 8192
+    rot = eng.model_runner.model.model.layers[0].self_attn.rotary
+    assert rot.cos.shape[0] == 8192
+    g = torch.Generator().manual_seed(4)
+    prompts = [torch.randint(0, 126000, (2048,), generator=g).tolist() for _ in range(2)]
+    steps = 24
+    sp = SamplingParams(max_new_tokens=6144, steps=steps, num_full_steps=1, block_size=6144, temperature=0.0)
+    out = eng.generate(prompts, sp)
+    torch.cuda.synchronize()
+    st = eng.execution_stats
+    assert st["full_forwards"] == 1 and st["full_forwards"] + st["sparse_forwards"] == steps
+    # processed steps 9-15 and 17-23 are Q-pruned; 2-8, 16 and 24 query every row
+    assert eng.model_runner.num_q_pruned_forwards == 14
+    for o, p in zip(out, prompts):
+        assert o["token_ids"][:2048] == p and len(o["token_ids"]) == 8192
+        assert o["token_ids"][2048:].count(eng.config.mask_id) < 6144 // 8
