@@ -17,12 +17,18 @@ projections/norms on either side of the path are outside the timed region (their
 pre-generated per layer). The caches are restored between steps (untimed) so every timed
 step sees the same salient fraction.
 
-value = B * Lq / step time (tokens/s). The roofline object is for the dominant kernel, the
-fused attention kernel of the step (timed with library-owned HIP events around that launch,
-dyllm_attention_timer); roofline_gate_up is the gathered gate_up SwiGLU GEMM, timed with HIP
-events on its own launches. The salient-row K/V
-projection GEMM (the step before the path, outside `value`) is timed on its own after the
-steps and reported as `kv_projection`.
+Steps follow config 1's cadence: step i of the timed K is a refresh step (every row queried,
+T = 8192, the salient set in K space) when i % 4 == 3, and a Q-pruned step (the 6144 response
+rows) otherwise; both denoise the same B * Lq = 6144 answer tokens.
+
+value = B * Lq / mean step time over the K steps (tokens/s); the Q-pruned and refresh steps are
+also reported on their own. The roofline object is for the dominant kernel of the Q-pruned step,
+the fused attention kernel (timed with library-owned HIP events around that launch,
+dyllm_attention_timer) or the gathered gate_up SwiGLU GEMM (HIP events on its own launches),
+whichever has the longer mean launch; the other rides along, as do the down GEMM, the fused
+kernel of the refresh step, the dense full-step attention, config 3's MoE expert FFN and the
+salient-row K/V projection (the step before the path, outside `value`), each timed with HIP
+events on its launching stream.
 """
 from __future__ import annotations
 
@@ -110,13 +116,14 @@ def build_workload(cfg, layers, device, seed=0):
         c[S_k] = (rows + 0.5 * rms * randn(len(sk), H * D).float()).to(torch.bfloat16)
         resp = torch.cat([torch.arange(b * L + P, (b + 1) * L, device=device) for b in range(B)])
         q = q_all[resp].contiguous()
+        q_full = q_all     # the refresh step queries every row
         k_new = (k_all[resp].float() + 0.1 * randn(Tq, Hkv, D).float()).to(torch.bfloat16)
         v_new = (v_all[resp].float() + 0.1 * randn(Tq, Hkv, D).float()).to(torch.bfloat16)
-        del q_all, k_all, v_all
+        del k_all, v_all
         # stand-in for the salient-row K/V projection output: kv rows [k | v] of every queried row
         kv_all = torch.cat([k_new.view(Tq, -1), v_new.view(Tq, -1)], dim=1).contiguous()
         del k_new, v_new
-        state.append(dict(attn=attn, k_cache=k_cache, mlp=mlp, q=q, kv_all=kv_all,
+        state.append(dict(attn=attn, k_cache=k_cache, mlp=mlp, q=q, q_full=q_full, kv_all=kv_all,
                           c_saved=attn.context_cache.cache.clone(), v_saved=attn.v_cache.cache.clone()))
     torch.cuda.synchronize()
     # RoPE tables (rotary_embedding.py:19-38, theta 500000); every position 0, where the rotation
@@ -125,47 +132,114 @@ def build_workload(cfg, layers, device, seed=0):
     inv = 1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32, device=device) / D))
     freqs = torch.outer(torch.arange(4096, dtype=torch.float32, device=device), inv)
     rope_cos, rope_sin = freqs.cos().contiguous(), freqs.sin().contiguous()
-    pos0 = torch.zeros(Tq, dtype=torch.long, device=device)
+    pos0 = torch.zeros(Tk, dtype=torch.long, device=device)
 
-    def set_sparse_context():
+    def set_sparse_context(refresh):
+        if refresh:   # every row queried; the salient set lives in K space (model_runner.py:217-222)
+            return set_context(False, cu_seqlens_q=cu_k, cu_seqlens_q_cpu=cu_k_cpu, cu_seqlens_k=cu_k,
+                               cu_seqlens_k_cpu=cu_k_cpu, cu_promptlens=cu_p, max_seqlen_q=L, max_seqlen_k=L,
+                               context_lens_cpu=[L] * B, cu_salientlens=cu_s, idx_salient_row=S_k,
+                               idx_salient_row_i32=S_k.to(torch.int32), idx_salient_row_k=None,
+                               max_salientlen=n_per, total_seqlen=Tk, total_seqlen_k=Tk)
         return set_context(False, cu_seqlens_q=cu_q, cu_seqlens_q_cpu=cu_q_cpu, cu_seqlens_k=cu_k,
                            cu_seqlens_k_cpu=cu_k_cpu, cu_promptlens=cu_p, max_seqlen_q=R, max_seqlen_k=L,
                            context_lens_cpu=[L] * B, cu_salientlens=cu_s, idx_salient_row=S_q,
-                           idx_salient_row_i32=S_q.to(torch.int32), idx_salient_row_k=S_k, max_salientlen=n_per, total_seqlen=Tq,
-                           total_seqlen_k=Tk)
+                           idx_salient_row_i32=S_q.to(torch.int32), idx_salient_row_k=S_k, max_salientlen=n_per,
+                           total_seqlen=Tq, total_seqlen_k=Tk)
 
     def restore():
         for st in state:
             st["attn"].context_cache.cache.copy_(st["c_saved"])
             st["attn"].v_cache.cache.copy_(st["v_saved"])
 
-    def step(events=None, n_sal=None):
-        ctx = set_sparse_context()
+    # Q-space row of every K row (the response rows of the Q-pruned layout), to find the stand-in
+    # projection rows of a K-space salient set
+    q_of_k = torch.full((Tk,), -1, dtype=torch.long, device=device)
+    q_of_k[S_k] = S_q
+
+    def step(events=None, n_sal=None, refresh=False):
+        ctx = set_sparse_context(refresh)
+        T = Tk if refresh else Tq
         for li, st in enumerate(state):
             idx = ctx.idx_salient_row
             if n_sal is not None:
                 n_sal.append(idx.numel())
             # the projection's [k | v] rows of the salient set (stand-in: a gather), then the fused
             # epilogue: RoPE + K-cache scatter of k, the compact v of the step
-            kv = ops.gather_rows_2D(st["kv_all"], idx)
-            v_sal = st["k_cache"].scatter_kv_rope(md.running_seqs_tensor, ctx.idx_salient_row_k, kv, Hkv, pos0,
+            kv = ops.gather_rows_2D(st["kv_all"], q_of_k[idx] if refresh else idx)
+            kidx = ctx.idx_salient_row if refresh else ctx.idx_salient_row_k
+            v_sal = st["k_cache"].scatter_kv_rope(md.running_seqs_tensor, kidx, kv, Hkv, pos0,
                                                   rope_cos, rope_sin, ctx.idx_salient_row_i32)
             k_full = st["k_cache"].get_seqs(md.running_seqs_tensor, md.running_seqs).view(-1, Hkv, D)
             ev = events.get(li) if events is not None else None
             if ev is not None:   # time the fused attention kernel of this layer's step call
                 _lib.load().dyllm_attention_timer(1)
-            o = st["attn"](st["q"], k_full, v_sal)
+            o = st["attn"](st["q_full"] if refresh else st["q"], k_full, v_sal)
             if ev is not None:
                 _lib.load().dyllm_attention_timer(0)
-            st["mlp"].forward_salient(o.view(Tq, H * D), gate_up_events=ev)
+            st["mlp"].forward_salient(o.view(T, H * D), timing=ev)
         return ctx
 
     return dict(step=step, restore=restore, Tq=Tq, Tk=Tk, n_per=n_per, S_q=S_q, state=state)
 
 
+def _median_time(fn, warmup=2, repeats=5):
+    """2 warm-ups, then the median of `repeats` wall-clock runs (time.perf_counter)."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def _cpu_layer(ref, torch, np, B, P, R, H, Hkv, D, hid, inter, n_per, tau, seed):
+    """Inputs of one sparse layer of the saliency path for the CPU oracle, and the closure that
+    runs it: RoPE of the salient keys, row-sparse attention of the salient queries, column-sparse
+    attention + statistics + tau test, compaction + fused offset, gathered SwiGLU FFN."""
+    L = P + R
+    Tk, Tq = B * L, B * R
+    g = torch.Generator().manual_seed(seed)
+    bf = torch.bfloat16
+    q = torch.randn(Tq, H, D, generator=g).to(bf)
+    k = torch.randn(Tk, Hkv, D, generator=g).to(bf)
+    v = torch.randn(Tk, Hkv, D, generator=g).to(bf)
+    c = torch.randn(Tq, H, D, generator=g).to(bf)
+    rng = np.random.default_rng(seed)
+    idx_q, idx_k = [], []
+    for b in range(B):
+        sel = np.sort(rng.choice(R, size=n_per, replace=False))
+        idx_q += (b * R + sel).tolist()
+        idx_k += (b * L + P + sel).tolist()
+    idx_q, idx_k = np.asarray(idx_q), np.asarray(idx_k)
+    cu_q, cu_k, cu_p, cu_s = (np.arange(B + 1) * x for x in (R, L, P, n_per))
+    dv = torch.zeros_like(k)
+    dv[idx_k] = (0.1 * torch.randn(len(idx_k), Hkv, D, generator=g)).to(bf)
+    w_gu = (0.02 * torch.randn(2 * inter, hid, generator=g)).to(bf)
+    w_d = (0.02 * torch.randn(hid, inter, generator=g)).to(bf)
+    rope_cos, rope_sin = ref.rope_tables(D, 4096, 500000.0)
+    ik, iq = torch.from_numpy(idx_k), torch.from_numpy(idx_q)
+    pos = torch.zeros(len(idx_k), dtype=torch.long)
+
+    def run():
+        kk = k.clone()
+        kk[ik] = ref.rope_neox(kk[ik], rope_cos, rope_sin, pos)
+        o_sal = ref.flash_attn_varlen(q[iq], kk, v, cu_s, cu_k)
+        new_c, _, mask = ref.attention_sparse_varlen(q, kk, dv, c, o_sal, cu_q, cu_k, idx_q, tau)
+        idxs, cu_sal = ref.compact(mask.numpy(), cu_q)
+        ref.fused_offset(idxs, cu_p, cu_sal)
+        ref.swiglu_ffn(new_c.reshape(Tq, -1)[iq], w_gu, w_d)
+
+    return run
+
+
 def cpu_baseline(cfg, n_sal, threads):
-    """One layer of the same workload through the CPU oracle (fp32 torch / numpy),
-    extrapolated to the model's layer count."""
+    """The CPU oracle (fp32 torch / numpy restatement of the reference path) on the GPU box's host,
+    timed as 2 warm-ups + the median of 5 repeats: one config-1 layer at full shape (x the layer
+    count), and config 0 (one layer, B = 1, 128 + 384 rows, 10 % salient) in full."""
     import numpy as np
     import torch
 
@@ -173,44 +247,19 @@ def cpu_baseline(cfg, n_sal, threads):
 
     torch.set_num_threads(threads)
     B, P, R = cfg["batch"], cfg["prompt"], cfg["response"]
-    L = P + R
     H, Hkv, D, hid, inter = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["hidden"], cfg["inter"]
-    Tk, Tq = B * L, B * R
-    g = torch.Generator().manual_seed(1)
-    bf = torch.bfloat16
-    q = torch.randn(Tq, H, D, generator=g).to(bf)
-    k = torch.randn(Tk, Hkv, D, generator=g).to(bf)
-    v = torch.randn(Tk, Hkv, D, generator=g).to(bf)
-    c = torch.randn(Tq, H, D, generator=g).to(bf)
     n_per = max(1, n_sal // B)
-    rng = np.random.default_rng(1)
-    idx_q, idx_k = [], []
-    for b in range(B):
-        sel = np.sort(rng.choice(R, size=n_per, replace=False))
-        idx_q += (b * R + sel).tolist()
-        idx_k += (b * L + P + sel).tolist()
-    idx_q, idx_k = np.asarray(idx_q), np.asarray(idx_k)
-    cu_q = np.arange(B + 1) * R
-    cu_k = np.arange(B + 1) * L
-    cu_p = np.arange(B + 1) * P
-    cu_s = np.arange(B + 1) * n_per
-    dv = torch.zeros_like(k)
-    dv[idx_k] = (0.1 * torch.randn(len(idx_k), Hkv, D, generator=g)).to(bf)
-    w_gu = (0.02 * torch.randn(2 * inter, hid, generator=g)).to(bf)
-    w_d = (0.02 * torch.randn(hid, inter, generator=g)).to(bf)
-    rope_cos, rope_sin = ref.rope_tables(D, 4096, 500000.0)
-    t0 = time.perf_counter()
-    k[torch.from_numpy(idx_k)] = ref.rope_neox(k[torch.from_numpy(idx_k)], rope_cos, rope_sin,
-                                               torch.zeros(len(idx_k), dtype=torch.long))
-    o_sal = ref.flash_attn_varlen(q[torch.from_numpy(idx_q)], k, v, cu_s, cu_k)
-    new_c, _, mask = ref.attention_sparse_varlen(q, k, dv, c, o_sal, cu_q, cu_k, idx_q, cfg["tau"])
-    idxs, cu_sal = ref.compact(mask.numpy(), cu_q)
-    ref.fused_offset(idxs, cu_p, cu_sal)
-    ref.swiglu_ffn(new_c.reshape(Tq, -1)[torch.from_numpy(idx_q)], w_gu, w_d)
-    t_layer = time.perf_counter() - t0
+    run1 = _cpu_layer(ref, torch, np, B, P, R, H, Hkv, D, hid, inter, n_per, cfg["tau"], 1)
+    t_layer = _median_time(run1)
+    run0 = _cpu_layer(ref, torch, np, 1, 128, 384, 32, 32, 128, 4096, 12288, 38, cfg["tau"], 2)
+    t0 = _median_time(run0)
+    Tq = B * R
     return dict(value=Tq / (t_layer * cfg["layers"]), unit="tokens/s", cores=threads, kind="port",
-                sample=f"1 of {cfg['layers']} layers at full config-1 shape ({n_sal} salient rows), "
-                       f"{t_layer:.2f} s, x{cfg['layers']}")
+                sample=f"1 of {cfg['layers']} layers at full config-1 shape ({n_per * B} salient rows): "
+                       f"median {t_layer:.3f} s of 5 after 2 warm-ups, x{cfg['layers']} layers",
+                config0={"value": 384 / t0, "unit": "tokens/s", "ms_per_layer": round(t0 * 1e3, 2),
+                         "sample": "config 0 in full: one layer, B=1, 128+384 rows, 38 salient rows, "
+                                   "median of 5 after 2 warm-ups"})
 
 
 def time_kv_projection(cfg, n_sal, reps=24, copies=8):
@@ -356,10 +405,90 @@ def profile_gate_up(cfg, reps=3):
           file=sys.stderr)
 
 
+def time_dense_attention(cfg, reps=5):
+    """Dense full-sequence attention (the full steps, attention.py:39-62: attention_kernel<Dense>)
+    at the config-1 shape, T = 8192 rows, HIP events on the launching stream."""
+    import torch
+
+    from dyllm_amd import ops
+
+    dev = "cuda"
+    B, L = cfg["batch"], cfg["prompt"] + cfg["response"]
+    H, Hkv, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    g = torch.Generator(device=dev).manual_seed(3)
+    rnd = lambda *sh: torch.empty(*sh, device=dev).normal_(generator=g).to(torch.bfloat16)
+    q, k, v = rnd(B * L, H, D), rnd(B * L, Hkv, D), rnd(B * L, Hkv, D)
+    cu = torch.arange(B + 1, dtype=torch.int32, device=dev) * L
+    ops.flash_attn_varlen_func(q, k, v, cu, cu, L, L)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ops.flash_attn_varlen_func(q, k, v, cu, cu, L, L)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / reps * 1e3
+    flops = 4.0 * B * L * L * H * D
+    tf = flops / (us * 1e-6) / 1e12
+    return {"kernel": "attention_kernel<Dense,4> (full step, 8 x 1024 rows)", "bound": "mfma",
+            "avg_launch_us": round(us, 2), "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop_per_launch": flops, "traffic": None}
+
+
+def time_moe(reps=6, copies=4):
+    """Config 3's MoE FFN over its salient rows (LLaDA-MoE: hidden 2048, 64 experts, top-8, expert
+    SwiGLU 1024; 15 % of 32 x 768 rows salient; router logits ~ N(0, 1) plus a per-expert bias
+    ~ N(0, 0.5), carried by a constant input feature, for a skewed load). Times dyllm_fused_experts
+    (align + grouped gate_up GEMM + grouped down GEMM + combine) with HIP events, cycling through
+    `copies` expert weight sets so the weights come from HBM as across 16 layers."""
+    import torch
+
+    from dyllm_amd import ops
+
+    dev = "cuda"
+    hid, E, top_k, inter = 2048, 64, 8, 1024
+    n = int(round(0.15 * 32 * 768))
+    g = torch.Generator(device=dev).manual_seed(5)
+    rnd = lambda *sh, std=1.0: torch.empty(*sh, device=dev).normal_(0.0, std, generator=g).to(torch.bfloat16)
+    x = rnd(n, hid)
+    wr = rnd(E, hid, std=hid ** -0.5)
+    x[:, 0] = 1.0
+    wr[:, 0] = rnd(E, std=0.5)
+    w1s = [rnd(E, 2 * inter, hid, std=hid ** -0.5) for _ in range(copies)]
+    w2s = [rnd(E, hid, inter, std=inter ** -0.5) for _ in range(copies)]
+    w, ids = ops.moe_gate(x, wr, top_k)
+    for i in range(copies):
+        ops.fused_experts(x, w1s[i], w2s[i], w, ids)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i, (e0, e1) in enumerate(evs):
+        e0.record()
+        ops.fused_experts(x, w1s[i % copies], w2s[i % copies], w, ids)
+        e1.record()
+    torch.cuda.synchronize()
+    us = sum(e0.elapsed_time(e1) for e0, e1 in evs) / reps * 1e3
+    flops = 6.0 * n * top_k * hid * inter
+    tf = flops / (us * 1e-6) / 1e12
+    load = torch.bincount(ids.reshape(-1).long(), minlength=E)
+    return {"kernel": "dyllm_fused_experts (align + grouped gate_up/down gemm_kernel + combine), config 3",
+            "bound": "mfma", "rows": n, "slots": n * top_k, "max_expert_load": int(load.max()),
+            "mean_expert_load": round(float(load.float().mean()), 1), "avg_launch_us": round(us, 2),
+            "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop_per_launch": flops, "traffic": None}
+
+
+def _attn_flops(T, L, HD, n, n_seq_sal):
+    """Algorithmic MFMA work of the fused attention kernel: row-sparse tiles 4 Lk H D per salient
+    query row; column-sparse tiles QK^T 2 Lk H D per other row plus PV over the salient keys of
+    its sequence."""
+    return 4.0 * L * HD * n + 2.0 * L * HD * (T - n) + 2.0 * n_seq_sal * HD * (T - n)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=8, help="timed denoise steps; step i is a refresh step when "
+                                                            "i %% 4 == 3 (config 1's cadence)")
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers than the model has")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -374,7 +503,11 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    import ctypes
+
     import torch
+
+    from dyllm_amd import _lib
 
     cfg = dict(CONFIG1)
     if args.profile_gate_up:
@@ -388,87 +521,124 @@ def main():
     torch.cuda.set_device(0)
     print(f"[bench] building config-1 workload ({layers} layers)", file=sys.stderr, flush=True)
     wl = build_workload(cfg, layers, dev)
-    for _ in range(args.warmup):
+    for i in range(args.warmup):
         wl["restore"]()
-        wl["step"]()
+        wl["step"](refresh=(i % 2 == 1))
     torch.cuda.synchronize()
 
-    total_ms = 0.0
-    gate_ms, n_sals = [], []
-    for _ in range(args.steps):
+    def read_attn_timer():
+        ms, n = ctypes.c_float(), ctypes.c_int()
+        _lib.call("dyllm_attention_timer_read", ctypes.addressof(ms), ctypes.addressof(n))
+        return ms.value, n.value
+
+    read_attn_timer()
+    kinds = {False: dict(ms=[], attn=[0.0, 0], gate=[], down=[], n_sal=[]),
+             True: dict(ms=[], attn=[0.0, 0], gate=[], down=[], n_sal=[])}
+    for i in range(args.steps):
+        refresh = i % 4 == 3
+        k = kinds[refresh]
         wl["restore"]()
-        # gate_up launches are bracketed with HIP events on every EVENT_STRIDE-th layer: each event
+        # GEMM launches are bracketed with HIP events on every EVENT_STRIDE-th layer: each event
         # pair is a pair of marker packets on the stream, so bracketing all 32 would add their cost
         # to the measured step
-        evs = {li: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        evs = {li: {"gate_up": (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)),
+                    "down": (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))}
                for li in range(0, layers, EVENT_STRIDE)}
-        n_sal = []
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        wl["step"](events=evs, n_sal=n_sal)
+        wl["step"](events=evs, n_sal=k["n_sal"], refresh=refresh)
         torch.cuda.synchronize()
-        total_ms += (time.perf_counter() - t0) * 1e3
-        gate_ms += [a.elapsed_time(b) for a, b in evs.values()]
-        n_sals += n_sal
+        k["ms"].append((time.perf_counter() - t0) * 1e3)
+        k["gate"] += [e["gate_up"][0].elapsed_time(e["gate_up"][1]) for e in evs.values()]
+        k["down"] += [e["down"][0].elapsed_time(e["down"][1]) for e in evs.values()]
+        ms, n = read_attn_timer()
+        k["attn"][0] += ms
+        k["attn"][1] += n
+    total_ms = sum(kinds[False]["ms"]) + sum(kinds[True]["ms"])
     ms_per_step = total_ms / args.steps
-    import ctypes
-
-    from dyllm_amd import _lib
-    attn_ms, attn_n = ctypes.c_float(), ctypes.c_int()
-    _lib.call("dyllm_attention_timer_read", ctypes.addressof(attn_ms), ctypes.addressof(attn_n))
-    avg_attn_ms = attn_ms.value / max(attn_n.value, 1)
-    Tq = wl["Tq"]
-    value = Tq / (ms_per_step / 1e3)
+    Tq, Tk = wl["Tq"], wl["Tk"]
+    value = Tq / (ms_per_step / 1e3)     # B x Lq denoised tokens per step, at the config-1 cadence
 
     hid, inter = cfg["hidden"], cfg["inter"]
-    avg_n = sum(n_sals) / len(n_sals)
-    flops = 2.0 * avg_n * hid * 2 * inter
-    # fused attention kernel, algorithmic work: row-sparse tiles 4 Lk H D per salient query row;
-    # column-sparse tiles QK^T 2 Lk H D per other row plus PV over its sequence's salient keys only
     L = cfg["prompt"] + cfg["response"]
     HD = cfg["heads"] * cfg["head_dim"]
-    attn_flops = (4.0 * L * HD * avg_n + 2.0 * L * HD * (Tq - avg_n)
-                  + 2.0 * (avg_n / cfg["batch"]) * HD * (Tq - avg_n))
-    attn_tf = attn_flops / (avg_attn_ms * 1e-3) / 1e12
-    avg_gate_ms = sum(gate_ms) / len(gate_ms)
-    from dyllm_amd import _lib
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
+    per = {}
+    for refresh, k in kinds.items():
+        if not k["ms"]:
+            continue
+        n = mean(k["n_sal"])
+        T = Tk if refresh else Tq
+        attn_ms = k["attn"][0] / max(k["attn"][1], 1)
+        af = _attn_flops(T, L, HD, n, n / cfg["batch"])
+        per[refresh] = dict(ms=mean(k["ms"]), n=n, attn_ms=attn_ms, attn_flops=af,
+                            attn_tf=af / (attn_ms * 1e-3) / 1e12, gate_ms=mean(k["gate"]),
+                            down_ms=mean(k["down"]), gu_flops=2.0 * n * hid * 2 * inter, dn_flops=2.0 * n * inter * hid)
+    q = per[False]
+    print(f"[bench] {ms_per_step:.3f} ms/step at the cadence; Q-pruned {q['ms']:.3f} ms "
+          f"({q['n']:.0f} salient rows/layer), attention {q['attn_ms'] * 1e3:.1f} us -> {q['attn_tf']:.1f} TFLOP/s, "
+          f"gate_up {q['gate_ms'] * 1e3:.1f} us, down {q['down_ms'] * 1e3:.1f} us", file=sys.stderr, flush=True)
+    if True in per:
+        r = per[True]
+        print(f"[bench] refresh {r['ms']:.3f} ms, attention {r['attn_ms'] * 1e3:.1f} us -> {r['attn_tf']:.1f} TFLOP/s",
+              file=sys.stderr, flush=True)
+    avg_n = q["n"]
     gate_bm = _lib.load().dyllm_ffn_tile_rows(int(round(avg_n)), 2 * inter, hid, 1)
-    achieved = flops / (avg_gate_ms * 1e-3) / 1e12
-    print(f"[bench] {ms_per_step:.3f} ms/step, avg salient rows per layer {avg_n:.1f}, "
-          f"attention {avg_attn_ms * 1e3:.1f} us -> {attn_tf:.1f} TFLOP/s, "
-          f"gate_up {avg_gate_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    down_bm = _lib.load().dyllm_ffn_tile_rows(int(round(avg_n)), hid, inter, 0)
 
-    kv_proj = time_kv_projection(cfg, int(round(avg_n)))
-    print(f"[bench] kv projection ({kv_proj['rows']} rows): {kv_proj['avg_launch_us']:.1f} us -> "
-          f"{kv_proj['achieved']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    def rf(kernel, flops, ms, traffic=None, algo_bytes=None, note=None):
+        tf = flops / (ms * 1e-3) / 1e12
+        d = {"kernel": kernel, "bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS,
+             "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+             "avg_launch_us": round(ms * 1e3, 2), "flop_per_launch": flops}
+        if traffic is not None:
+            d["traffic_unit"] = "bytes per launch (PMC)"
+        if algo_bytes is not None:
+            d["algorithmic_bytes"] = algo_bytes
+        if note:
+            d["note"] = note
+        return d
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        del wl
-        torch.cuda.empty_cache()
-        threads = min(16, os.cpu_count() or 1)
-        print(f"[bench] CPU baseline on {threads} threads", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(cfg, int(round(avg_n)), threads)
-
-    rf_attn = {"kernel": "attention_step_kernel<4> (fused step: row-sparse + column-sparse tiles)",
-               "bound": "mfma", "achieved": round(attn_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-               "frac": round(attn_tf / PEAK_BF16_TFLOPS, 4), "traffic": ATTN_TRAFFIC_BYTES,
-               "traffic_unit": "bytes per launch (PMC)", "algorithmic_bytes": 345.0e6,
-               "avg_launch_us": round(avg_attn_ms * 1e3, 2), "flop_per_launch": attn_flops,
-               "note": "VALU/latency bound (softmax over all query-key pairs); frac counts algorithmic "
-                       "MFMA work only"}
-    rf_gate = {"kernel": f"gemm_kernel<{gate_bm},4,SwiGLU> (gathered gate_up + SiLU*up, tile {gate_bm}x256)",
-               "bound": "mfma",
-               "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-               "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
-               "traffic_unit": "bytes per launch (PMC)", "algorithmic_bytes": 231.4e6,
-               "avg_launch_us": round(avg_gate_ms * 1e3, 2),
-               "flop_per_launch": flops}
+    rf_attn = rf("attention_step_kernel<4> (fused Q-pruned step: row-sparse + column-sparse tiles)",
+                 q["attn_flops"], q["attn_ms"], ATTN_TRAFFIC_BYTES, 345.0e6,
+                 "bound by its VALU plus MFMA issue (softmax over all query-key pairs); frac counts algorithmic "
+                 "MFMA work only")
+    rf_gate = rf(f"gemm_kernel<{gate_bm},4,SwiGLU> (gathered gate_up + SiLU*up, tile {gate_bm}x256)",
+                 q["gu_flops"], q["gate_ms"], GATE_UP_TRAFFIC_BYTES, 231.4e6)
+    rf_down = rf(f"gemm_kernel<{down_bm},4,Store> down + FFN-cache scatter (+ split-K reduction)",
+                 q["dn_flops"], q["down_ms"])
     # the dominant kernel (longest mean launch) carries "roofline", the other one rides along
-    if avg_attn_ms >= avg_gate_ms:
+    if q["attn_ms"] >= q["gate_ms"]:
         rf_main, rf_other_key, rf_other = rf_attn, "roofline_gate_up", rf_gate
     else:
         rf_main, rf_other_key, rf_other = rf_gate, "roofline_attention", rf_attn
+    extra = {}
+    if True in per:
+        r = per[True]
+        extra["refresh_step"] = {"ms_per_step": round(r["ms"], 4), "tokens_per_s": round(Tq / (r["ms"] / 1e3), 1),
+                                 "queried_rows": Tk, "avg_salient_rows_per_layer": round(r["n"], 1),
+                                 "roofline_attention": rf("attention_step_kernel<4> (fused refresh step, every row "
+                                                          "queried)", r["attn_flops"], r["attn_ms"])}
+    extra["q_pruned_step"] = {"ms_per_step": round(q["ms"], 4), "tokens_per_s": round(Tq / (q["ms"] / 1e3), 1)}
+    del wl
+    torch.cuda.empty_cache()
+    extra["roofline_down"] = rf_down
+    extra["roofline_dense_attention"] = time_dense_attention(cfg)
+    extra["roofline_moe_config3"] = time_moe()
+    kv_proj = time_kv_projection(cfg, int(round(avg_n)))
+    print(f"[bench] dense attention {extra['roofline_dense_attention']['avg_launch_us']:.1f} us, "
+          f"MoE (config 3) {extra['roofline_moe_config3']['avg_launch_us']:.1f} us -> "
+          f"{extra['roofline_moe_config3']['achieved']:.1f} TFLOP/s, kv projection {kv_proj['avg_launch_us']:.1f} us",
+          file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the box allots 16 host threads to a one-GPU job (OMP_NUM_THREADS); os.cpu_count() counts
+        # the whole host, whose cores other jobs share
+        threads = min(int(os.environ.get("OMP_NUM_THREADS", "16") or 16), os.cpu_count() or 1)
+        print(f"[bench] CPU baseline on {threads} threads (host reports {os.cpu_count()} CPUs)",
+              file=sys.stderr, flush=True)
+        cpu = cpu_baseline(cfg, int(round(avg_n)), threads)
 
     line = {
         "metric": "salient-path tokens/s per denoise step, LLaDA-8B shape bf16; % HBM/MFMA roofline",
@@ -483,12 +653,15 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init N(0,0.02) weights, N(0,1) K/V/Q, 15% perturbed response rows)",
-        "config": {"workload": "config1: LLaDA-8B shape, Q-pruned sparse step over 32 layers",
-                   "layers": layers, "batch": cfg["batch"], "seq_len": cfg["prompt"] + cfg["response"],
-                   "response_len": cfg["response"], "hidden": hid, "heads": cfg["heads"], "ffn": inter,
-                   "tau": cfg["tau"], "avg_salient_rows_per_layer": round(avg_n, 1)},
+        "config": {"workload": "config1: LLaDA-8B shape, sparse denoise steps over 32 layers at the config-1 "
+                               "cadence (3 Q-pruned : 1 refresh)",
+                   "layers": layers, "batch": cfg["batch"], "seq_len": L, "response_len": cfg["response"],
+                   "hidden": hid, "heads": cfg["heads"], "ffn": inter, "tau": cfg["tau"],
+                   "q_pruned_steps": len(kinds[False]["ms"]), "refresh_steps": len(kinds[True]["ms"]),
+                   "avg_salient_rows_per_layer": round(avg_n, 1)},
         "roofline": rf_main,
         rf_other_key: rf_other,
+        **extra,
         "cpu_baseline": cpu,
         "kv_projection": kv_proj,
     }

@@ -84,12 +84,13 @@ class LLaDAMLP(nn.Module):
         y = ops.swiglu_ffn(x.contiguous(), self.gate_up_proj, self.down_proj)
         return self.cache_update(y)
 
-    def forward_salient(self, h_all, gate_up_events=None):
+    def forward_salient(self, h_all, timing=None):
         """Sparse step, fused: h_all = all queried rows after post_attention_layernorm. The
         salient rows are gathered inside the gate_up GEMM and the down GEMM scatters into the FFN
         cache. When the salient set is still on the device (Context.salient_pending), the GEMMs
         read its size from device memory: no host synchronisation.
-        ``gate_up_events`` (start, end) brackets the gathered gate_up GEMM for timing."""
+        ``timing`` (optional): {"gate_up": (start, end), "down": (start, end)} HIP events that
+        bracket the gathered gate_up GEMM and the down GEMM (with its split-K reduction)."""
         ctx = get_context()
         md = get_metadata()
         cm = self.cache_update.cache_manager
@@ -101,13 +102,19 @@ class LLaDAMLP(nn.Module):
             rows, count, hint = ctx.idx_salient_row_i32, None, 0
             kidx = ctx.idx_salient_row_k if ctx.idx_salient_row_k is not None else ctx.idx_salient_row
         h_all = h_all.contiguous()
-        if gate_up_events is not None:
-            gate_up_events[0].record()
+        tg = timing.get("gate_up") if timing else None
+        td = timing.get("down") if timing else None
+        if tg is not None:
+            tg[0].record()
         h = ops.ffn_gate_up(h_all, self.gate_up_proj, rows_idx=rows, count=count, hint=hint)
-        if gate_up_events is not None:
-            gate_up_events[1].record()
+        if tg is not None:
+            tg[1].record()
         dest = cm.dest_rows(md.running_seqs_tensor, kidx, count)
+        if td is not None:
+            td[0].record()
         ops.ffn_down(h, self.down_proj, out=cm._slab, out_rows=dest, count=count, hint=hint)
+        if td is not None:
+            td[1].record()
         cm.finish(md.finished_seqs)
         return self.cache_update.gather_all()
 

@@ -36,7 +36,7 @@ class LLaDAMoESparseBlock(nn.Module):
         """Reference interface: x = gathered salient rows (sparse) or all rows (full)."""
         return self.cache_update(self.experts(x.contiguous()))
 
-    def forward_salient(self, h_all, gate_up_events=None):
+    def forward_salient(self, h_all, timing=None):
         """Sparse step: route the salient rows of ``h_all`` and write the expert outputs
         straight into the FFN cache rows."""
         ctx = get_context()
