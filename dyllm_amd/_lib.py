@@ -61,6 +61,7 @@ SIGNATURES = {
     "dyllm_kv_rope_scatter": [_P, _L, _L, _P, _P, _P, _P, _P, _I, _I, _I, _P, c_float, _P, _P, _P, _P, _P, _I, _P,
                               _P],
     "dyllm_rms_norm": [_P, _L, _P, _L, _P, _L, _I, c_float, _P, _L, _P, _L, _P],
+    "dyllm_rms_norm_cache_rows": [_P, _L, _P, _P, _P, _P, _I, _P, _L, _P, _L, _I, c_float, _P, _L, _P, _L, _P],
     "dyllm_moe_gate": [_P, _P, _L, _I, _P, _I, _I, _I, _P, _P, _P],
     "dyllm_moe_align_block_size": [_P, _L, _I, _I, _P, _L, _P, _P, _P],
     "dyllm_fused_experts_workspace_bytes": [_L, _I, _I, _I, _I],

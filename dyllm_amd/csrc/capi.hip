@@ -795,6 +795,49 @@ int dyllm_rms_norm(const void* x, int64_t ld_x, const void* residual, int64_t ld
   return launch_add_rms_norm(a, DYLLM_STREAM(stream));
 }
 
+int dyllm_rms_norm_cache_rows(const void* cache, int64_t ld_cache, const int64_t* seq_starts, const int64_t* seq_ids,
+                              const int32_t* cu_seqlens_k, const int32_t* cu_seqlens_q, int batch,
+                              const void* residual, int64_t ld_residual, const void* weight, int64_t rows, int hidden,
+                              float eps, void* out, int64_t ld_out, void* residual_out, int64_t ld_residual_out,
+                              void* stream) {
+  DYLLM_REQUIRE(hidden > 0 && hidden % 8 == 0 && hidden <= 8192, "hidden size must be a positive multiple of 8, at most 8192");
+  if (rows <= 0) return 0;
+  DYLLM_NONNULL(cache);
+  DYLLM_NONNULL(seq_starts);
+  DYLLM_NONNULL(seq_ids);
+  DYLLM_NONNULL(cu_seqlens_k);
+  DYLLM_NONNULL(cu_seqlens_q);
+  DYLLM_NONNULL(weight);
+  DYLLM_NONNULL(out);
+  DYLLM_REQUIRE(batch >= 1, "batch must be >= 1");
+  DYLLM_REQUIRE(residual == nullptr || residual_out != nullptr, "residual_out must be given with a residual");
+  DYLLM_REQUIRE(aligned_to(16, {cache, residual, weight, out, residual_out}), "all row buffers and the weight must be 16-byte aligned");
+  DYLLM_REQUIRE(ld_cache >= hidden && ld_cache % 8 == 0 && ld_out >= hidden && ld_out % 8 == 0,
+                "row strides must be >= hidden and multiples of 8");
+  DYLLM_REQUIRE(residual == nullptr || (ld_residual >= hidden && ld_residual % 8 == 0 && ld_residual_out >= hidden &&
+                                        ld_residual_out % 8 == 0),
+                "residual row strides must be >= hidden and multiples of 8");
+  NormArgs a{};
+  a.x = static_cast<const uint16_t*>(cache);
+  a.ld_x = ld_cache;
+  a.x_seq_starts = seq_starts;
+  a.x_seq_ids = seq_ids;
+  a.x_cu_k = cu_seqlens_k;
+  a.x_cu_q = cu_seqlens_q;
+  a.x_batch = batch;
+  a.residual = static_cast<const uint16_t*>(residual);
+  a.ld_r = ld_residual;
+  a.weight = static_cast<const uint16_t*>(weight);
+  a.rows = rows;
+  a.hidden = hidden;
+  a.eps = eps;
+  a.out = static_cast<uint16_t*>(out);
+  a.ld_out = ld_out;
+  a.residual_out = static_cast<uint16_t*>(residual_out);
+  a.ld_ro = ld_residual_out;
+  return launch_add_rms_norm(a, DYLLM_STREAM(stream));
+}
+
 size_t dyllm_linear_workspace_bytes(int64_t rows, int64_t rows_hint, int out_features, int in_features) {
   return dyllm_ffn_down_workspace_bytes(rows, rows_hint, out_features, in_features);
 }

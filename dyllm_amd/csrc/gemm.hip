@@ -62,11 +62,10 @@ __device__ __forceinline__ void bf16x4_to_f32(uint2 v, float* f) {
 __device__ __forceinline__ int swz_chunk(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kGemmBK + (swz_chunk(row, chunk) << 3); }
 
-// One BM x 256 output tile (K slice kz of ksplit).
-template <int BM, int WGN, GemmEpi EPI>
+// One BM x BN output tile (K slice kz of ksplit).
+template <int BM, int BN, int WGN, GemmEpi EPI>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, int nt, int kz) {
   extern __shared__ __attribute__((aligned(16))) uint16_t gsm[];
-  constexpr int BN = kGemmBN;
   constexpr int NW = 2 * WGN;                 // wavefronts: 2 along M x WGN along N
   constexpr int WM = BM / 2, WN = BN / WGN;   // wave tile (rows of A, rows of W)
   constexpr int TM = WM / 32, TN = WN / 32;   // 32x32 MFMA tiles per wave
@@ -90,7 +89,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   // (m >= M, padding ids, n >= N) are clamped to a valid row: their products are never stored.
   constexpr int CA = BM / (8 * NW), CW = BN / (8 * NW);  // 1 KB blocks per wavefront per K slice
   const int lrow = lane >> 3;
-  const uint16_t* a_src[CA];
+  // per-lane source of each 1 KB block: the A row (gathered) and W row, kept as 32-bit row
+  // numbers (the host checks rows * leading dimension < 2^31) so the 1-wave-per-SIMD tiles keep
+  // their registers for the accumulators; the chunk offset is the same for every block
+  int a_row[CA];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
     const int64_t m = m0 + (w + NW * i) * 8 + lrow;
@@ -102,9 +104,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
         row = (id < g.id_limit) ? id / g.a_div : 0;
       }
     }
-    a_src[i] = g.A + row * g.lda + int64_t(k_begin) * kGemmBK + swz_chunk((w + NW * i) * 8 + lrow, lane & 7) * 8;
+    a_row[i] = int(row);
   }
-  const uint16_t* w_src[CW];
+  int w_row[CW];
 #pragma unroll
   for (int i = 0; i < CW; ++i) {
     const int r = (w + NW * i) * 8 + lrow;
@@ -114,8 +116,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     else
       wrow = int64_t(nt) * BN + r;
     if (wrow >= g.N) wrow = 0;
-    w_src[i] = Wb + wrow * g.ldw + int64_t(k_begin) * kGemmBK + swz_chunk(r, lane & 7) * 8;
+    w_row[i] = int(wrow);
   }
+  // (w + NW * i) * 8 + lrow == lrow (mod 8): the swizzled chunk of a lane is the same in every block
+  const int lane_chunk = swz_chunk(w * 8 + lrow, lane & 7) * 8;
+  const uint16_t* const a_base = g.A + int64_t(k_begin) * kGemmBK + lane_chunk;
+  const uint16_t* const w_base = Wb + int64_t(k_begin) * kGemmBK + lane_chunk;
   typedef __attribute__((address_space(3))) void lds_void;
   typedef const __attribute__((address_space(1))) void glb_void;
   // LDS: A slices double-buffered, W slices (streamed from HBM) triple-buffered so their loads
@@ -127,7 +133,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     uint16_t* As = a_lds + buf * (BM * kGemmBK);
 #pragma unroll
     for (int i = 0; i < CA; ++i)
-      __builtin_amdgcn_global_load_lds((glb_void*)(a_src[i] + ko),
+      __builtin_amdgcn_global_load_lds((glb_void*)(a_base + int64_t(a_row[i]) * g.lda + ko),
                                        (lds_void*)(As + (w + NW * i) * 8 * kGemmBK), 16, 0, 0);
   };
   auto stage_w = [&](int kt, int buf) {
@@ -135,7 +141,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     uint16_t* Ws = w_lds + buf * (BN * kGemmBK);
 #pragma unroll
     for (int i = 0; i < CW; ++i)
-      __builtin_amdgcn_global_load_lds((glb_void*)(w_src[i] + ko),
+      __builtin_amdgcn_global_load_lds((glb_void*)(w_base + int64_t(w_row[i]) * g.ldw + ko),
                                        (lds_void*)(Ws + (w + NW * i) * 8 * kGemmBK), 16, 0, 0);
   };
 
@@ -171,15 +177,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
 #pragma unroll
       for (int j = 0; j < TM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[i], af[j], acc[i][j], 0, 0, 0);
   };
-  // one MFMA, one LDS read, ... for the TN+TM reads, then the remaining MFMAs
+  // the TN+TM LDS reads of the next substep spread evenly over this substep's TN*TM MFMAs
+  // (one read after every RS MFMAs), then the remaining MFMAs
+  constexpr int RS = (TN * TM) / (TN + TM) > 0 ? (TN * TM) / (TN + TM) : 1;
   auto interleave = [&]() {
 #pragma unroll
     for (int r = 0; r < TN + TM; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, RS, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
 #pragma unroll
-    for (int r = TN + TM; r < TN * TM; ++r) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    for (int r = (TN + TM) * RS; r < TN * TM; ++r) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
   };
 
   // The per-slice synchronisation is an s_barrier preceded by explicit waits, not
@@ -189,12 +197,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   // the LDS ping-pong needs; the workgroup-scope fences of __syncthreads() cost 2-4 % of the step.
   // Loads complete in issue order, so vmcnt(CW) at the end of slice kt leaves only the W loads
   // of slice kt+2 (issued last) in flight: A and W of slice kt+1 have landed.
-  static_assert(CW == 4, "vmcnt immediate below assumes 4 W blocks per wavefront");
+  static_assert(CW == 4 || CW == 6 || CW == 8, "vmcnt immediates below cover 4, 6 or 8 W blocks per wavefront");
+  auto wait_w_in_flight = [&]() {   // vmcnt(CW): only the newest CW loads (W of slice kt+2) in flight
+    if constexpr (CW == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else if constexpr (CW == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  };
   stage_a(0, 0);
   stage_w(0, 0);
   if (nk > 1) {
     stage_w(1, 1);
-    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    wait_w_in_flight();
   } else {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
@@ -228,7 +241,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     // this wave's LDS reads of the current slice are done before any wave refills its buffers
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (kt + 2 < nk) {
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      wait_w_in_flight();
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
@@ -316,10 +329,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
 // the GEMM is enqueued without the host knowing M. Tiles are split into 8 contiguous ranges,
 // one per XCD (workgroup b runs on XCD b % 8), ordered split-K slice > N tile > M tile, so the
 // M tiles that share a weight slice run together on one XCD and read it from HBM once.
-template <int BM, int WGN, GemmEpi EPI>
-__global__ __launch_bounds__(128 * WGN) void gemm_kernel(GemmArgs g) {
+template <int BM, int BN, int WGN, GemmEpi EPI>
+__global__ __launch_bounds__(128 * WGN) __attribute__((amdgpu_waves_per_eu(WGN == 2 ? 1 : 2, WGN == 2 ? 1 : 2)))
+void gemm_kernel(GemmArgs g) {
   const int64_t M = g.num_m_dev ? min(int64_t(g.num_m_dev[0]), g.M) : g.M;   // never past the host capacity
-  const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (kGemmBN / 2)) : int(cdiv(g.N, kGemmBN));
+  const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (BN / 2)) : int(cdiv(g.N, BN));
   const int mtr = int(cdiv(M, BM));
   const int64_t total = int64_t(mtr) * n_tiles * g.ksplit;
   const int P = gridDim.x;
@@ -340,7 +354,7 @@ __global__ __launch_bounds__(128 * WGN) void gemm_kernel(GemmArgs g) {
     const int64_t rest = t / mtr;
     const int nt = int(rest % n_tiles);
     const int kz = int(rest / n_tiles);
-    gemm_tile<BM, WGN, EPI>(g, M, mt, nt, kz);
+    gemm_tile<BM, BN, WGN, EPI>(g, M, mt, nt, kz);
   }
 }
 
@@ -389,27 +403,27 @@ static int num_cus() {
   return n;
 }
 
-static constexpr size_t lds_bytes(int bm) { return size_t(2 * bm + 3 * kGemmBN) * kGemmBK * sizeof(uint16_t); }
+static constexpr size_t lds_bytes(int bm, int bn) { return size_t(2 * bm + 3 * bn) * kGemmBK * sizeof(uint16_t); }
 
-template <int BM, int WGN, GemmEpi EPI>
+template <int BM, int BN, int WGN, GemmEpi EPI>
 static int launch_gemm_cfg(const GemmArgs& g0, int64_t m_tiles, int ksplit, hipStream_t s) {
   GemmArgs g = g0;
   g.ksplit = ksplit;
   g.m_pad = m_tiles * BM;
-  const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (kGemmBN / 2)) : int(cdiv(g.N, kGemmBN));
+  const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (BN / 2)) : int(cdiv(g.N, BN));
   const int64_t tiles = m_tiles * n_tiles * ksplit;
   if (tiles == 0) return 0;
   int64_t nwg = tiles < num_cus() ? tiles : num_cus();
   if (nwg >= 8) nwg &= ~int64_t(7);
-  const size_t lds = lds_bytes(BM);
+  const size_t lds = lds_bytes(BM, BN);
   static bool attr_set = false;
   if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, WGN, EPI>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WGN, EPI>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
       return fail("hipFuncSetAttribute(max dynamic LDS) failed for the GEMM kernel");
     attr_set = true;
   }
-  gemm_kernel<BM, WGN, EPI><<<unsigned(nwg), 128 * WGN, lds, s>>>(g);
+  gemm_kernel<BM, BN, WGN, EPI><<<unsigned(nwg), 128 * WGN, lds, s>>>(g);
   if (int rc = check_launch("gemm_kernel")) return rc;
   if (ksplit > 1) {
     const int64_t threads = m_tiles * BM * (g.N / 4);
@@ -480,13 +494,23 @@ int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, int
   if (epi == GemmEpi::SwiGLU) {
     DYLLM_REQUIRE(g.N == 2 * g.half_n, "SwiGLU weight must hold gate rows then up rows (N = 2 * intermediate)");
     DYLLM_REQUIRE(g.half_n % (kGemmBN / 2) == 0, "SwiGLU intermediate size must be a multiple of 128");
-    if (tile_m == 256) return launch_gemm_cfg<256, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
-    if (tile_m == 192) return launch_gemm_cfg<192, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
-    return launch_gemm_cfg<128, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
+#ifdef DYLLM_GEMM_W4
+    if (tile_m == 256) return launch_gemm_cfg<256, 256, 2, GemmEpi::SwiGLU>(g, mt, 1, s);
+    if (tile_m == 192) return launch_gemm_cfg<192, 256, 2, GemmEpi::SwiGLU>(g, mt, 1, s);
+#else
+    if (tile_m == 256) return launch_gemm_cfg<256, 256, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
+    if (tile_m == 192) return launch_gemm_cfg<192, 256, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
+#endif
+    return launch_gemm_cfg<128, 256, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
   }
-  if (tile_m == 256) return launch_gemm_cfg<256, 4, GemmEpi::Store>(g, mt, ksplit, s);
-  if (tile_m == 192) return launch_gemm_cfg<192, 4, GemmEpi::Store>(g, mt, ksplit, s);
-  return launch_gemm_cfg<128, 4, GemmEpi::Store>(g, mt, ksplit, s);
+#ifdef DYLLM_GEMM_W4
+  if (tile_m == 256) return launch_gemm_cfg<256, 256, 2, GemmEpi::Store>(g, mt, ksplit, s);
+  if (tile_m == 192) return launch_gemm_cfg<192, 256, 2, GemmEpi::Store>(g, mt, ksplit, s);
+#else
+  if (tile_m == 256) return launch_gemm_cfg<256, 256, 4, GemmEpi::Store>(g, mt, ksplit, s);
+  if (tile_m == 192) return launch_gemm_cfg<192, 256, 4, GemmEpi::Store>(g, mt, ksplit, s);
+#endif
+  return launch_gemm_cfg<128, 256, 4, GemmEpi::Store>(g, mt, ksplit, s);
 }
 
 }  // namespace dyllm

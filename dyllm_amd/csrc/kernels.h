@@ -33,6 +33,14 @@ struct NormArgs {
   int64_t ld_out;
   uint16_t* residual_out;    // with residual: [rows, ld_ro] = bf16(x + residual) (may alias residual)
   int64_t ld_ro;
+  // optional: x rows read from a per-layer row cache instead (x = the cache slab, rows ld_x apart):
+  // packed row r of sequence b = segment of cu_q holding r reads cache row
+  // seq_starts[seq_ids[b]] + (Lk_b - Lq_b) + (r - cu_q[b])  (the tail block, get_block)
+  const int64_t* x_seq_starts;
+  const int64_t* x_seq_ids;
+  const int32_t* x_cu_k;
+  const int32_t* x_cu_q;
+  int x_batch;
 };
 int launch_add_rms_norm(const NormArgs& a, hipStream_t s);
 // Salient-row K/V epilogue: k -> (k_norm) -> rotary -> K-cache row, v -> v_out (rope.hip).

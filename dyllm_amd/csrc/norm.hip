@@ -6,6 +6,9 @@
 // in one pass over the row (the reference's torch ops read and write the [T, hidden] tensors
 // several times). One 256-thread workgroup per row, 16-byte loads, up to 4 chunks of 8 values
 // per thread (hidden <= 8192), the sum of squares reduced over the workgroup in a fixed order.
+// x may also be read straight from a per-layer row cache through the tail-block addressing of
+// get_block (the FFN-output cache of a sparse step), so the packed copy of those rows that the
+// reference hands to the next layer's norm (mlp_cache_manage.py:33-38) is never made.
 #include "kernels.h"
 
 namespace dyllm {
@@ -17,7 +20,13 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(NormArgs a) 
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x;
   const int nch = a.hidden / 8;
-  const uint4* xr = reinterpret_cast<const uint4*>(a.x + row * a.ld_x);
+  int64_t xrow = row;
+  if (a.x_seq_starts) {   // the row lives in a cache slab (uniform across the workgroup)
+    const int b = find_segment(a.x_cu_q, a.x_batch + 1, row);
+    xrow = a.x_seq_starts[a.x_seq_ids[b]] + (a.x_cu_k[b + 1] - a.x_cu_k[b]) - (a.x_cu_q[b + 1] - a.x_cu_q[b]) +
+           (row - a.x_cu_q[b]);
+  }
+  const uint4* xr = reinterpret_cast<const uint4*>(a.x + xrow * a.ld_x);
   const uint4* rr = a.residual ? reinterpret_cast<const uint4*>(a.residual + row * a.ld_r) : nullptr;
   float v[kNormMaxChunks][8];
   float ss = 0.f;

@@ -4,6 +4,7 @@ are returned (stale rows from the cache, fresh rows just computed)."""
 import torch
 from torch import nn
 
+from ... import ops
 from ...engine.cache_manager import CacheManager
 from ...utils.context import get_context
 from ...utils.metadata import get_metadata
@@ -25,11 +26,16 @@ class MLPcache(nn.Module):
         md = get_metadata()
         return self.cache_manager.dest_rows(md.running_seqs_tensor, self.salient_rows())
 
-    def gather_all(self):
-        """All queried rows, packed (mlp_cache_manage.py:33/38)."""
+    def gather_all(self, lazy: bool = False):
+        """All queried rows, packed (mlp_cache_manage.py:33/38). With ``lazy``, a Q-pruned step
+        returns them as ``ops.CacheRows`` (read in place by the next layer's norm, no copy)."""
         ctx = get_context()
         md = get_metadata()
         if ctx.q_pruned:
+            if lazy:
+                cm = self.cache_manager
+                return ops.CacheRows(cm._slab, cm.seq_start_gpu, md.running_seqs_tensor, ctx.cu_seqlens_k,
+                                     ctx.cu_seqlens_q, ctx.total_seqlen)
             return self.cache_manager.get_seqs_block(md.running_seqs_tensor)
         return self.cache_manager.get_seqs(md.running_seqs_tensor, md.running_seqs)
 

@@ -39,6 +39,10 @@ class RMSNorm(nn.Module):
 
     def forward(self, x, residual=None):
         hidden = x.shape[-1]
+        if isinstance(x, ops.CacheRows):   # rows read in place from a layer's FFN cache
+            if residual is None:
+                return ops.rms_norm(x, self.weight, self.eps)
+            return ops.rms_norm(x, self.weight, self.eps, residual=residual.reshape(-1, hidden).contiguous())
         if x.is_cuda and x.dtype == torch.bfloat16 and 1024 <= hidden <= 8192 and hidden % 8 == 0:
             # decoder-layer norms over the hidden size: one native pass per row (dyllm_rms_norm)
             x2 = x.reshape(-1, hidden).contiguous()
@@ -84,13 +88,14 @@ class LLaDAMLP(nn.Module):
         y = ops.swiglu_ffn(x.contiguous(), self.gate_up_proj, self.down_proj)
         return self.cache_update(y)
 
-    def forward_salient(self, h_all, timing=None):
+    def forward_salient(self, h_all, timing=None, lazy=False):
         """Sparse step, fused: h_all = all queried rows after post_attention_layernorm. The
         salient rows are gathered inside the gate_up GEMM and the down GEMM scatters into the FFN
         cache. When the salient set is still on the device (Context.salient_pending), the GEMMs
         read its size from device memory: no host synchronisation.
         ``timing`` (optional): {"gate_up": (start, end), "down": (start, end)} HIP events that
-        bracket the gathered gate_up GEMM and the down GEMM (with its split-K reduction)."""
+        bracket the gathered gate_up GEMM and the down GEMM (with its split-K reduction).
+        ``lazy``: return the queried rows of a Q-pruned step as ``ops.CacheRows`` (no copy)."""
         ctx = get_context()
         md = get_metadata()
         cm = self.cache_update.cache_manager
@@ -116,7 +121,7 @@ class LLaDAMLP(nn.Module):
         if td is not None:
             td[1].record()
         cm.finish(md.finished_seqs)
-        return self.cache_update.gather_all()
+        return self.cache_update.gather_all(lazy)
 
 
 class LLaDAAttention(nn.Module):
@@ -201,7 +206,8 @@ class LLaDADecoderLayer(nn.Module):
         if get_context().is_full:
             hidden = self.mlp(hidden)
         else:
-            hidden = self.mlp.forward_salient(hidden)
+            # the FFN rows stay in the FFN cache: the next norm reads them in place
+            hidden = self.mlp.forward_salient(hidden, lazy=True)
         return hidden, residual
 
 

@@ -36,7 +36,7 @@ class LLaDAMoESparseBlock(nn.Module):
         """Reference interface: x = gathered salient rows (sparse) or all rows (full)."""
         return self.cache_update(self.experts(x.contiguous()))
 
-    def forward_salient(self, h_all, timing=None):
+    def forward_salient(self, h_all, timing=None, lazy=False):
         """Sparse step: route the salient rows of ``h_all`` and write the expert outputs
         straight into the FFN cache rows."""
         ctx = get_context()
@@ -46,7 +46,7 @@ class LLaDAMoESparseBlock(nn.Module):
         dest = self.cache_update.dest_rows()
         self.experts(x, out=cm._slab, out_rows=dest)
         cm.finish(md.finished_seqs)
-        return self.cache_update.gather_all()
+        return self.cache_update.gather_all(lazy)
 
 
 class LLaDAMoEDecoderLayer(LLaDADecoderLayer):

@@ -573,11 +573,29 @@ def kv_rope_scatter(kv, num_kv_heads, positions, cos, sin, k_cache, k_rows, cu_s
     return v_out
 
 
+class CacheRows:
+    """The queried rows of a per-layer row cache, not copied out: packed row r of sequence b reads
+    slab row seq_starts[seq_ids[b]] + (Lk_b - Lq_b) + (r - cu_q[b]) (get_block addressing). The
+    consumer (``rms_norm``) reads them in place; ``materialize()`` makes the packed copy."""
+
+    def __init__(self, slab, seq_starts, seq_ids, cu_seqlens_k, cu_seqlens_q, rows):
+        self.slab, self.seq_starts, self.seq_ids = slab, seq_starts, seq_ids
+        self.cu_k, self.cu_q = _i32(cu_seqlens_k), _i32(cu_seqlens_q)
+        self.rows = int(rows)
+        self.shape = (self.rows, slab.shape[1])
+        self.dtype, self.device = slab.dtype, slab.device
+
+    def materialize(self):
+        return get_block_cuda(self.slab, self.seq_starts, self.cu_k, self.cu_q, self.seq_ids, self.rows)
+
+
 def rms_norm(x, weight, eps, residual=None, out=None, residual_out=None):
     """RMSNorm (layernorm.py:15-24) or, with ``residual``, the fused add + RMSNorm
     (layernorm.py:29-37) in one pass per row (dyllm_rms_norm). Returns y, or (y, residual_out)
     with residual_out = bf16(x + residual); ``out`` / ``residual_out`` may be x / residual
-    (in place)."""
+    (in place). ``x`` may be a ``CacheRows`` (rows read from the cache in place)."""
+    if isinstance(x, CacheRows):
+        return _rms_norm_cache_rows(x, weight, eps, residual, out, residual_out)
     _check(x, "x", torch.bfloat16, 2)
     _check(weight, "weight", torch.bfloat16, 1)
     rows, hidden = x.shape
@@ -596,6 +614,31 @@ def rms_norm(x, weight, eps, residual=None, out=None, residual_out=None):
             residual_out = torch.empty_like(residual)
     if rows:
         _lib.call("dyllm_rms_norm", _ptr(x), x.stride(0), _ptr(residual),
+                  residual.stride(0) if residual is not None else 0, _ptr(weight), rows, hidden, float(eps),
+                  _ptr(out), out.stride(0), _ptr(residual_out),
+                  residual_out.stride(0) if residual_out is not None else 0, _stream())
+    return out if residual is None else (out, residual_out)
+
+
+def _rms_norm_cache_rows(x, weight, eps, residual, out, residual_out):
+    _check(weight, "weight", torch.bfloat16, 1)
+    rows, hidden = x.shape
+    if weight.numel() != hidden or not weight.is_contiguous():
+        raise RuntimeError("weight must be a contiguous [hidden] tensor")
+    if x.slab.stride(1) != 1:
+        raise RuntimeError("cache rows must be contiguous")
+    if out is None:
+        out = torch.empty(rows, hidden, dtype=torch.bfloat16, device=x.device)
+    _check(out, "out", torch.bfloat16, 2)
+    if residual is not None:
+        _check(residual, "residual", torch.bfloat16, 2)
+        if tuple(residual.shape) != (rows, hidden) or residual.stride(1) != 1:
+            raise RuntimeError("residual must be [rows, hidden] with contiguous rows")
+        if residual_out is None:
+            residual_out = torch.empty_like(residual)
+    if rows:
+        _lib.call("dyllm_rms_norm_cache_rows", _ptr(x.slab), x.slab.stride(0), _ptr(x.seq_starts), _ptr(x.seq_ids),
+                  _ptr(x.cu_k), _ptr(x.cu_q), x.cu_q.numel() - 1, _ptr(residual),
                   residual.stride(0) if residual is not None else 0, _ptr(weight), rows, hidden, float(eps),
                   _ptr(out), out.stride(0), _ptr(residual_out),
                   residual_out.stride(0) if residual_out is not None else 0, _stream())

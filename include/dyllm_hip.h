@@ -288,6 +288,17 @@ int dyllm_rms_norm(const void* x, int64_t ld_x, const void* residual, int64_t ld
                    int64_t rows, int hidden, float eps, void* out, int64_t ld_out, void* residual_out,
                    int64_t ld_residual_out, void* stream);
 
+/* The same norm with x read from a per-layer row cache (no reference counterpart: it removes
+ * the packed copy of the cached FFN rows, mlp_cache_manage.py:33-38, that the reference hands to
+ * the next layer's norm). Packed row r, of sequence b (cu_seqlens_q[b] <= r < cu_seqlens_q[b+1]),
+ * reads cache row seq_starts[seq_ids[b]] + (Lk_b - Lq_b) + (r - cu_seqlens_q[b]), the tail-block
+ * addressing of dyllm_get_block (Lq == Lk: the whole sequence, dyllm_get_seqs). */
+int dyllm_rms_norm_cache_rows(const void* cache, int64_t ld_cache, const int64_t* seq_starts, const int64_t* seq_ids,
+                              const int32_t* cu_seqlens_k, const int32_t* cu_seqlens_q, int batch,
+                              const void* residual, int64_t ld_residual, const void* weight, int64_t rows, int hidden,
+                              float eps, void* out, int64_t ld_out, void* residual_out, int64_t ld_residual_out,
+                              void* stream);
+
 /* ---- MoE ------------------------------------------------------------------------------- */
 
 /* Router: topk_weights (bf16) / topk_ids (int32) [tokens, top_k] from fp32 softmax of

@@ -45,3 +45,41 @@ def test_rms_norm_in_place(dev):
     y_want, ro_want = ref.add_rms_norm(x, r, w, 1e-6)
     assert torch.equal(rd.cpu(), ro_want)
     assert_bf16_close(xd.cpu(), y_want, what="in place")
+
+
+@pytest.mark.parametrize("refresh", [False, True])
+def test_rms_norm_reads_cache_rows_in_place(dev, refresh):
+    """x read straight from a row cache through the tail-block addressing (ops.CacheRows): the
+    same bits as the norm of the packed copy (dyllm_get_block / get_seqs), for a ragged batch whose
+    sequences sit in the slab out of batch order."""
+    from dyllm_amd import ops
+
+    print(f"[rms_norm] cache rows refresh={refresh}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    hidden = 4096
+    lens_k, lens_q = [300, 41, 129], [200, 41, 1]
+    if refresh:
+        lens_q = lens_k
+    seq_ids = [5, 0, 2]
+    starts = torch.full((8,), -1, dtype=torch.long)
+    pos = 7
+    for sid, L in zip([2, 5, 0], [lens_k[2], lens_k[0], lens_k[1]]):     # slab order differs from batch order
+        starts[sid] = pos
+        pos += L + 3
+    slab = (2 * torch.randn(pos + 5, hidden, generator=g)).to(BF)
+    cu_k = torch.tensor([0, 300, 341, 470], dtype=torch.int32)
+    cu_q = torch.tensor([0] + list(torch.tensor(lens_q).cumsum(0).tolist()), dtype=torch.int32)
+    T = int(cu_q[-1])
+    r = torch.randn(T, hidden, generator=g).to(BF)
+    w = (1 + 0.2 * torch.randn(hidden, generator=g)).to(BF)
+    sd, std, sid, ckd, cqd = (t.to(dev) for t in (slab, starts, torch.tensor(seq_ids), cu_k, cu_q))
+    rows = ops.CacheRows(sd, std, sid, ckd, cqd, T)
+    packed = rows.materialize()
+    want_p = ref.get_block(slab, starts, cu_k, cu_q, seq_ids, T)
+    assert torch.equal(packed.cpu(), want_p)
+    y, ro = ops.rms_norm(rows, w.to(dev), 1e-5, residual=r.to(dev))
+    y2, ro2 = ops.rms_norm(packed, w.to(dev), 1e-5, residual=r.to(dev))
+    y3 = ops.rms_norm(rows, w.to(dev), 1e-5)
+    y4 = ops.rms_norm(packed, w.to(dev), 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), y2.cpu()) and torch.equal(ro.cpu(), ro2.cpu()) and torch.equal(y3.cpu(), y4.cpu())
