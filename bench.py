@@ -118,11 +118,12 @@ def build_workload(cfg, layers, device, seed=0):
         resp = torch.cat([torch.arange(b * L + P, (b + 1) * L, device=device) for b in range(B)])
         q = q_all[resp].contiguous()
         q_full = q_all     # the refresh step queries every row
-        k_new = (k_all[resp].float() + 0.1 * randn(Tq, Hkv, D).float()).to(torch.bfloat16)
-        v_new = (v_all[resp].float() + 0.1 * randn(Tq, Hkv, D).float()).to(torch.bfloat16)
+        # stand-in for the salient-row K/V projection output: kv rows [k | v] of every K row
+        # (addressed by K-space salient index in both step kinds, so any salient set is in range)
+        k_new = (k_all.float() + 0.1 * randn(Tk, Hkv, D).float()).to(torch.bfloat16)
+        v_new = (v_all.float() + 0.1 * randn(Tk, Hkv, D).float()).to(torch.bfloat16)
         del k_all, v_all
-        # stand-in for the salient-row K/V projection output: kv rows [k | v] of every queried row
-        kv_all = torch.cat([k_new.view(Tq, -1), v_new.view(Tq, -1)], dim=1).contiguous()
+        kv_all = torch.cat([k_new.view(Tk, -1), v_new.view(Tk, -1)], dim=1).contiguous()
         del k_new, v_new
         state.append(dict(attn=attn, k_cache=k_cache, mlp=mlp, q=q, q_full=q_full, kv_all=kv_all,
                           c_saved=attn.context_cache.cache.clone(), v_saved=attn.v_cache.cache.clone()))
@@ -153,11 +154,6 @@ def build_workload(cfg, layers, device, seed=0):
             st["attn"].context_cache.cache.copy_(st["c_saved"])
             st["attn"].v_cache.cache.copy_(st["v_saved"])
 
-    # Q-space row of every K row (the response rows of the Q-pruned layout), to find the stand-in
-    # projection rows of a K-space salient set
-    q_of_k = torch.full((Tk,), -1, dtype=torch.long, device=device)
-    q_of_k[S_k] = S_q
-
     def step(events=None, n_sal=None, refresh=False):
         ctx = set_sparse_context(refresh)
         T = Tk if refresh else Tq
@@ -167,8 +163,8 @@ def build_workload(cfg, layers, device, seed=0):
                 n_sal.append(idx.numel())
             # the projection's [k | v] rows of the salient set (stand-in: a gather), then the fused
             # epilogue: RoPE + K-cache scatter of k, the compact v of the step
-            kv = ops.gather_rows_2D(st["kv_all"], q_of_k[idx] if refresh else idx)
             kidx = ctx.idx_salient_row if refresh else ctx.idx_salient_row_k
+            kv = ops.gather_rows_2D(st["kv_all"], kidx)
             v_sal = st["k_cache"].scatter_kv_rope(md.running_seqs_tensor, kidx, kv, Hkv, pos0,
                                                   rope_cos, rope_sin, ctx.idx_salient_row_i32)
             k_full = st["k_cache"].get_seqs(md.running_seqs_tensor, md.running_seqs).view(-1, Hkv, D)

@@ -48,7 +48,7 @@ SIGNATURES = {
     "dyllm_reset_block": [_P, _P, _L, _P, _P, _P, _P, _I, _L, _P],
     "dyllm_scatter_update": [_P, _P, _L, _P, _L, _P, _P, _P, _I, _P],
     "dyllm_scatter_dest_rows": [_P, _L, _P, _P, _P, _P, _I, _P, _P],
-    "dyllm_gather_rows": [_P, _P, _L, _P, _L, _P],
+    "dyllm_gather_rows": [_P, _L, _P, _L, _P, _L, _P],
     "dyllm_swiglu_ffn_workspace_bytes": [_L, _I],
     "dyllm_swiglu_ffn": [_P, _L, _P, _L, _P, _P, _I, _I, _P, c_size_t, _P, _P, _P],
     "dyllm_ffn_tile_rows": [_L, _I, _I, _I],

@@ -17,7 +17,7 @@ __device__ __forceinline__ bool map_row(const RowMapArgs& a, int64_t r, int64_t&
   if constexpr (M == RowMap::Gather) {
     src_row = a.row_idx[r];
     dst_row = r;
-    return true;
+    return src_row >= 0 && src_row < a.src_rows;
   } else if constexpr (M == RowMap::Scatter) {
     const int64_t k = a.row_idx[r];
     const int b = find_segment(a.cu, a.B + 1, k);
@@ -61,7 +61,13 @@ __global__ __launch_bounds__(256) void row_map_copy_kernel(RowMapArgs a) {
   const int lane = threadIdx.x & 63;
   if (r >= a.n_rows) return;
   int64_t s, d;
-  if (!map_row<M>(a, r, s, d)) return;
+  if (!map_row<M>(a, r, s, d)) {
+    if constexpr (M == RowMap::Gather) {   // out-of-range index: a zero row, no read
+      uint4* dst = reinterpret_cast<uint4*>(a.dst + r * a.row_bytes);
+      for (int64_t i = lane; i < (a.row_bytes >> 4); i += 64) dst[i] = make_uint4(0, 0, 0, 0);
+    }
+    return;
+  }
   const uint4* src = reinterpret_cast<const uint4*>(a.src + s * a.row_bytes);
   uint4* dst = reinterpret_cast<uint4*>(a.dst + d * a.row_bytes);
   const int64_t n16 = a.row_bytes >> 4;

@@ -103,7 +103,7 @@ int dyllm_attention_timer_read(float* total_ms, int* launches) {
   tm.used = 0;
   return 0;
 }
-int dyllm_abi_version(void) { return 1; }
+int dyllm_abi_version(void) { return 2; }
 
 // ---------------------------------------------------------------------------------------
 size_t dyllm_attention_sparse_workspace_bytes(int batch, int num_heads, int64_t total_q, int max_seqlen_k) {
@@ -510,7 +510,7 @@ int dyllm_fused_offset_launch(const int32_t* idxs, const int32_t* num_idxs, cons
 // ---------------------------------------------------------------------------------------
 static int row_map(RowMap mode, const void* src, void* dst, int64_t row_bytes, int64_t n_rows,
                    const int64_t* seq_starts, const int32_t* cu, const int32_t* cu_q, const int64_t* seq_ids,
-                   const int64_t* row_idx, int batch, void* stream) {
+                   const int64_t* row_idx, int batch, void* stream, int64_t src_rows = 0) {
   DYLLM_NONNULL(src);
   DYLLM_NONNULL(dst);
   DYLLM_REQUIRE(batch >= 0, "batch must be non-negative");
@@ -526,6 +526,7 @@ static int row_map(RowMap mode, const void* src, void* dst, int64_t row_bytes, i
   a.seq_ids = seq_ids;
   a.row_idx = row_idx;
   a.B = batch;
+  a.src_rows = src_rows;
   return launch_row_map(mode, a, DYLLM_STREAM(stream));
 }
 
@@ -587,9 +588,11 @@ int dyllm_scatter_dest_rows(const int64_t* row_idx, int64_t rows, const int32_t*
   return launch_scatter_dest_rows(row_idx, rows, rows_dev, cu_seqlens, seq_starts, seq_ids, batch, dest,
                                   DYLLM_STREAM(stream));
 }
-int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t* idx, int64_t rows, void* stream) {
+int dyllm_gather_rows(const void* x, int64_t x_rows, void* out, int64_t row_bytes, const int64_t* idx, int64_t rows,
+                      void* stream) {
   DYLLM_NONNULL(idx);
-  return row_map(RowMap::Gather, x, out, row_bytes, rows, nullptr, nullptr, nullptr, nullptr, idx, 0, stream);
+  DYLLM_REQUIRE(x_rows >= 0, "x_rows must be non-negative");
+  return row_map(RowMap::Gather, x, out, row_bytes, rows, nullptr, nullptr, nullptr, nullptr, idx, 0, stream, x_rows);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -17,6 +17,7 @@ struct RowMapArgs {
   const int64_t* seq_ids;
   const int64_t* row_idx;
   int B;
+  int64_t src_rows;   // Gather: rows of src (indices outside [0, src_rows) give zero rows)
 };
 int launch_row_map(RowMap mode, const RowMapArgs& a, hipStream_t stream);
 // RMSNorm with the optional fused residual add (norm.hip).

@@ -431,7 +431,7 @@ def gather_rows_2D(x, row_idx):
     ri = _i64(row_idx)
     out = torch.empty((ri.numel(), x.shape[1]), dtype=x.dtype, device=x.device)
     if ri.numel():
-        _lib.call("dyllm_gather_rows", _ptr(x), _ptr(out), _row_bytes(x), _ptr(ri), ri.numel(), _stream())
+        _lib.call("dyllm_gather_rows", _ptr(x), x.shape[0], _ptr(out), _row_bytes(x), _ptr(ri), ri.numel(), _stream())
     return out
 
 

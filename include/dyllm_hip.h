@@ -212,8 +212,10 @@ int dyllm_scatter_update(void* cache, const void* new_vals, int64_t row_bytes, c
 int dyllm_scatter_dest_rows(const int64_t* row_idx, int64_t rows, const int32_t* rows_dev,
                             const int32_t* cu_seqlens, const int64_t* seq_starts, const int64_t* seq_ids, int batch,
                             int64_t* dest, void* stream);
-/* out[m] = x[idx[m]] */
-int dyllm_gather_rows(const void* x, void* out, int64_t row_bytes, const int64_t* idx, int64_t rows, void* stream);
+/* out[m] = x[idx[m]] for the x_rows rows of x; an index outside [0, x_rows) yields a zero row
+ * (the device never reads past x). */
+int dyllm_gather_rows(const void* x, int64_t x_rows, void* out, int64_t row_bytes, const int64_t* idx, int64_t rows,
+                      void* stream);
 
 /* ---- FFN ------------------------------------------------------------------------------- */
 

@@ -79,6 +79,10 @@ def test_cache_ops_exact(dev, D):
     gi = torch.tensor([5, 5, 0, 169], dtype=torch.long)
     got = ops.gather_rows_2D(c_d, gi.to(dev)).cpu()
     assert torch.equal(got, ref.gather_rows_2D(cache, gi))
+    # indices outside [0, rows) give zero rows; the kernel never reads outside x
+    bad = torch.tensor([3, -1, cache.shape[0], 2], dtype=torch.long)
+    got = ops.gather_rows_2D(c_d, bad.to(dev)).cpu()
+    assert torch.equal(got[[0, 3]], cache[[3, 2]]) and not got[[1, 2]].any()
 
 
 # ---------------------------------------------------------------------------------------
