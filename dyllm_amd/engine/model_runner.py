@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from ..config import Config
-from ..model_executor.layers.sampler import DreamSampler, LLaDASampler
+from ..model_executor.layers.sampler import DreamSampler, LLaDASampler, RowLogits
 from ..utils.context import get_context, reset_context, set_context
 from ..utils.metadata import get_metadata
 from .sequence import Sequence
@@ -243,7 +243,9 @@ class ModelRunner:
     # -- execution ------------------------------------------------------------------------
     @torch.inference_mode()
     def run_model(self, input_ids, positions, is_full: bool):
-        return self.model.compute_logits(self.model(input_ids, positions))
+        """Hidden states of every queried row; the LM head runs later on the sampler's candidate
+        rows only (RowLogits)."""
+        return RowLogits(self.model(input_ids, positions), self.model.compute_logits)
 
     def run(self, seqs: List[Sequence], is_full: bool, finished_seqs: Optional[List[int]] = None):
         if is_full:

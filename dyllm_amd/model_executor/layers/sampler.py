@@ -45,6 +45,30 @@ def top_k_logits(logits: torch.Tensor, top_k: Union[int, torch.Tensor, None] = N
     return logits.masked_fill(logits < thr, torch.finfo(logits.dtype).min)
 
 
+class RowLogits:
+    """Logits computed only for the rows the sampler asks for: ``index_select(0, rows)`` runs the LM
+    head on those hidden rows. The reference computes the LM head over every queried row
+    (model_runner.py:375-388) and then keeps the candidate rows (sampler.py:264-266); each logits
+    row depends only on its own hidden row, so the selected rows are the same values. ``shift``
+    (Dream) reads row r from hidden row max(r - shift, 0), the one-row shift of sampler.py:322-326."""
+
+    def __init__(self, hidden: torch.Tensor, compute, shift: int = 0):
+        self.hidden, self.compute, self.shift = hidden, compute, shift
+        self.device = hidden.device
+
+    def size(self, dim: int = 0) -> int:
+        return self.hidden.size(dim) if dim == 0 else self.compute(self.hidden[:1]).size(dim)
+
+    def shifted(self, k: int) -> "RowLogits":
+        return RowLogits(self.hidden, self.compute, self.shift + k)
+
+    def index_select(self, dim: int, rows: torch.Tensor) -> torch.Tensor:
+        assert dim == 0
+        if self.shift:
+            rows = (rows - self.shift).clamp_min(0)
+        return self.compute(self.hidden.index_select(0, rows))
+
+
 class BaseSampler(nn.Module):
 
     def __init__(self, algorithm: str = "confidence"):
@@ -131,6 +155,8 @@ class DreamSampler(BaseSampler):
     packed batch (sampler.py:322-326); sampling is categorical when a temperature is set."""
 
     def adjust_logits(self, logits):
+        if isinstance(logits, RowLogits):
+            return logits.shifted(1)
         if logits.size(0) <= 1:
             return logits
         return torch.cat([logits[:1], logits[:-1]], dim=0)
