@@ -106,6 +106,7 @@ def build_workload(cfg, layers, device, seed=0):
         attn = Attention(H, D, D ** -0.5, Hkv, cfg["tau"], device=device)
         k_cache = CacheManager(Hkv * D, device=torch.device(device))
         mlp = LLaDAMLP(hid, inter, device=device, gen=g)
+        attn.ffn_cache = mlp.cache_update.cache_manager   # the step computes the FFN's scatter rows
         q_all, k_all, v_all = randn(Tk, H, D), randn(Tk, Hkv, D), randn(Tk, Hkv, D)
         k_cache.reset_full(k_all.view(Tk, -1), md.running_seqs_tensor, md.running_seqs)
         attn(q_all, k_all, v_all)

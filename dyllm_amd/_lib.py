@@ -31,11 +31,11 @@ SIGNATURES = {
     "dyllm_sparse_step_workspace_bytes": [_I, _I, _I, _I, _L, _L, _I, _L],
     "dyllm_sparse_attention_step": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I, _L, _L,
                                     _I, _I, _P, _P, _P, _P, c_float, c_float, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                    _P, _P, c_size_t, _P],
+                                    _P, _P, _P, _P, c_size_t, _P],
     "dyllm_sparse_step_scratch_bytes": [],
     "dyllm_sparse_attention_step_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I,
                                             _L, _L, _I, _I, _P, _P, _P, _P, c_float, c_float, _P, _P, _P, _P, _P,
-                                            _P, _P, _P, _P, _P, _P],
+                                            _P, _P, _P, _P, _P, _P, _P, _P],
     "dyllm_v_delta_update": [_P, _P, _P, _L, _L, _P, _P],
     "dyllm_seq_row_starts": [_P, _P, _P, _P, _I, _P, _P],
     "dyllm_cosine_mask": [_P, _L, c_float, _P, _P],

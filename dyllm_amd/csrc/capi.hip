@@ -103,7 +103,7 @@ int dyllm_attention_timer_read(float* total_ms, int* launches) {
   tm.used = 0;
   return 0;
 }
-int dyllm_abi_version(void) { return 2; }
+int dyllm_abi_version(void) { return 3; }
 
 // ---------------------------------------------------------------------------------------
 size_t dyllm_attention_sparse_workspace_bytes(int batch, int num_heads, int64_t total_q, int max_seqlen_k) {
@@ -280,8 +280,9 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                 const int64_t* idx_k64, const int32_t* idx_k32, float softmax_scale, float threshold,
                                 void* out, float* cosine_stats, uint8_t* cosine_out, int64_t* next_idx64,
                                 int32_t* next_idx32, int64_t* next_idx_k64, int32_t* next_idx_k32,
-                                int32_t* next_cu_salientlens, int32_t* next_count, int32_t* host_meta,
-                                void* workspace, size_t workspace_bytes, void* stream) {
+                                int32_t* next_cu_salientlens, int32_t* next_count, const int64_t* dest_seq_starts,
+                                int64_t* next_dest_rows, int32_t* host_meta, void* workspace, size_t workspace_bytes,
+                                void* stream) {
   DYLLM_NONNULL(v_cache);
   DYLLM_NONNULL(v_seq_starts);
   DYLLM_NONNULL(c_seq_starts);
@@ -379,9 +380,12 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
   // statistics reduction, tau test and compaction of the next salient set (attention.py:141-173)
   if (int rc = launch_reduce_stats(cw.part, cosine_stats, cosine_out, total_q, num_heads, threshold, block_counts, s))
     return rc;
+  DYLLM_REQUIRE(next_dest_rows == nullptr || dest_seq_starts != nullptr, "next_dest_rows needs dest_seq_starts");
+  CompactDest dd{};
+  if (next_dest_rows) dd = CompactDest{dest_seq_starts, seq_ids, cu_seqlens_k, next_dest_rows};
   return launch_compact_blocks(cosine_out, total_q, block_counts, cu_seqlens_q, batch, cu_promptlens, next_idx64,
                                next_idx32, q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr,
-                               next_cu_salientlens, next_count, host_meta_dev, s);
+                               next_cu_salientlens, next_count, host_meta_dev, s, dd);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -399,7 +403,8 @@ int dyllm_sparse_attention_step_noalloc(const void* q, const void* k, const int6
                                         float threshold, void* out, float* cosine_stats, uint8_t* cosine_out,
                                         int64_t* next_idx64, int32_t* next_idx32, int64_t* next_idx_k64,
                                         int32_t* next_idx_k32, int32_t* next_cu_salientlens, int32_t* next_count,
-                                        int32_t* host_meta, void* stream) {
+                                        const int64_t* dest_seq_starts, int64_t* next_dest_rows, int32_t* host_meta,
+                                        void* stream) {
   DYLLM_REQUIRE(num_salient >= 0 && batch >= 1 && total_q >= 0 && total_k >= 0, "bad sizes");
   const size_t need = dyllm_sparse_step_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, total_q, total_k,
                                                         max_seqlen_k, num_salient);
@@ -413,8 +418,8 @@ int dyllm_sparse_attention_step_noalloc(const void* q, const void* k, const int6
                                      cu_promptlens, max_seqlen_q, max_seqlen_k, total_q, total_k, num_salient,
                                      max_salientlen, cu_salientlens, idx_q32, idx_k64, idx_k32, softmax_scale,
                                      threshold, out, cosine_stats, cosine_out, next_idx64, next_idx32, next_idx_k64,
-                                     next_idx_k32, next_cu_salientlens, next_count, host_meta, ws, kStepScratchBytes,
-                                     stream);
+                                     next_idx_k32, next_cu_salientlens, next_count, dest_seq_starts, next_dest_rows,
+                                     host_meta, ws, kStepScratchBytes, stream);
 }
 
 size_t dyllm_sparse_step_scratch_bytes(void) { return kStepScratchBytes; }

@@ -309,7 +309,7 @@ __global__ __launch_bounds__(kReduceRows) void compact_blocks_kernel(
     const uint8_t* __restrict__ mask, int64_t T, const int32_t* __restrict__ block_counts,
     const int32_t* __restrict__ cu_q, int B, const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64,
     int32_t* __restrict__ idx32, int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32,
-    int32_t* __restrict__ cu_sal, int32_t* __restrict__ count, int32_t* __restrict__ host_meta) {
+    int32_t* __restrict__ cu_sal, int32_t* __restrict__ count, int32_t* __restrict__ host_meta, CompactDest dd) {
   constexpr int NWV = kReduceRows / 64;
   __shared__ int wtot[NWV];
   __shared__ int part_sh[NWV];
@@ -341,11 +341,15 @@ __global__ __launch_bounds__(kReduceRows) void compact_blocks_kernel(
   if (sal) {
     idx64[pos] = t;
     if (idx32) idx32[pos] = int32_t(t);
-    if (idx_k) {
+    if (idx_k || dd.dest) {
       const int seg = find_segment(cu_q, B + 1, t);
-      const int64_t kk = t + cu_prompt[seg + 1];
-      idx_k[pos] = kk;
-      if (idx_k32) idx_k32[pos] = int32_t(kk);
+      const int64_t kk = idx_k ? t + cu_prompt[seg + 1] : t;   // K-space row (refresh: Q space == K space)
+      if (idx_k) {
+        idx_k[pos] = kk;
+        if (idx_k32) idx_k32[pos] = int32_t(kk);
+      }
+      // row of this salient row in the consumer's cache (the FFN-output scatter target)
+      if (dd.dest) dd.dest[pos] = dd.dest_starts[dd.seq_ids[seg]] + (kk - dd.cu_k[seg]);
     }
   }
   __syncthreads();
@@ -371,12 +375,15 @@ __global__ __launch_bounds__(kReduceRows) void compact_blocks_kernel(
 
 int launch_compact_blocks(const uint8_t* mask, int64_t T, const int32_t* block_counts, const int32_t* cu_q, int B,
                           const int32_t* cu_prompt, int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32,
-                          int32_t* cu_sal, int32_t* count, int32_t* host_meta, hipStream_t s) {
+                          int32_t* cu_sal, int32_t* count, int32_t* host_meta, hipStream_t s,
+                          const CompactDest& dest) {
   DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
   DYLLM_REQUIRE(T >= 1 && T < (int64_t(1) << 31), "row count out of range");
   DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
+  DYLLM_REQUIRE(dest.dest == nullptr || (dest.dest_starts && dest.seq_ids && dest.cu_k),
+                "cache rows need the cache's sequence starts, the sequence ids and cu_seqlens_k");
   compact_blocks_kernel<<<unsigned(cdiv(T, kReduceRows)), kReduceRows, 0, s>>>(
-      mask, T, block_counts, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count, host_meta);
+      mask, T, block_counts, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count, host_meta, dest);
   return check_launch("compact_blocks_kernel");
 }
 

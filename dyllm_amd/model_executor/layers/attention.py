@@ -43,6 +43,9 @@ class Attention(nn.Module):
         self.context_cache = CacheManager(self.num_heads * self.head_dim, device=torch.device(device))
         self.v_cache = CacheManager(self.num_kv_heads * self.head_dim, device=torch.device(device))
         self._bufs = None  # reusable outputs / workspace of the sparse step (ops.StepBuffers)
+        # optional: the FFN-output cache of this layer; the step's compaction then also produces
+        # the rows of the next salient set in it (the FFN's scatter targets)
+        self.ffn_cache = None
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
         ctx = get_context()
@@ -83,7 +86,8 @@ class Attention(nn.Module):
             bufs, q, k, self.v_cache._slab, self.v_cache.seq_start_gpu, v.view(n, self.num_kv_heads, self.head_dim),
             self.context_cache._slab, self.context_cache.seq_start_gpu, seq_ids, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
             ctx.cu_promptlens if q_pruned else None, ctx.max_seqlen_q, ctx.max_seqlen_k, Tk, n, ctx.max_salientlen,
-            ctx.cu_salientlens, idx_q32, idx_k64, idx_k32, self.scale, self.threshold)
+            ctx.cu_salientlens, idx_q32, idx_k64, idx_k32, self.scale, self.threshold,
+            dest_seq_starts=self.ffn_cache.seq_start_gpu if self.ffn_cache is not None else None)
         # the next layer's salient set stays on the device until it is needed (Context.resolve_salient)
         ctx.set_pending(bufs.compacted())
         new_c = bufs.out

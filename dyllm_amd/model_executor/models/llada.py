@@ -114,7 +114,10 @@ class LLaDAMLP(nn.Module):
         h = ops.ffn_gate_up(h_all, self.gate_up_proj, rows_idx=rows, count=count, hint=hint)
         if tg is not None:
             tg[1].record()
-        dest = cm.dest_rows(md.running_seqs_tensor, kidx, count)
+        if comp is not None and comp.dest_rows is not None and comp.dest_starts is cm.seq_start_gpu:
+            dest = comp.dest_rows        # produced by the attention step's compaction
+        else:
+            dest = cm.dest_rows(md.running_seqs_tensor, kidx, count)
         if td is not None:
             td[0].record()
         ops.ffn_down(h, self.down_proj, out=cm._slab, out_rows=dest, count=count, hint=hint)
@@ -190,6 +193,8 @@ class LLaDADecoderLayer(nn.Module):
                                         qkv_bias=cfg.qkv_bias, qk_layernorm=cfg.qk_layernorm,
                                         rms_norm_eps=cfg.rms_norm_eps, device=device, gen=gen)
         self.mlp = self._make_mlp(cfg, device, gen)
+        if isinstance(self.mlp, LLaDAMLP):   # the attention step computes the FFN's scatter rows
+            self.self_attn.attn.ffn_cache = self.mlp.cache_update.cache_manager
         self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device=device)
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device=device)
 

@@ -208,10 +208,13 @@ _HOST_META_TIMEOUT_S = 60.0
 class Compacted:
     """Device results of one compaction; ``count`` stays on the device until asked for."""
 
-    def __init__(self, idx64, idx32, idx_k, cu_salientlens, count, idx_k32=None, host_meta=None):
+    def __init__(self, idx64, idx32, idx_k, cu_salientlens, count, idx_k32=None, host_meta=None, dest_rows=None,
+                 dest_starts=None):
         self.idx64, self.idx32, self.idx_k, self.idx_k32 = idx64, idx32, idx_k, idx_k32
         self.cu_salientlens, self.count = cu_salientlens, count
         self.host_meta = host_meta
+        # rows of the salient set in the cache whose sequence-start table is dest_starts
+        self.dest_rows, self.dest_starts = dest_rows, dest_starts
 
     def host(self):
         """(count, cu_salientlens as a list): one device->host read for both. When the producing
@@ -284,48 +287,58 @@ class StepBuffers:
         self.meta = torch.empty(B + 2, **i32)          # [count, cu_salientlens...]
         self.count, self.cu_sal = self.meta[0:1], self.meta[1:]
         self.host_meta = torch.empty(B + 2, dtype=torch.int32, pin_memory=True)
+        self.dest_rows = torch.empty(max(Tq, 1), **i64)
+        self.dest_starts = None       # the cache table dest_rows was computed for, in the last call
         self.ws_bytes = _lib.load().dyllm_sparse_step_workspace_bytes(B, H, Hkv, D, Tq, Tk, max_k, Tq)
         self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
 
     def compacted(self):
         return Compacted(self.idx64, self.idx32, self.idx_k64, self.cu_sal, self.count, self.idx_k32,
-                         self.host_meta)
+                         self.host_meta, self.dest_rows if self.dest_starts is not None else None, self.dest_starts)
 
 
 def sparse_attention_step(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_seq_starts, seq_ids, cu_seqlens_q,
                           cu_seqlens_k, cu_promptlens, max_seqlen_q, max_seqlen_k, total_k, n_sal, max_salientlen,
-                          cu_salientlens, idx_q32, idx_k64, idx_k32, softmax_scale, threshold, k_start=None):
+                          cu_salientlens, idx_q32, idx_k64, idx_k32, softmax_scale, threshold, k_start=None,
+                          dest_seq_starts=None):
     """The sparse branch of Attention.forward in one native call (dyllm_sparse_attention_step).
-    Results land in ``bufs`` (out / stats / mask and the next salient set, left on the device)."""
+    Results land in ``bufs`` (out / stats / mask and the next salient set, left on the device);
+    with ``dest_seq_starts`` (another per-layer cache's start table) also the rows of the next
+    salient set in that cache (``bufs.dest_rows``)."""
     Tq, H, D = q.shape
     Hkv = v_new.shape[1] if v_new.dim() == 3 else v_cache.shape[1] // D
     bufs.host_meta.fill_(-1)   # "not written yet" for Compacted.host()
+    bufs.dest_starts = dest_seq_starts
     _lib.call("dyllm_sparse_attention_step", _ptr(q), _ptr(k), _ptr(k_start), _ptr(v_cache), _ptr(v_seq_starts),
               _ptr(v_new), _ptr(c_cache), _ptr(c_seq_starts), _ptr(seq_ids), seq_ids.numel(), H, Hkv, D,
               _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), _ptr(cu_promptlens), int(max_seqlen_q), int(max_seqlen_k), Tq,
               int(total_k), int(n_sal), int(max_salientlen), _ptr(cu_salientlens), _ptr(idx_q32), _ptr(idx_k64),
               _ptr(idx_k32), float(softmax_scale), float(threshold), _ptr(bufs.out), _ptr(bufs.stats),
               _ptr(bufs.mask), _ptr(bufs.idx64), _ptr(bufs.idx32), _ptr(bufs.idx_k64), _ptr(bufs.idx_k32),
-              _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(bufs.host_meta), _ptr(bufs.ws), bufs.ws_bytes, _stream())
+              _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(dest_seq_starts),
+              _ptr(bufs.dest_rows if dest_seq_starts is not None else None), _ptr(bufs.host_meta), _ptr(bufs.ws),
+              bufs.ws_bytes, _stream())
     return bufs
 
 
 def sparse_attention_step_noalloc(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_seq_starts, seq_ids,
                                   cu_seqlens_q, cu_seqlens_k, cu_promptlens, max_seqlen_q, max_seqlen_k, total_k,
                                   n_sal, max_salientlen, cu_salientlens, idx_q32, idx_k64, idx_k32, softmax_scale,
-                                  threshold, k_start=None):
+                                  threshold, k_start=None, dest_seq_starts=None):
     """``sparse_attention_step`` through dyllm_sparse_attention_step_noalloc: the workspace is the
     library's own per-GPU scratch array (``bufs.ws`` is not used), so the call allocates nothing."""
     Tq, H, D = q.shape
     Hkv = v_new.shape[1] if v_new.dim() == 3 else v_cache.shape[1] // D
     bufs.host_meta.fill_(-1)
+    bufs.dest_starts = dest_seq_starts
     _lib.call("dyllm_sparse_attention_step_noalloc", _ptr(q), _ptr(k), _ptr(k_start), _ptr(v_cache),
               _ptr(v_seq_starts), _ptr(v_new), _ptr(c_cache), _ptr(c_seq_starts), _ptr(seq_ids), seq_ids.numel(), H,
               Hkv, D, _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), _ptr(cu_promptlens), int(max_seqlen_q),
               int(max_seqlen_k), Tq, int(total_k), int(n_sal), int(max_salientlen), _ptr(cu_salientlens),
               _ptr(idx_q32), _ptr(idx_k64), _ptr(idx_k32), float(softmax_scale), float(threshold), _ptr(bufs.out),
               _ptr(bufs.stats), _ptr(bufs.mask), _ptr(bufs.idx64), _ptr(bufs.idx32), _ptr(bufs.idx_k64),
-              _ptr(bufs.idx_k32), _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(bufs.host_meta), _stream())
+              _ptr(bufs.idx_k32), _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(dest_seq_starts),
+              _ptr(bufs.dest_rows if dest_seq_starts is not None else None), _ptr(bufs.host_meta), _stream())
     return bufs
 
 

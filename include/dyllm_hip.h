@@ -115,6 +115,10 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
  * context caches are addressed through their seq_start tables (indexed by seq_ids[b]).
  * cu_promptlens != NULL selects a Q-pruned step (Q rows are the response rows; the next set is
  * also produced in K space); otherwise Q space == K space and idx_k* = idx_q*.
+ * next_dest_rows (optional, capacity total_q) receives, for every row of the next salient set, its row in
+ * another per-layer cache whose sequence starts are dest_seq_starts (indexed by seq_ids[b]): the
+ * scatter_update address of its K-space row, i.e. where the layer's FFN writes that row's output
+ * (mlp_cache_manage.py:24-40), so no separate address pass is needed.
  * host_meta (optional, pinned host memory of batch + 2 int32 from hipHostMalloc) receives
  * [next_count, next_cu_salientlens...] directly from the compaction kernel, so the host can read
  * the salient count without a device->host copy: each entry is stored once, by the workgroup
@@ -132,8 +136,9 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                 const int64_t* idx_k64, const int32_t* idx_k32, float softmax_scale, float threshold,
                                 void* out, float* cosine_stats, uint8_t* cosine_out, int64_t* next_idx64,
                                 int32_t* next_idx32, int64_t* next_idx_k64, int32_t* next_idx_k32,
-                                int32_t* next_cu_salientlens, int32_t* next_count, int32_t* host_meta,
-                                void* workspace, size_t workspace_bytes, void* stream);
+                                int32_t* next_cu_salientlens, int32_t* next_count, const int64_t* dest_seq_starts,
+                                int64_t* next_dest_rows, int32_t* host_meta, void* workspace, size_t workspace_bytes,
+                                void* stream);
 
 /* The same step as dyllm_sparse_attention_step without the workspace arguments: no counterpart
  * in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
@@ -156,7 +161,8 @@ int dyllm_sparse_attention_step_noalloc(const void* q, const void* k, const int6
                                         float threshold, void* out, float* cosine_stats, uint8_t* cosine_out,
                                         int64_t* next_idx64, int32_t* next_idx32, int64_t* next_idx_k64,
                                         int32_t* next_idx_k32, int32_t* next_cu_salientlens, int32_t* next_count,
-                                        int32_t* host_meta, void* stream);
+                                        const int64_t* dest_seq_starts, int64_t* next_dest_rows, int32_t* host_meta,
+                                        void* stream);
 
 /* dV and V-cache update of attention.py:67-74 (dv = v_new - v_cache[row]; v_cache[row] = v_new)
  * for compact rows; dest_rows are cache rows (dyllm_scatter_dest_rows). */

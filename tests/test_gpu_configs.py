@@ -90,6 +90,11 @@ def test_sparse_attention_step_full_shape(dev, case, q_pruned):
     q = q_all[i64(resp)].contiguous()
     c_old = o_full[i64(resp)].cpu() if q_pruned else o_full.cpu()
     v_saved, c_saved = attn.v_cache.cache.clone(), attn.context_cache.cache.clone()
+    # a stand-in FFN cache laid out differently from the attention caches: the step's compaction
+    # also returns the rows of the next salient set in it
+    from types import SimpleNamespace
+    ffn_starts = torch.as_tensor(np.arange(B)[::-1].copy() * (L + 37) + 11, dtype=torch.int64, device=dev)
+    attn.ffn_cache = SimpleNamespace(seq_start_gpu=ffn_starts)
 
     def run(tau):
         attn.threshold = tau
@@ -116,8 +121,12 @@ def test_sparse_attention_step_full_shape(dev, case, q_pruned):
     idx_ref, cu_ref = ref.compact(mask_gpu, cu_q)
     assert np.array_equal(ctx.idx_salient_row.cpu().numpy(), idx_ref)
     assert np.array_equal(ctx.cu_salientlens.cpu().numpy(), cu_ref)
+    kspace = ref.fused_offset(idx_ref, cu_p, cu_ref) if q_pruned else idx_ref
     if q_pruned:
-        assert np.array_equal(ctx.idx_salient_row_k.cpu().numpy(), ref.fused_offset(idx_ref, cu_p, cu_ref))
+        assert np.array_equal(ctx.idx_salient_row_k.cpu().numpy(), kspace)
+    seg = np.searchsorted(cu_k, kspace, side="right") - 1
+    want_dest = ffn_starts.cpu().numpy()[seg] + (kspace - cu_k[seg])
+    assert np.array_equal(attn._bufs.dest_rows[:len(idx_ref)].cpu().numpy(), want_dest)
     assert 0 < len(idx_ref) < Tq
     # V cache: the salient key rows hold the new V rows, every other row is unchanged
     v_after = attn.v_cache.cache.view(Tk, Hkv, D)
