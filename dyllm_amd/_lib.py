@@ -20,6 +20,9 @@ SIGNATURES = {
     "dyllm_last_error": [],
     "dyllm_abi_version": [],
     "dyllm_attention_timer": [_I],
+    "dyllm_attention_kernel_info": [_I, _I, _P],
+    "dyllm_unmask_step": [_P, _P, _I, _P, _P, _P, _L, _P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                          _P, _I, _P],
     "dyllm_attention_timer_read": [_P, _P],
     "dyllm_attention_sparse_workspace_bytes": [_I, _I, _L, _I],
     "dyllm_attention_sparse_varlen": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _L, _I, _P, _P, _P,

@@ -958,6 +958,19 @@ static bool attn_aligned(const AttnArgs& a) {
   return (m % 16) == 0 && reinterpret_cast<uintptr_t>(a.O) % 8 == 0;
 }
 
+int attention_kernel_info(int dim, int64_t* out) {
+  hipFuncAttributes fa{};
+  const void* fn = reinterpret_cast<const void*>(&attention_step_kernel<4>);
+  if (hipFuncGetAttributes(&fa, fn) != hipSuccess) return fail("hipFuncGetAttributes failed for attention_step_kernel");
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, 0) != hipSuccess)
+    return fail("hipOccupancyMaxActiveBlocksPerMultiprocessor failed for attention_step_kernel");
+  const int64_t v[10] = {fa.numRegs, int64_t(fa.localSizeBytes), int64_t(fa.sharedSizeBytes), 0, 256, blocks,
+                         4 * 32, kBK, 1, dim == kD ? 1 : 0};
+  for (int i = 0; i < 10; ++i) out[i] = v[i];
+  return 0;
+}
+
 int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s) {
   DYLLM_REQUIRE(a.B >= 1 && a.H >= 1 && a.Hkv >= 1 && a.H % a.Hkv == 0, "bad head counts");
   DYLLM_REQUIRE(attn_aligned(a), "Q, K, V and context buffers must be 16-byte aligned (output 8-byte)");

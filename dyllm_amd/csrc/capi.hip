@@ -424,6 +424,54 @@ int dyllm_sparse_attention_step_noalloc(const void* q, const void* k, const int6
 
 size_t dyllm_sparse_step_scratch_bytes(void) { return kStepScratchBytes; }
 
+int dyllm_unmask_step(int64_t* tokens, const int32_t* cu_seqlens_k, int batch, const int64_t* sampled_pos,
+                      const int64_t* sampled_tok, const int32_t* sampled_counts, int64_t ld_sampled,
+                      int32_t* generated, const int32_t* prompt_len, const int32_t* answer_start,
+                      const int32_t* block_size, int64_t mask_id, int q_pruned, const int32_t* cu_seqlens_q,
+                      int64_t* idx_q, int32_t* idx_q32, int64_t* idx_k, int32_t* idx_k32, int32_t* idx_upd,
+                      int64_t* positions_k, int32_t* cu_salientlens, int64_t* input_ids, int64_t* cand_rel,
+                      int32_t* cand_n, int width, void* stream) {
+  for (const void* p : {(const void*)tokens, (const void*)cu_seqlens_k, (const void*)sampled_pos,
+                        (const void*)sampled_tok, (const void*)sampled_counts, (const void*)generated,
+                        (const void*)prompt_len, (const void*)answer_start, (const void*)block_size,
+                        (const void*)cu_seqlens_q, (const void*)idx_q, (const void*)idx_q32, (const void*)idx_k,
+                        (const void*)idx_k32, (const void*)idx_upd, (const void*)positions_k,
+                        (const void*)cu_salientlens, (const void*)cand_rel, (const void*)cand_n})
+    DYLLM_REQUIRE(p != nullptr, "null pointer argument");
+  UnmaskArgs a{};
+  a.tok = tokens;
+  a.cu_k = cu_seqlens_k;
+  a.pos = sampled_pos;
+  a.val = sampled_tok;
+  a.cnt = sampled_counts;
+  a.ld_sampled = ld_sampled;
+  a.generated = generated;
+  a.prompt_len = prompt_len;
+  a.answer_start = answer_start;
+  a.block_size = block_size;
+  a.mask_id = mask_id;
+  a.pruned = q_pruned ? 1 : 0;
+  a.cu_q = cu_seqlens_q;
+  a.idx_q = idx_q;
+  a.idx_q32 = idx_q32;
+  a.idx_k = idx_k;
+  a.idx_k32 = idx_k32;
+  a.idx_upd = idx_upd;
+  a.positions_k = positions_k;
+  a.cu_s = cu_salientlens;
+  a.input_ids = input_ids;
+  a.cand_rel = cand_rel;
+  a.cand_n = cand_n;
+  a.width = width;
+  return launch_unmask_step(a, batch, DYLLM_STREAM(stream));
+}
+
+int dyllm_attention_kernel_info(int dim, int mask_v_rows, int64_t* out) {
+  DYLLM_NONNULL(out);
+  (void)mask_v_rows;   // one kernel: the column-sparse tiles always skip PV on key groups without salient rows
+  return attention_kernel_info(dim, out);
+}
+
 int dyllm_v_delta_update(void* v_cache, const void* v_new, const int64_t* dest_rows, int64_t rows,
                          int64_t row_elems, void* dv_out, void* stream) {
   DYLLM_REQUIRE(rows == 0 || (v_cache && v_new && dest_rows && dv_out), "null pointer argument");

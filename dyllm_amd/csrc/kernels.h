@@ -129,6 +129,37 @@ struct AttnArgs {
 int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s);
 // Row-sparse tiles (fused output) and column-sparse tiles in one launch (4-wave workgroups).
 int launch_attention_step(const AttnArgs& rs, int max_rows_rs, const AttnArgs& cs, int max_rows_cs, hipStream_t s);
+// device-side unmasking bookkeeping between two sparse steps (unmask.hip)
+struct UnmaskArgs {
+  int64_t* tok;                 // token rows of the batch, packed by cu_k
+  const int32_t* cu_k;          // [B+1]
+  const int64_t* pos;           // previous sampler output [B][ld_sampled]: absolute positions
+  const int64_t* val;           // ... and tokens
+  const int32_t* cnt;           // [B] entries per sequence
+  int64_t ld_sampled;
+  int32_t* generated;           // [B] generated-token counters (updated)
+  const int32_t* prompt_len;    // [B]
+  const int32_t* answer_start;  // [B]
+  const int32_t* block_size;    // [B]
+  int64_t mask_id;
+  int pruned;                   // next step queries only the answer rows
+  const int32_t* cu_q;          // [B+1] next step's query rows
+  int64_t* idx_q;
+  int32_t* idx_q32;
+  int64_t* idx_k;
+  int32_t* idx_k32;
+  int32_t* idx_upd;
+  int64_t* positions_k;
+  int32_t* cu_s;                // [B+1]
+  int64_t* input_ids;           // next step's Q-pruned input ids (NULL: not produced)
+  int64_t* cand_rel;            // [B][width] candidate offsets from the first queried row
+  int32_t* cand_n;              // [B]
+  int width;
+};
+int launch_unmask_step(const UnmaskArgs& a, int batch, hipStream_t s);
+// launch resources of the fused step kernel: [regs, local_bytes, static_lds, dynamic_lds, threads,
+// max_active_blocks_per_cu, block_q, block_k, d_split, ok]
+int attention_kernel_info(int dim, int64_t* out);
 int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal, const int32_t* cu_k, int B,
                           int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, int32_t* kslot, int64_t Tk,
                           hipStream_t s);

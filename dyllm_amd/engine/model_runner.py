@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from ..config import Config
-from ..model_executor.layers.sampler import DreamSampler, LLaDASampler, RowLogits
+from ..model_executor.layers.sampler import DenseCandidates, DreamSampler, LLaDASampler, RowLogits
 from ..utils.context import get_context, reset_context, set_context
 from ..utils.metadata import get_metadata
 from .sequence import Sequence
@@ -86,6 +86,91 @@ class _HostStaging:
         return {name: dev[o:o + arr.nbytes].view(dt) for (name, arr, dt), o in zip(fields, offs)}
 
 
+class _DeviceBatch:
+    """Device-resident state of one running batch between its sparse steps: the token rows (packed
+    by cu_seqlens_k), the generated-token counters, the per-sequence layout and sampling knobs, and
+    the previous sampler output. A step of the same batch is then built on the device by one
+    ``dyllm_unmask_step`` launch (commit + salient lists + input ids + sampler candidates) instead
+    of host lists; the host keeps only the sizes it launches with (from its mirrors). Built from
+    the host mirrors before a host-built step's output is committed; dropped when the batch
+    changes."""
+
+    def __init__(self, runner: "ModelRunner", seqs: List[Sequence]):
+        dev = runner.device
+        cfg = runner.config
+        self.ids = [s.seq_id for s in seqs]
+        B = len(seqs)
+        lens = [len(s) for s in seqs]
+        cu_k = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        astart = [s.answer_start for s in seqs]
+        prompt = [s.num_prompt_tokens for s in seqs]
+        i32 = lambda x: torch.as_tensor(np.asarray(x), dtype=torch.int32, device=dev)
+        self.lens, self.cu_k_cpu = lens, cu_k.tolist()
+        self.tok = torch.from_numpy(np.concatenate([s.token_arr for s in seqs])).to(dev)
+        self.cu_k, self.prompt, self.astart = i32(cu_k), i32(prompt), i32(astart)
+        self.astart_cpu = astart
+        self.cu_p = i32(np.concatenate([[0], np.cumsum(prompt)]))
+        self.block = i32([s.block_size for s in seqs])
+        self.generated = i32([s.num_completion_tokens for s in seqs])
+        self.lens_t = i32(lens)
+        self.seq_ids = torch.tensor(self.ids, dtype=torch.long, device=dev)
+        self.W = max(s.block_size if s.block_size is not None else s.max_new_tokens for s in seqs)
+        W = self.W
+        # the two step layouts: Q-pruned (answer rows) and refresh (every row)
+        cu_q = np.concatenate([[0], np.cumsum([L - a for L, a in zip(lens, astart)])]).astype(np.int64)
+        pos_p = np.concatenate([np.arange(a, L, dtype=np.int64) for L, a in zip(lens, astart)])
+        pos_r = np.concatenate([np.arange(L, dtype=np.int64) for L in lens])
+        self.layout = {
+            True: (cu_q.tolist(), i32(cu_q), torch.from_numpy(pos_p).to(dev), i32(astart)),
+            False: (self.cu_k_cpu, self.cu_k, torch.from_numpy(pos_r).to(dev), i32([0] * B)),
+        }
+        # per-sequence sampling knobs ([B]; None when no sequence sets one), as prepare_sample
+        temps = [s.temperature if (s.temperature is not None and s.temperature > 1e-6) else 1.0 for s in seqs]
+        has_t = any(s.temperature is not None and s.temperature > 1e-6 for s in seqs)
+        f32 = lambda x: torch.tensor(x, dtype=torch.float32, device=dev)
+        self.temps = f32(temps) if has_t else None
+        self.top_ks = i32([s.top_k if s.top_k is not None else 1 << 30 for s in seqs]) \
+            if any(s.top_k is not None for s in seqs) else None
+        self.top_ps = f32([s.top_p if s.top_p is not None else 1.0 for s in seqs]) \
+            if any(s.top_p is not None for s in seqs) else None
+        self.thrs = f32([s.confidence_threshold if s.confidence_threshold is not None else float("inf")
+                         for s in seqs]) if any(s.confidence_threshold is not None for s in seqs) else None
+        self.transfers = i32([1 if s.confidence_threshold is not None else s.num_transfer_tokens for s in seqs])
+        # outputs of the device build (capacities: every sampled slot, every queried row)
+        cap = max(B * W, 1)
+        self.idx_q = torch.empty(cap, dtype=torch.long, device=dev)
+        self.idx_q32 = torch.empty(cap, dtype=torch.int32, device=dev)
+        self.idx_k = torch.empty(cap, dtype=torch.long, device=dev)
+        self.idx_k32 = torch.empty(cap, dtype=torch.int32, device=dev)
+        self.idx_upd = torch.empty(cap, dtype=torch.int32, device=dev)
+        self.pos_k = torch.empty(cap, dtype=torch.long, device=dev)
+        self.cu_s = torch.empty(B + 1, dtype=torch.int32, device=dev)
+        self.input_ids = torch.empty(max(int(cu_q[-1]), 1), dtype=torch.long, device=dev)
+        self.cand_rel = torch.empty(B, W, dtype=torch.long, device=dev)
+        self.cand_n = torch.empty(B, dtype=torch.int32, device=dev)
+        # previous sampled set: the host mirrors' last written positions (each sequence's salient
+        # rows when this step samples nothing for it, as the host path)
+        lp = torch.zeros(B, W, dtype=torch.long)
+        lt = torch.zeros(B, W, dtype=torch.long)
+        lc = torch.zeros(B, dtype=torch.int32)
+        for b, s in enumerate(seqs):
+            n = min(len(s.last_token_pos), W)
+            lp[b, :n] = torch.tensor(s.last_token_pos[:n], dtype=torch.long)
+            lt[b, :n] = torch.tensor(s.last_tokens[:n], dtype=torch.long)
+            lc[b] = n
+        self.last = (lp.to(dev), lt.to(dev), lc.to(dev))
+
+    def matches(self, seqs: List[Sequence]) -> bool:
+        return [s.seq_id for s in seqs] == self.ids
+
+    def record(self, pos, tok, cnt):
+        """Keep this step's sampler output; a sequence that sampled nothing keeps its previous set."""
+        lp, lt, lc = self.last
+        got = (cnt > 0)
+        self.last = (torch.where(got.unsqueeze(1), pos.long(), lp), torch.where(got.unsqueeze(1), tok.long(), lt),
+                     torch.where(got, cnt.to(torch.int32), lc))
+
+
 def q_pruned_step(seq: Sequence, period: int = 4) -> bool:
     """Sparse step that queries only the response rows (model_runner.py:211, period 4 there):
     after `period` processed steps, all but every `period`-th step."""
@@ -105,6 +190,9 @@ class ModelRunner:
         self.model = model if model is not None else build_model(config, device)
         self.sampler = DreamSampler("entropy") if hf.model_type == "Dream" else LLaDASampler("confidence")
         self.staging = _HostStaging(self.device)
+        self._dev_batch: Optional[_DeviceBatch] = None   # state of the running sparse batch
+        self.device_bookkeeping = True                   # build repeated sparse steps on the device
+        self.device_steps = 0                            # sparse steps built on the device
 
     # -- batch preparation -------------------------------------------------------------
     def prepare_full(self, seqs: List[Sequence]):
@@ -247,12 +335,59 @@ class ModelRunner:
         rows only (RowLogits)."""
         return RowLogits(self.model(input_ids, positions), self.model.compute_logits)
 
+    def _run_device_step(self, db: _DeviceBatch, seqs: List[Sequence], pruned: bool):
+        """A sparse step of the same batch as the previous one, built on the device."""
+        from .. import _lib
+        md = get_metadata()
+        B = len(seqs)
+        cu_q_cpu, cu_q, positions, offsets = db.layout[pruned]
+        lp, lt, lc = db.last
+        _lib.call("dyllm_unmask_step", db.tok.data_ptr(), db.cu_k.data_ptr(), B, lp.data_ptr(), lt.data_ptr(),
+                  lc.data_ptr(), lp.shape[1], db.generated.data_ptr(), db.prompt.data_ptr(), db.astart.data_ptr(),
+                  db.block.data_ptr(), int(self.config.mask_id), int(pruned), cu_q.data_ptr(), db.idx_q.data_ptr(),
+                  db.idx_q32.data_ptr(), db.idx_k.data_ptr(), db.idx_k32.data_ptr(), db.idx_upd.data_ptr(),
+                  db.pos_k.data_ptr(), db.cu_s.data_ptr(), db.input_ids.data_ptr() if pruned else None,
+                  db.cand_rel.data_ptr(), db.cand_n.data_ptr(), db.W, torch.cuda.current_stream().cuda_stream)
+        # host-side sizes from the mirrors (updated by the scheduler from the same sampled set)
+        kept = [sum(1 for p in s.last_token_pos if p >= a) for s, a in zip(seqs, db.astart_cpu)]
+        n = sum(kept)
+        md.running_seqs = db.ids
+        md.running_seqs_tensor = db.seq_ids
+        idx_k = db.idx_k[:n]
+        set_context(False, cu_seqlens_q=cu_q, cu_seqlens_q_cpu=cu_q_cpu, cu_seqlens_k=db.cu_k,
+                    cu_seqlens_k_cpu=db.cu_k_cpu, cu_promptlens=db.cu_p, cu_updatedlens=db.cu_s,
+                    cu_salientlens=db.cu_s, max_seqlen_q=max(cu_q_cpu[i + 1] - cu_q_cpu[i] for i in range(B)),
+                    max_seqlen_k=max(db.lens), idx_updated_row=db.idx_upd[:n], idx_salient_row=db.idx_q[:n],
+                    idx_salient_row_i32=db.idx_q32[:n], idx_salient_row_k=idx_k if pruned else None,
+                    max_salientlen=max(kept), context_lens=db.lens_t, context_lens_cpu=db.lens,
+                    total_seqlen_k=db.cu_k_cpu[-1], total_seqlen=cu_q_cpu[-1], positions_k=db.pos_k[:n])
+        input_ids = db.input_ids[:cu_q_cpu[-1]] if pruned else db.tok
+        logits = self.run_model(input_ids, positions, False)
+        with torch.inference_mode():
+            pos, tok, cnt = self.sampler(input_logits=logits, ctx=get_context(),
+                                         input_indices=DenseCandidates(db.cand_rel, db.cand_n, offsets),
+                                         temperatures=db.temps, num_transfer=db.transfers, top_k=db.top_ks,
+                                         top_p=db.top_ps, block_size=db.W, confidence_thresholds=db.thrs)
+        db.record(pos, tok, cnt)
+        reset_context()
+        self.device_steps += 1
+        return pos, tok, cnt
+
     def run(self, seqs: List[Sequence], is_full: bool, finished_seqs: Optional[List[int]] = None):
         if is_full:
             self.num_full_forwards += 1
         else:
             self.num_sparse_forwards += 1
         get_metadata().finished_seqs = list(finished_seqs or [])
+        db = self._dev_batch
+        if not is_full and self.device.type == "cuda" and db is not None and db.matches(seqs):
+            pruned = all(q_pruned_step(s, self.config.refresh_period) for s in seqs)
+            self.num_q_pruned_forwards += int(pruned)
+            return self._run_device_step(db, seqs, pruned)
+        # host-built step; a sparse batch keeps a device state for its following steps
+        self._dev_batch = db = None
+        if not is_full and self.device.type == "cuda" and self.device_bookkeeping:
+            db = _DeviceBatch(self, seqs)
         # all host-built metadata of the step (batch layout and sampling inputs) in one transfer
         finish_batch = self.prepare_full(seqs) if is_full else self.prepare_sparse(seqs)
         pruned = not is_full and all(q_pruned_step(s, self.config.refresh_period) for s in seqs)
@@ -267,6 +402,9 @@ class ModelRunner:
                                          temperatures=params[0], num_transfer=transfers, top_k=params[1],
                                          top_p=params[2], block_size=params[3], confidence_thresholds=params[4])
         reset_context()
+        if db is not None:
+            db.record(pos, tok, cnt)
+            self._dev_batch = db
         return pos, tok, cnt
 
     def call(self, method: str, *args):

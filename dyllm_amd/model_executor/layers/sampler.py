@@ -69,6 +69,15 @@ class RowLogits:
         return self.compute(self.hidden.index_select(0, rows))
 
 
+class DenseCandidates:
+    """Candidate rows already laid out [B, W] on the device (dyllm_unmask_step): rel[b, j] is the
+    offset of candidate j from sequence b's first queried row, valid for j < count[b], in ascending
+    position order; offsets[b] turns an offset into the absolute position."""
+
+    def __init__(self, rel: torch.Tensor, count: torch.Tensor, offsets: torch.Tensor):
+        self.rel, self.count, self.offsets = rel, count, offsets
+
+
 class BaseSampler(nn.Module):
 
     def __init__(self, algorithm: str = "confidence"):
@@ -97,6 +106,9 @@ class BaseSampler(nn.Module):
                 confidence_thresholds: Optional[torch.Tensor] = None):
         logits = self.adjust_logits(input_logits)
         dev = logits.device
+        if isinstance(input_indices, DenseCandidates):
+            return self._forward_dense(logits, ctx, input_indices, temperatures, num_transfer, top_k, top_p,
+                                       confidence_thresholds)
         rel, offsets, cu = input_indices
         B = cu.numel() - 1
         n = rel.numel()
@@ -126,6 +138,36 @@ class BaseSampler(nn.Module):
         d_tokens[g, s] = tokens[inside]
         d_pos[g, s] = pos[inside]
 
+        return self._select(d_scores, d_tokens, d_pos, num_transfer, confidence_thresholds)
+
+    def _forward_dense(self, logits, ctx, cands: DenseCandidates, temperatures, num_transfer, top_k, top_p,
+                       confidence_thresholds):
+        """The same selection from candidates laid out [B, W] on the device: per-sequence knobs
+        ([B] tensors) apply to every candidate of the sequence; empty slots score -inf."""
+        dev = cands.rel.device
+        B, W = cands.rel.shape
+        valid = torch.arange(W, device=dev).unsqueeze(0) < cands.count.long().unsqueeze(1)
+        rows = (ctx.cu_seqlens_q[:-1].long().unsqueeze(1) + cands.rel).masked_fill(~valid, 0).reshape(-1)
+        cand = logits.index_select(0, rows)
+        rep = lambda t: t.reshape(-1).repeat_interleave(W, output_size=B * W)
+        if temperatures is not None:
+            cand = cand / rep(temperatures).unsqueeze(-1)
+        cand = top_k_logits(cand, rep(top_k) if top_k is not None else None)
+        cand = top_p_logits(cand, rep(top_p) if top_p is not None else None)
+        probs = F.softmax(cand, dim=-1)
+        top_probs, top_tokens = probs.max(dim=-1)
+        scores = self.compute_scores(probs, top_probs)
+        tokens = self.sample_token(probs, top_tokens, rep(temperatures) if temperatures is not None else None)
+        d_scores = scores.view(B, W).masked_fill(~valid, float("-inf"))
+        d_tokens = tokens.view(B, W).masked_fill(~valid, 0)
+        d_pos = (cands.rel + cands.offsets.long().unsqueeze(1)).masked_fill(~valid, 0)
+        return self._select(d_scores, d_tokens, d_pos, num_transfer, confidence_thresholds)
+
+    def _select(self, d_scores, d_tokens, d_pos, num_transfer, confidence_thresholds):
+        """Order every sequence's candidates by score (stable: ties keep position order) and keep
+        the first num_transfer plus every one whose score reaches the threshold (sampler.py:44-86)."""
+        dev = d_scores.device
+        B, W = d_scores.shape
         s_scores, order = torch.sort(d_scores, dim=1, descending=True, stable=True)
         s_tokens = d_tokens.gather(1, order)
         s_pos = d_pos.gather(1, order)

@@ -13,6 +13,7 @@ Reference signatures mirrored:
 """
 from __future__ import annotations
 
+import ctypes
 import time
 
 import torch
@@ -340,6 +341,15 @@ def sparse_attention_step_noalloc(bufs, q, k, v_cache, v_seq_starts, v_new, c_ca
               _ptr(bufs.idx_k32), _ptr(bufs.cu_sal), _ptr(bufs.count), _ptr(dest_seq_starts),
               _ptr(bufs.dest_rows if dest_seq_starts is not None else None), _ptr(bufs.host_meta), _stream())
     return bufs
+
+
+def attention_kernel_info(dim, mask_v_rows=False):
+    """attention.cpp:205-208: launch resources of this build's main attention kernel,
+    [regs, local_bytes, static_smem, dynamic_smem, tb_size, max_active_blocks_per_sm, block_q,
+    block_k, d_split, ok] (per CU on this GPU)."""
+    out = (ctypes.c_int64 * 10)()
+    _lib.call("dyllm_attention_kernel_info", int(dim), int(bool(mask_v_rows)), ctypes.addressof(out))
+    return list(out)
 
 
 def fused_offset_launch(idxs, num_idxs, cu_promptlens, cu_salientlens, out_tensor, max_threads):

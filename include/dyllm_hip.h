@@ -28,6 +28,8 @@
  *   dyllm_moe_gate                 <- moe_gate, dyllm/model_executor/layers/fused_moe.py:375-408
  *   dyllm_moe_align_block_size     <- moe_align_block_size, fused_moe.py:37-85
  *   dyllm_fused_experts            <- fused_experts, fused_moe.py:269-335
+ *   dyllm_unmask_step              <- Scheduler.postprocess + ModelRunner.prepare_sparse / prepare_sample
+ *                                     (dyllm/engine/scheduler.py:89-145, model_runner.py:186-372) between sparse steps
  *   dyllm_sparse_attention_step, dyllm_attention_colsparse_cached, dyllm_v_delta_update, dyllm_seq_row_starts
  *                                  <- the sparse branch of Attention.forward, attention.py:64-178, with the
  *                                     K/V/context cache gathers and the full-size dV fused away
@@ -48,6 +50,34 @@ extern "C" {
 const char* dyllm_last_error(void);
 /* ABI version of this library. */
 int dyllm_abi_version(void);
+
+/* Unmasking bookkeeping between two sparse steps of one running batch, on the device (the host
+ * work of Scheduler.postprocess + ModelRunner.prepare_sparse / prepare_sample,
+ * dyllm/engine/scheduler.py:89-145, dyllm/engine/model_runner.py:186-372). One launch:
+ *   commit   tokens[cu_k[b] + p] = tok for the previous sampler output (sampled_pos / sampled_tok,
+ *            [batch][ld_sampled], sampled_counts[b] entries); positions that held mask_id and now hold
+ *            another token are added to generated[b];
+ *   salient  the kept positions p >= answer_start[b], in sampler order, as the next step's lists:
+ *            idx_q (p - prompt_len[b] + cu_q[b] when q_pruned, else p + cu_q[b]), idx_k = idx_upd =
+ *            p + cu_k[b], positions_k = p, cu_salientlens [batch+1] (capacity: batch * ld_sampled);
+ *   inputs   q_pruned and input_ids != NULL: input_ids[cu_q[b] + i] = tokens[cu_k[b] + answer_start[b] + i];
+ *   candidates  the first `width` positions p in [offset, limit) holding mask_id, offset = answer_start
+ *            (q_pruned) or 0, limit = min(L, block_size * (block_idx + 1) + prompt_len) with
+ *            block_idx = generated / block_size: cand_rel[b][j] = p - offset, cand_n[b] = count. */
+int dyllm_unmask_step(int64_t* tokens, const int32_t* cu_seqlens_k, int batch, const int64_t* sampled_pos,
+                      const int64_t* sampled_tok, const int32_t* sampled_counts, int64_t ld_sampled,
+                      int32_t* generated, const int32_t* prompt_len, const int32_t* answer_start,
+                      const int32_t* block_size, int64_t mask_id, int q_pruned, const int32_t* cu_seqlens_q,
+                      int64_t* idx_q, int32_t* idx_q32, int64_t* idx_k, int32_t* idx_k32, int32_t* idx_upd,
+                      int64_t* positions_k, int32_t* cu_salientlens, int64_t* input_ids, int64_t* cand_rel,
+                      int32_t* cand_n, int width, void* stream);
+
+/* Launch resources of the fused attention kernel (attention_kernel_info, pybind op of
+ * dyllm/csrc/attention/attention.cpp:205-208): out[10] = [registers, local (scratch) bytes per lane,
+ * static LDS bytes, dynamic LDS bytes, threads per block, max active blocks per CU, query rows per
+ * block, keys per block, d_split, ok (1 when dim == 128)]. mask_v_rows is accepted for the
+ * reference's signature; this build has one kernel for both. */
+int dyllm_attention_kernel_info(int dim, int mask_v_rows, int64_t* out);
 
 /* Timing of the fused attention kernel inside dyllm_sparse_attention_step (no counterpart in
  * the reference; for benchmarks that need that kernel's own duration): while enabled (per host

@@ -102,3 +102,28 @@ def test_generate_config4_long_context(dev):
     for o, p in zip(out, prompts):
         assert o["token_ids"][:2048] == p and len(o["token_ids"]) == 8192
         assert o["token_ids"][2048:].count(eng.config.mask_id) < 6144 // 8
+
+
+@pytest.mark.parametrize("model", ["tiny-llada", "tiny-dream", "tiny-llada-moe"])
+def test_device_bookkeeping_same_tokens(dev, model):
+    """Sparse steps of a running batch built on the device (dyllm_unmask_step: commit, salient
+    lists, input ids, sampler candidates) generate the same tokens as host-built steps, with
+    fixed-count and confidence-threshold unmasking and a batch that changes mid-run."""
+    from dyllm_amd import SamplingParams, dLLM
+
+    print(f"[engine] device bookkeeping {model}", flush=True)
+    outs, dev_steps = [], []
+    for on in (False, True):
+        eng = dLLM(model, threshold=0.99, max_num_seqs=3)
+        eng.model_runner.device_bookkeeping = on
+        sps = [SamplingParams(max_new_tokens=64, steps=16, num_full_steps=2, block_size=16, temperature=0.0),
+               SamplingParams(max_new_tokens=48, steps=12, num_full_steps=3, block_size=8, temperature=0.0,
+                              confidence_threshold=0.05),
+               SamplingParams(max_new_tokens=64, steps=16, num_full_steps=2, block_size=16, temperature=0.0)]
+        prompts = [[3, 14, 15, 92, 65], [2, 71, 82, 81, 82, 84, 59], [1] * 12, [9, 9, 8]]
+        out = eng.generate(prompts, sps + [sps[0]])
+        torch.cuda.synchronize()
+        outs.append([o["token_ids"] for o in out])
+        dev_steps.append(eng.model_runner.device_steps)
+    assert dev_steps[0] == 0 and dev_steps[1] > 10
+    assert outs[0] == outs[1]

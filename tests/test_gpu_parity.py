@@ -334,3 +334,14 @@ def test_moe_align_clamps_out_of_range_ids(dev):
     assert int(npp.item()) == n_ref
     assert np.array_equal(sorted_ids.cpu().numpy()[:n_ref], s_ref)
     assert np.array_equal(tile_e.cpu().numpy()[:n_ref // 4], e_ref)
+
+
+def test_attention_kernel_info(dev):
+    """attention.cpp:205-208 mirror: [regs, local_bytes, static_smem, dynamic_smem, tb_size,
+    max_active_blocks_per_sm, block_q, block_k, d_split, ok]."""
+    info = _ops().attention_kernel_info(128)
+    assert len(info) == 10
+    regs, local, smem, dyn, tb, blocks, bq, bk, dsplit, ok = info
+    assert 0 < regs <= 512 and tb == 256 and bq == 128 and bk == 64 and ok == 1
+    assert 0 < smem <= 160 * 1024 and blocks >= 1 and local >= 0
+    assert _ops().attention_kernel_info(96)[-1] == 0
