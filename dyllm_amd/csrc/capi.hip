@@ -704,6 +704,7 @@ static int store_gemm(const void* a, int64_t lda, const int32_t* rows_idx, int64
   GemmArgs d{};
   d.A = static_cast<const uint16_t*>(a);
   d.lda = lda;
+  d.a_rows = rows_idx ? 0 : rows;   // a gathered source's row count is not known here
   d.a_ids = rows_idx;
   d.a_div = 1;
   d.id_limit = INT64_MAX;
@@ -994,6 +995,7 @@ int dyllm_fused_experts(const void* x, const int32_t* rows_idx, int64_t tokens, 
   GemmArgs g{};
   g.A = static_cast<const uint16_t*>(x);
   g.lda = hidden;
+  g.a_rows = tokens;
   g.a_ids = sorted;
   g.a_div = top_k;
   g.id_limit = S;
@@ -1014,6 +1016,7 @@ int dyllm_fused_experts(const void* x, const int32_t* rows_idx, int64_t tokens, 
   GemmArgs d{};
   d.A = inter;
   d.lda = intermediate;
+  d.a_rows = S;
   d.a_ids = sorted;
   d.a_div = 1;
   d.id_limit = S;

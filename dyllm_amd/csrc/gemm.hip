@@ -22,7 +22,8 @@
 // (WGN = 4; a 2 x 2 grid of 1-wave-per-SIMD tiles, and two 4-wave BM x 128 workgroups per CU,
 // both measured slower), each wavefront (BM/2) x 64
 // of v_mfma_f32_32x32x16_bf16 tiles. Operands move global -> LDS with the gfx950 direct
-// LDS-load (global_load_lds_dwordx4), no register staging. Operands are staged through
+// LDS-load (buffer_load_dwordx4 ... lds: per-lane row offsets fixed for the tile, the K
+// position a scalar offset), no register staging. Operands are staged through
 // LDS in unpadded 128-byte rows whose 16-byte chunks are XOR-swizzled by row
 // (chunk ^ (row & 7)), so the fragment reads are spread over the banks. A slices (the gathered
 // rows, L2-resident) are double-buffered and loaded one slice ahead; W slices (streamed from
@@ -31,8 +32,8 @@
 // newest W loads in flight (32-wide K stages with 4-5 buffers of both operands measured slower). Within a slice the fragment reads of the next 16-wide K
 // substep are interleaved one per MFMA with the current substep, pinned with
 // sched_group_barrier (the compiler's own schedule clusters the reads and stalls on them;
-// 4-8 % with warm caches). In the 128- and 192-row tiles the last substep's MFMAs are issued after the
-// slice's barrier, over the first fragment reads of the next slice (8-15 % fewer cycles per tile). The MFMA is issued as D = W_tile * A_tile^T
+// 4-8 % with warm caches). The last substep's MFMAs are issued after the slice's barrier, over the first
+// fragment reads of the next slice (8-15 % fewer cycles per tile). The MFMA is issued as D = W_tile * A_tile^T
 // so that each lane owns one output row and four consecutive output columns per register
 // group: 8-byte stores and one row lookup per lane for the scatter. Workgroups are ordered
 // M-fastest and remapped XCD-major so the M tiles sharing a weight slice run on one XCD and
@@ -72,7 +73,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   constexpr int TM = WM / 32, TN = WN / 32;   // 32x32 MFMA tiles per wave
   const int64_t m0 = int64_t(mt) * BM;
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wave index in a scalar register: the LDS destinations of the loads are scalar arithmetic
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w & 1, wn = w >> 1;
   constexpr int GW = BN / (2 * WGN);          // SwiGLU: gate (and up) rows per wavefront
   const int l32 = lane & 31, half = lane >> 5;
@@ -90,10 +93,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   // (m >= M, padding ids, n >= N) are clamped to a valid row: their products are never stored.
   constexpr int CA = BM / (8 * NW), CW = BN / (8 * NW);  // 1 KB blocks per wavefront per K slice
   const int lrow = lane >> 3;
-  // per-lane source of each 1 KB block: the A row (gathered) and W row, kept as 32-bit row
-  // numbers (the host checks rows * leading dimension < 2^31) so the 1-wave-per-SIMD tiles keep
-  // their registers for the accumulators; the chunk offset is the same for every block
-  int a_row[CA];
+  // (w + NW * i) * 8 + lrow == lrow (mod 8): the swizzled chunk of a lane is the same in every block
+  const int lane_chunk = swz_chunk(w * 8 + lrow, lane & 7) * 8;
+  // The loads are buffer loads (buffer_load_dwordx4 ... lds): a scalar resource holds the operand's
+  // base at this split-K slice's first column, each lane a fixed 32-bit byte offset of its row and
+  // chunk, and the K position of the slice is the scalar offset, so a K slice costs no vector
+  // address arithmetic. Offsets are 32-bit: every operand spans less than 4 GiB (checked on the
+  // host where the extent is known).
+  uint32_t a_vo[CA];
 #pragma unroll
   for (int i = 0; i < CA; ++i) {
     const int64_t m = m0 + (w + NW * i) * 8 + lrow;
@@ -105,9 +112,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
         row = (id < g.id_limit) ? id / g.a_div : 0;
       }
     }
-    a_row[i] = int(row);
+    a_vo[i] = uint32_t((row * g.lda + lane_chunk) * 2);
   }
-  int w_row[CW];
+  uint32_t w_vo[CW];
 #pragma unroll
   for (int i = 0; i < CW; ++i) {
     const int r = (w + NW * i) * 8 + lrow;
@@ -117,33 +124,36 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     else
       wrow = int64_t(nt) * BN + r;
     if (wrow >= g.N) wrow = 0;
-    w_row[i] = int(wrow);
+    w_vo[i] = uint32_t((wrow * g.ldw + lane_chunk) * 2);
   }
-  // (w + NW * i) * 8 + lrow == lrow (mod 8): the swizzled chunk of a lane is the same in every block
-  const int lane_chunk = swz_chunk(w * 8 + lrow, lane & 7) * 8;
-  const uint16_t* const a_base = g.A + int64_t(k_begin) * kGemmBK + lane_chunk;
-  const uint16_t* const w_base = Wb + int64_t(k_begin) * kGemmBK + lane_chunk;
+  // the resource base must be wave-uniform (a scalar register): the pointer is read from lane 0
+  auto uniform_ptr = [](const uint16_t* p) -> void* {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo32 = __builtin_amdgcn_readfirstlane(uint32_t(v)), hi32 = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+    return reinterpret_cast<void*>((uint64_t(hi32) << 32) | lo32);
+  };
+  // raw buffer (stride 0), range check disabled (num_records = 0xffffffff), gfx9 data format word
+  constexpr int kRsrcWord3 = 0x00020000;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(g.A + int64_t(k_begin) * kGemmBK), 0, -1, kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(Wb + int64_t(k_begin) * kGemmBK), 0, -1, kRsrcWord3);
   typedef __attribute__((address_space(3))) void lds_void;
-  typedef const __attribute__((address_space(1))) void glb_void;
   // LDS: A slices double-buffered, W slices (streamed from HBM) triple-buffered so their loads
   // are issued two slices ahead: [A0 | A1 | W0 | W1 | W2]
   uint16_t* const a_lds = gsm;
   uint16_t* const w_lds = gsm + 2 * BM * kGemmBK;
   auto stage_a = [&](int kt, int buf) {
-    const int64_t ko = int64_t(kt) * kGemmBK;
     uint16_t* As = a_lds + buf * (BM * kGemmBK);
 #pragma unroll
     for (int i = 0; i < CA; ++i)
-      __builtin_amdgcn_global_load_lds((glb_void*)(a_base + int64_t(a_row[i]) * g.lda + ko),
-                                       (lds_void*)(As + (w + NW * i) * 8 * kGemmBK), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(As + (w + NW * i) * 8 * kGemmBK), 16, int(a_vo[i]),
+                                               kt * (kGemmBK * 2), 0, 0);
   };
   auto stage_w = [&](int kt, int buf) {
-    const int64_t ko = int64_t(kt) * kGemmBK;
     uint16_t* Ws = w_lds + buf * (BN * kGemmBK);
 #pragma unroll
     for (int i = 0; i < CW; ++i)
-      __builtin_amdgcn_global_load_lds((glb_void*)(w_base + int64_t(w_row[i]) * g.ldw + ko),
-                                       (lds_void*)(Ws + (w + NW * i) * 8 * kGemmBK), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)(Ws + (w + NW * i) * 8 * kGemmBK), 16, int(w_vo[i]),
+                                               kt * (kGemmBK * 2), 0, 0);
   };
 
   // W-tile row base of the wave's n-subtile i
@@ -163,14 +173,20 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   // Fragments are double-buffered in registers (two named sets so every index stays static):
-  // the LDS reads of K-substep ks+1 are issued one by one between the MFMAs of ks.
+  // the LDS reads of K-substep ks+1 are issued one by one between the MFMAs of ks. Fragment rows
+  // are multiples of 32 plus l32, so the swizzle depends on l32 only: one lane offset per substep
+  // (lo), the row base of each fragment an immediate.
   bf16x8_t wf0[TN], af0[TM], wf1[TN], af1[TM];
+  int lo[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) lo[ks] = swz(l32, 2 * ks + half);
   auto fload = [&](const uint16_t* As, const uint16_t* Ws, int ks, bf16x8_t* wf, bf16x8_t* af) {
-    const int ch = 2 * ks + half;
+    const uint16_t* wp = Ws + lo[ks];
+    const uint16_t* ap = As + wm * WM * kGemmBK + lo[ks];
 #pragma unroll
-    for (int i = 0; i < TN; ++i) wf[i] = *reinterpret_cast<const bf16x8_t*>(&Ws[swz(wrow_base(i) + l32, ch)]);
+    for (int i = 0; i < TN; ++i) wf[i] = *reinterpret_cast<const bf16x8_t*>(wp + wrow_base(i) * kGemmBK);
 #pragma unroll
-    for (int j = 0; j < TM; ++j) af[j] = *reinterpret_cast<const bf16x8_t*>(&As[swz(wm * WM + 32 * j + l32, ch)]);
+    for (int j = 0; j < TM; ++j) af[j] = *reinterpret_cast<const bf16x8_t*>(ap + 32 * j * kGemmBK);
   };
   auto mma = [&](const bf16x8_t* wf, const bf16x8_t* af) {
 #pragma unroll
@@ -214,91 +230,52 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   }
   __builtin_amdgcn_s_barrier();
   int wcur = 0;   // kt % 3
-  if constexpr (BM <= 192) {
-    // The last K substep of each slice is carried across the slice's barrier: its fragments are
-    // read before the barrier and its MFMAs issued after it, while the first fragment reads of the
-    // next slice are in flight, so the MFMA pipe does not idle through the barrier and the reads.
-    // (The 256-row tile has no registers left for it.)
-    fload(a_lds, w_lds, 0, wf0, af0);
-    for (int kt = 0; kt < nk; ++kt) {
-      const uint16_t* As = a_lds + (kt & 1) * (BM * kGemmBK);
-      const uint16_t* Ws = w_lds + wcur * (BN * kGemmBK);
-      const int wnext2 = wcur == 0 ? 2 : wcur - 1;   // (kt + 2) % 3
-      // raised wave priority over the slice's MFMA stretch: the SIMD's arbiter then favours a
-      // wave issuing MFMAs over its partner wave issuing loads
-      __builtin_amdgcn_s_setprio(1);
-      if (kt > 0) mma(wf1, af1);   // substep 3 of slice kt-1
-      __builtin_amdgcn_sched_barrier(0);
-      if (kt + 1 < nk) stage_a(kt + 1, (kt & 1) ^ 1);
-      __builtin_amdgcn_sched_barrier(0);
-      fload(As, Ws, 1, wf1, af1);
-      mma(wf0, af0);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
-      // the weight loads after the first substep's MFMAs (issued last: the vmcnt wait below
-      // leaves exactly them in flight)
-      if (kt + 2 < nk) stage_w(kt + 2, wnext2);
-      __builtin_amdgcn_sched_barrier(0);
-      fload(As, Ws, 2, wf0, af0);
-      mma(wf1, af1);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
-      fload(As, Ws, 3, wf1, af1);
-      mma(wf0, af0);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_setprio(0);
-      // this wave's LDS reads of the slice (substep 3 included) are done before any wave
-      // refills its buffers
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (kt + 2 < nk) {
-        wait_w_in_flight();
-      } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      }
-      __builtin_amdgcn_s_barrier();
-      wcur = wcur == 2 ? 0 : wcur + 1;
-      if (kt + 1 < nk) fload(a_lds + ((kt + 1) & 1) * (BM * kGemmBK), w_lds + wcur * (BN * kGemmBK), 0, wf0, af0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+  // The last K substep of each slice is carried across the slice's barrier: its fragments are
+  // read before the barrier and its MFMAs issued after it, while the first fragment reads of the
+  // next slice are in flight, so the MFMA pipe does not idle through the barrier and the reads.
+  fload(a_lds, w_lds, 0, wf0, af0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint16_t* As = a_lds + (kt & 1) * (BM * kGemmBK);
+    const uint16_t* Ws = w_lds + wcur * (BN * kGemmBK);
+    const int wnext2 = wcur == 0 ? 2 : wcur - 1;   // (kt + 2) % 3
+    // raised wave priority over the slice's MFMA stretch: the SIMD's arbiter then favours a
+    // wave issuing MFMAs over its partner wave issuing loads
+    __builtin_amdgcn_s_setprio(1);
+    if (kt > 0) mma(wf1, af1);   // substep 3 of slice kt-1
+    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < nk) stage_a(kt + 1, (kt & 1) ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    fload(As, Ws, 1, wf1, af1);
+    mma(wf0, af0);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    // the weight loads after the first substep's MFMAs (issued last: the vmcnt wait below
+    // leaves exactly them in flight)
+    if (kt + 2 < nk) stage_w(kt + 2, wnext2);
+    __builtin_amdgcn_sched_barrier(0);
+    fload(As, Ws, 2, wf0, af0);
     mma(wf1, af1);
-  } else {
-    for (int kt = 0; kt < nk; ++kt) {
-      const uint16_t* As = a_lds + (kt & 1) * (BM * kGemmBK);
-      const uint16_t* Ws = w_lds + wcur * (BN * kGemmBK);
-      const int wnext2 = wcur == 0 ? 2 : wcur - 1;   // (kt + 2) % 3
-      if (kt + 1 < nk) stage_a(kt + 1, (kt & 1) ^ 1);
-      if (kt + 2 < nk) stage_w(kt + 2, wnext2);
-      fload(As, Ws, 0, wf0, af0);
-      __builtin_amdgcn_sched_barrier(0);
-      // raised wave priority from the first MFMA of the slice to its end: the SIMD's arbiter then
-      // favours a wave in its MFMA stretch over its partner wave issuing the next slice's loads
-      __builtin_amdgcn_s_setprio(1);
-      fload(As, Ws, 1, wf1, af1);
-      mma(wf0, af0);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
-      fload(As, Ws, 2, wf0, af0);
-      mma(wf1, af1);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
-      fload(As, Ws, 3, wf1, af1);
-      mma(wf0, af0);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
-      mma(wf1, af1);
-      __builtin_amdgcn_s_setprio(0);
-      // this wave's LDS reads of the current slice are done before any wave refills its buffers
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (kt + 2 < nk) {
-        wait_w_in_flight();
-      } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      }
-      __builtin_amdgcn_s_barrier();
-      wcur = wcur == 2 ? 0 : wcur + 1;
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    fload(As, Ws, 3, wf1, af1);
+    mma(wf0, af0);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
+    // this wave's LDS reads of the slice (substep 3 included) are done before any wave
+    // refills its buffers
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (kt + 2 < nk) {
+      wait_w_in_flight();
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
+    __builtin_amdgcn_s_barrier();
+    wcur = wcur == 2 ? 0 : wcur + 1;
+    if (kt + 1 < nk) fload(a_lds + ((kt + 1) & 1) * (BM * kGemmBK), w_lds + wcur * (BN * kGemmBK), 0, wf0, af0);
+    __builtin_amdgcn_sched_barrier(0);
   }
+  mma(wf1, af1);
 
   // ---- epilogue: lane owns row m = m0 + wm*WM + 32j + l32 -------------------------------
   if constexpr (EPI == GemmEpi::Store) {
@@ -532,6 +509,10 @@ int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, int
   DYLLM_REQUIRE(g.K > 0 && g.K % kGemmBK == 0, "GEMM K must be a positive multiple of 64");
   DYLLM_REQUIRE(g.N > 0 && g.N % 8 == 0, "GEMM N must be a positive multiple of 8");
   DYLLM_REQUIRE(g.lda % 8 == 0 && g.ldw % 8 == 0 && g.ldc % 4 == 0, "GEMM leading dimensions must keep 16-byte rows");
+  // 32-bit byte offsets inside one operand (the buffer loads of the tile): the weight (one expert's
+  // block for the grouped GEMM) always, A when the caller states its row count
+  DYLLM_REQUIRE(int64_t(g.N) * g.ldw * 2 <= (int64_t(1) << 32), "GEMM weight must span less than 4 GiB");
+  DYLLM_REQUIRE(g.a_rows <= 0 || g.a_rows * g.lda * 2 <= (int64_t(1) << 32), "GEMM input rows must span less than 4 GiB");
   DYLLM_REQUIRE(reinterpret_cast<uintptr_t>(g.A) % 16 == 0 && reinterpret_cast<uintptr_t>(g.W) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(g.Cout) % 8 == 0 && reinterpret_cast<uintptr_t>(g.bias) % 8 == 0,
                 "GEMM operands must be 16-byte aligned (output and bias 8-byte)");

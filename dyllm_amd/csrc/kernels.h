@@ -198,6 +198,7 @@ enum class GemmEpi : int { Store = 0, SwiGLU = 1 };
 struct GemmArgs {
   const uint16_t* A;
   int64_t lda;
+  int64_t a_rows;             // rows A holds, when known (0: unknown); A spans < 4 GiB either way
   const int32_t* a_ids;
   int a_div;
   int64_t id_limit;

@@ -461,11 +461,19 @@ def gather_rows_2D(x, row_idx):
 # ---------------------------------------------------------------------------------------
 # FFN / MoE
 # ---------------------------------------------------------------------------------------
+def _gemm_source(x, name="x"):
+    """The GEMM kernels address an operand with 32-bit byte offsets: a gathered input must span
+    less than 4 GiB (the library cannot see a gathered source's extent)."""
+    if x.shape[0] and ((x.shape[0] - 1) * x.stride(0) + x.shape[1]) * 2 > (1 << 32):
+        raise ValueError(f"{name} spans more than 4 GiB; the GEMM kernels address it with 32-bit offsets")
+
+
 def ffn_gate_up(x, w_gate_up, rows_idx=None, count=None, hint=0):
     """h = silu(a Wg^T) * (a Wu^T) for a = x[rows_idx] (gathered inside the GEMM). With
     ``count`` (device int32 [1]) ``rows_idx`` is a capacity-sized buffer of which the first
     count[0] rows are used -- no host synchronisation; ``hint`` is the expected count."""
     _check(x, "x", torch.bfloat16, 2)
+    _gemm_source(x)
     _check(w_gate_up, "w_gate_up", torch.bfloat16, 2)
     hidden = x.shape[1]
     inter = w_gate_up.shape[0] // 2
@@ -508,6 +516,7 @@ def linear(x, w, bias=None, rows_idx=None, count=None, hint=0):
     kv_proj of llada.py:108 / dream.py:103 / lladamoe.py:204. ``count``/``hint`` as for
     ffn_gate_up (rows beyond count[0] are left unwritten)."""
     _check(x, "x", torch.bfloat16, 2)
+    _gemm_source(x)
     _check(w, "w", torch.bfloat16, 2)
     n_out, k_in = w.shape
     if x.shape[1] != k_in:

@@ -254,6 +254,10 @@ int dyllm_gather_rows(const void* x, int64_t x_rows, void* out, int64_t row_byte
                       void* stream);
 
 /* ---- FFN ------------------------------------------------------------------------------- */
+/* Every GEMM operand (the input rows x, h, the weights; one expert's block of a stacked expert
+ * weight) must span less than 4 GiB: the kernels address them with 32-bit byte offsets. The
+ * weights and ungathered inputs are checked (-> error); a gathered x's extent is not known to
+ * the library and is the caller's to keep. */
 
 /* Workspace of dyllm_swiglu_ffn: dyllm_swiglu_ffn_workspace_bytes (the [rows, intermediate]
  * bf16 activations) + dyllm_ffn_down_workspace_bytes (split-K partials of the down GEMM). */
