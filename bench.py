@@ -52,7 +52,7 @@ PEAK_HBM_GBS = 8000.0
 # calibrated against a 256 MiB copy (profiles/pmc_gemm_gate_up_config1.md).
 GATE_UP_TRAFFIC_BYTES = 361.7e6
 # HBM bytes per launch of the fused attention kernel, same method (profiles/pmc_attention_step_config1.md)
-ATTN_TRAFFIC_BYTES = 418.8e6
+ATTN_TRAFFIC_BYTES = 420.4e6
 
 
 def build_workload(cfg, layers, device, seed=0):

@@ -48,7 +48,10 @@ namespace dyllm {
 constexpr int kGemmBK = 64;
 constexpr int kGemmBN = 256;
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+// x * sigmoid(x) with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE division:
+// within 2-3 ulp of fp32 x / (1 + exp(-x)) before the bf16 rounding of the product (saturates
+// to -0 / x at the tails like the division does)
+__device__ __forceinline__ float silu_f(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ float bf16_rt(float x) { return __uint_as_float(uint32_t(f32_to_bf16(x)) << 16); }
 __device__ __forceinline__ void bf16x4_to_f32(uint2 v, float* f) {
   f[0] = __uint_as_float(v.x << 16);
@@ -56,6 +59,12 @@ __device__ __forceinline__ void bf16x4_to_f32(uint2 v, float* f) {
   f[2] = __uint_as_float(v.y << 16);
   f[3] = __uint_as_float(v.y & 0xffff0000u);
 }
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8),
+// issued through the builtin rather than inline asm so that the compiler's own wait insertion sees
+// them (it does not parse inline asm, and would otherwise re-wait on LDS reads already complete)
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int waitcnt_lgkm0() { return 15 | (3 << 14) | (7 << 4); }
 
 // element offset of (row, 16-byte chunk) in a swizzled 64-element-wide tile. gfx950 serves a
 // 16-byte LDS read for 16 lanes at a time over 64 banks (two 128-byte rows): the 16 rows a
@@ -216,9 +225,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   // of slice kt+2 (issued last) in flight: A and W of slice kt+1 have landed.
   static_assert(CW == 4 || CW == 6 || CW == 8, "vmcnt immediates below cover 4, 6 or 8 W blocks per wavefront");
   auto wait_w_in_flight = [&]() {   // vmcnt(CW): only the newest CW loads (W of slice kt+2) in flight
-    if constexpr (CW == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else if constexpr (CW == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(CW));
   };
   stage_a(0, 0);
   stage_w(0, 0);
@@ -226,7 +233,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     stage_w(1, 1);
     wait_w_in_flight();
   } else {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   __builtin_amdgcn_s_barrier();
   int wcur = 0;   // kt % 3
@@ -264,11 +271,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     __builtin_amdgcn_s_setprio(0);
     // this wave's LDS reads of the slice (substep 3 included) are done before any wave
     // refills its buffers
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0());
     if (kt + 2 < nk) {
       wait_w_in_flight();
     } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     }
     __builtin_amdgcn_s_barrier();
     wcur = wcur == 2 ? 0 : wcur + 1;
