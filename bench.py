@@ -45,6 +45,12 @@ if ROOT not in sys.path:
 
 CONFIG1 = dict(layers=32, hidden=4096, heads=32, kv_heads=32, head_dim=128, inter=12288, batch=8, prompt=256,
                response=768, tau=0.99, perturb=0.15)
+# BASELINE.json configs[2] (Dream-v0-7B shape, GQA 28/4, perturbed fraction 25 % of {5, 25, 50} %) and
+# configs[4] (LLaDA-8B shape at 8192 rows per sequence, tau 0.995, refresh every 8 steps)
+CONFIG2 = dict(layers=28, hidden=3584, heads=28, kv_heads=4, head_dim=128, inter=18944, batch=16, prompt=512,
+               response=1536, tau=0.99, perturb=0.25)
+CONFIG4 = dict(layers=32, hidden=4096, heads=32, kv_heads=32, head_dim=128, inter=12288, batch=2, prompt=2048,
+               response=6144, tau=0.995, perturb=0.05)
 PEAK_BF16_TFLOPS = 2500.0
 EVENT_STRIDE = 8
 PEAK_HBM_GBS = 8000.0
@@ -483,6 +489,106 @@ def _attn_flops(T, L, HD, n, n_seq_sal):
     return 4.0 * L * HD * n + 2.0 * L * HD * (T - n) + 2.0 * n_seq_sal * HD * (T - n)
 
 
+def _read_attn_timer():
+    import ctypes
+
+    from dyllm_amd import _lib
+    ms, n = ctypes.c_float(), ctypes.c_int()
+    _lib.call("dyllm_attention_timer_read", ctypes.addressof(ms), ctypes.addressof(n))
+    return ms.value, n.value
+
+
+def _run_cadence(wl, steps, period, layers):
+    """Timed denoise steps of a built workload: step i is a refresh step when i % period ==
+    period - 1, a Q-pruned step otherwise. Per step kind: wall times, salient rows per layer, the
+    fused attention launches (library HIP events) and the gate_up / down launches (HIP events on
+    every EVENT_STRIDE-th layer)."""
+    import torch
+
+    _read_attn_timer()
+    kinds = {False: dict(ms=[], attn=[0.0, 0], gate=[], down=[], n_sal=[]),
+             True: dict(ms=[], attn=[0.0, 0], gate=[], down=[], n_sal=[])}
+    for i in range(steps):
+        refresh = i % period == period - 1
+        k = kinds[refresh]
+        wl["restore"]()
+        # GEMM launches are bracketed with HIP events on every EVENT_STRIDE-th layer: each event
+        # pair is a pair of marker packets on the stream, so bracketing all layers would add their
+        # cost to the measured step
+        evs = {li: {"gate_up": (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)),
+                    "down": (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))}
+               for li in range(0, layers, EVENT_STRIDE)}
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        wl["step"](events=evs, n_sal=k["n_sal"], refresh=refresh)
+        torch.cuda.synchronize()
+        k["ms"].append((time.perf_counter() - t0) * 1e3)
+        k["gate"] += [e["gate_up"][0].elapsed_time(e["gate_up"][1]) for e in evs.values()]
+        k["down"] += [e["down"][0].elapsed_time(e["down"][1]) for e in evs.values()]
+        ms, n = _read_attn_timer()
+        k["attn"][0] += ms
+        k["attn"][1] += n
+    return kinds
+
+
+def _summarize(kinds, cfg, Tq, Tk):
+    """Per step kind: mean step time, salient rows per layer, and the mean launch time and
+    algorithmic work of the fused attention kernel and of the two FFN GEMMs."""
+    hid, inter = cfg["hidden"], cfg["inter"]
+    L = cfg["prompt"] + cfg["response"]
+    HD = cfg["heads"] * cfg["head_dim"]
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
+    per = {}
+    for refresh, k in kinds.items():
+        if not k["ms"]:
+            continue
+        n = mean(k["n_sal"])
+        T = Tk if refresh else Tq
+        attn_ms = k["attn"][0] / max(k["attn"][1], 1)
+        af = _attn_flops(T, L, HD, n, n / cfg["batch"])
+        per[refresh] = dict(ms=mean(k["ms"]), n=n, attn_ms=attn_ms, attn_flops=af,
+                            attn_tf=af / (attn_ms * 1e-3) / 1e12, gate_ms=mean(k["gate"]),
+                            down_ms=mean(k["down"]), gu_flops=2.0 * n * hid * 2 * inter, dn_flops=2.0 * n * inter * hid)
+    return per
+
+
+def time_config(name, cfg, steps, period, note):
+    """Another configuration's sparse denoise steps (all its layers, the same timed step as
+    config 1's), reported beside the config-1 line: step time at its cadence, tokens/s, and the
+    fused attention and gate_up launches."""
+    import torch
+
+    layers = cfg["layers"]
+    wl = build_workload(cfg, layers, "cuda:0", seed=1)
+    wl["restore"]()
+    wl["step"](refresh=False)
+    torch.cuda.synchronize()
+    kinds = _run_cadence(wl, steps, period, layers)
+    Tq, Tk = wl["Tq"], wl["Tk"]
+    per = _summarize(kinds, cfg, Tq, Tk)
+    del wl
+    torch.cuda.empty_cache()
+    ms = (sum(kinds[False]["ms"]) + sum(kinds[True]["ms"])) / steps
+    out = {"workload": f"{name}: {note}", "layers": layers, "batch": cfg["batch"],
+           "seq_len": cfg["prompt"] + cfg["response"], "response_len": cfg["response"], "hidden": cfg["hidden"],
+           "heads": cfg["heads"], "kv_heads": cfg["kv_heads"], "ffn": cfg["inter"], "tau": cfg["tau"],
+           "perturbed": cfg["perturb"], "steps": steps, "refresh_every": period,
+           "ms_per_step": round(ms, 4), "tokens_per_s": round(Tq / (ms / 1e3), 1)}
+    for refresh, key in ((False, "q_pruned"), (True, "refresh")):
+        if refresh not in per:
+            continue
+        r = per[refresh]
+        out[key] = {"ms_per_step": round(r["ms"], 4), "avg_salient_rows_per_layer": round(r["n"], 1),
+                    "attention_us": round(r["attn_ms"] * 1e3, 2),
+                    "attention_tflops": round(r["attn_tf"], 1),
+                    "attention_frac": round(r["attn_tf"] / PEAK_BF16_TFLOPS, 4),
+                    "gate_up_us": round(r["gate_ms"] * 1e3, 2),
+                    "gate_up_frac": round(r["gu_flops"] / (r["gate_ms"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                    "down_us": round(r["down_ms"] * 1e3, 2)}
+    print(f"[bench] {name}: {ms:.3f} ms/step, {out['tokens_per_s']:.0f} tokens/s", file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -491,6 +597,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--layers", type=int, default=None, help="debug only: fewer layers than the model has")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true", help="skip the config-2 / config-4 step lines")
     ap.add_argument("--profile-gate-up", action="store_true",
                     help="run only the gate_up GEMM + a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--profile-hbm", action="store_true",
@@ -501,8 +608,6 @@ def main():
               "(sequences would split across data-parallel ranks with no exchange). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
-
-    import ctypes
 
     import torch
 
@@ -525,34 +630,7 @@ def main():
         wl["step"](refresh=(i % 2 == 1))
     torch.cuda.synchronize()
 
-    def read_attn_timer():
-        ms, n = ctypes.c_float(), ctypes.c_int()
-        _lib.call("dyllm_attention_timer_read", ctypes.addressof(ms), ctypes.addressof(n))
-        return ms.value, n.value
-
-    read_attn_timer()
-    kinds = {False: dict(ms=[], attn=[0.0, 0], gate=[], down=[], n_sal=[]),
-             True: dict(ms=[], attn=[0.0, 0], gate=[], down=[], n_sal=[])}
-    for i in range(args.steps):
-        refresh = i % 4 == 3
-        k = kinds[refresh]
-        wl["restore"]()
-        # GEMM launches are bracketed with HIP events on every EVENT_STRIDE-th layer: each event
-        # pair is a pair of marker packets on the stream, so bracketing all 32 would add their cost
-        # to the measured step
-        evs = {li: {"gate_up": (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)),
-                    "down": (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))}
-               for li in range(0, layers, EVENT_STRIDE)}
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        wl["step"](events=evs, n_sal=k["n_sal"], refresh=refresh)
-        torch.cuda.synchronize()
-        k["ms"].append((time.perf_counter() - t0) * 1e3)
-        k["gate"] += [e["gate_up"][0].elapsed_time(e["gate_up"][1]) for e in evs.values()]
-        k["down"] += [e["down"][0].elapsed_time(e["down"][1]) for e in evs.values()]
-        ms, n = read_attn_timer()
-        k["attn"][0] += ms
-        k["attn"][1] += n
+    kinds = _run_cadence(wl, args.steps, 4, layers)
     total_ms = sum(kinds[False]["ms"]) + sum(kinds[True]["ms"])
     ms_per_step = total_ms / args.steps
     Tq, Tk = wl["Tq"], wl["Tk"]
@@ -560,19 +638,7 @@ def main():
 
     hid, inter = cfg["hidden"], cfg["inter"]
     L = cfg["prompt"] + cfg["response"]
-    HD = cfg["heads"] * cfg["head_dim"]
-    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")
-    per = {}
-    for refresh, k in kinds.items():
-        if not k["ms"]:
-            continue
-        n = mean(k["n_sal"])
-        T = Tk if refresh else Tq
-        attn_ms = k["attn"][0] / max(k["attn"][1], 1)
-        af = _attn_flops(T, L, HD, n, n / cfg["batch"])
-        per[refresh] = dict(ms=mean(k["ms"]), n=n, attn_ms=attn_ms, attn_flops=af,
-                            attn_tf=af / (attn_ms * 1e-3) / 1e12, gate_ms=mean(k["gate"]),
-                            down_ms=mean(k["down"]), gu_flops=2.0 * n * hid * 2 * inter, dn_flops=2.0 * n * inter * hid)
+    per = _summarize(kinds, cfg, Tq, Tk)
     q = per[False]
     print(f"[bench] {ms_per_step:.3f} ms/step at the cadence; Q-pruned {q['ms']:.3f} ms "
           f"({q['n']:.0f} salient rows/layer), attention {q['attn_ms'] * 1e3:.1f} us -> {q['attn_tf']:.1f} TFLOP/s, "
@@ -629,6 +695,12 @@ def main():
           f"MoE (config 3) {extra['roofline_moe_config3']['avg_launch_us']:.1f} us -> "
           f"{extra['roofline_moe_config3']['achieved']:.1f} TFLOP/s, kv projection {kv_proj['avg_launch_us']:.1f} us",
           file=sys.stderr, flush=True)
+
+    if not args.no_other_configs:
+        extra["config2_step"] = time_config("config2", CONFIG2, 4, 4, "Dream-v0-7B shape (GQA 28/4, FFN 18944), "
+                                            "B=16 x (512+1536), 25 % perturbed, refresh every 4th step")
+        extra["config4_step"] = time_config("config4", CONFIG4, 8, 8, "LLaDA-8B shape, B=2 x (2048+6144), "
+                                            "tau 0.995, 5 % perturbed, refresh every 8th step")
 
     cpu = None
     if not args.no_cpu_baseline:
