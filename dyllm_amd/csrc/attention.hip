@@ -34,7 +34,7 @@ constexpr int kBK = 64;              // keys per block (reference block width)
 constexpr int kKStride = kD + 8;     // K tile row stride (elements): 272 B, conflict-free b128 reads
 constexpr int kVStride = kBK + 12;   // V^T tile row stride (elements): 152 B, conflict-free b64 reads
 
-// Two-pass column-sparse path (sequences of at most kMaxBlk2 key blocks): LDS it needs beyond
+// Two-pass column-sparse path (keys in chunks of kMaxBlk2 blocks): LDS it needs beyond
 // the K / V^T tiles.
 constexpr int kMaxBlk2 = 64;
 struct ColSparseLds {
@@ -62,7 +62,7 @@ __device__ __forceinline__ int xcd_remap(int wg, int nwg) {
 
 // One (sequence, head, query tile) of NW*32 rows. wg is the tile index after the XCD remap
 // (all query tiles of one (sequence, kv-head) land on the same XCD and share its L2).
-template <AttnMode MODE, int NW>
+template <AttnMode MODE, int NW, bool CHUNKED = false>
 __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16_t* __restrict__ k_lds,
                                                uint16_t* __restrict__ vt_lds, const ColSparseLds& sp) {
   constexpr int NT = NW * 64;              // threads
@@ -226,7 +226,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
   };
 
   bool two_pass = false;
-  if constexpr (MODE == AttnMode::ColSparse) two_pass = sp.m != nullptr && nkb <= kMaxBlk2;
+  if constexpr (MODE == AttnMode::ColSparse) two_pass = sp.m != nullptr && (CHUNKED || nkb <= kMaxBlk2);
   if (two_pass) {
     // Two passes instead of PV on every 16-key group that holds a salient key.
     // Pass 1: S = Q K^T over all keys for the running max and row sum only (the same fp32
@@ -235,6 +235,10 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     // sequence, P = bf16(exp2(S*c2 - m_kb*c2)) -- the identical bf16 values the single pass
     // feeds its PV -- and O += P dV with the accumulator rescaled from the previous group's
     // block max to this one's (the product of the per-block rescales in one factor).
+    // The LDS max table holds kMaxBlk2 blocks (4096 keys); longer sequences are taken in chunks of
+    // that many blocks, pass 1 and pass 2 of a chunk before the next chunk's pass 1, with the
+    // running maxima, the row sums and pass 2's accumulator (and its rescale chain) carried from
+    // chunk to chunk: the same P values and the same accumulation as one chunk would give.
     float* m_tab = sp.m + w * (kMaxBlk2 * 32) + ql;
     auto qk = [&](f32x16_t (&sa)[2], const uint16_t* kt) {
 #pragma unroll
@@ -272,13 +276,15 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     // staged while block kb is scored, one barrier per block
     static_assert(kBK * kKStride <= kD * kVStride, "V^T tile too small for a K tile");
     if (nkb > 0) fetch_k(0);   // in flight while the group list is built
-    if (w == 0) {
-      // salient-key groups of this sequence from the per-block key bits
+    // salient-key groups of blocks kb0 .. kb0+nkc-1 from the per-block key bits (wave 0; keys and
+    // blocks relative to kb0)
+    auto build_groups = [&](int kb0, int nkc) {
+      if (w != 0) return;
       uint64_t word = 0;
       int grp = 0;
-      if (lane < nkb) {
-        word = a.kmask[int64_t(b) * a.nblk + lane];
-        if (lane == nkb - 1 && (Lk & (kBK - 1))) word &= (1ull << (Lk & (kBK - 1))) - 1;   // keys < Lk only
+      if (lane < nkc) {
+        word = a.kmask[int64_t(b) * a.nblk + kb0 + lane];
+        if (kb0 + lane == nkb - 1 && (Lk & (kBK - 1))) word &= (1ull << (Lk & (kBK - 1))) - 1;   // keys < Lk only
         grp = (__popcll(word) + 15) >> 4;
       }
       int inc = grp;
@@ -297,214 +303,292 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       }
       for (; n < grp * 16; ++n) sp.keys[g0 * 16 + n] = -1;
       for (int j = 0; j < grp; ++j) sp.gblk[g0 + j] = uint8_t(lane);
-    }
-    // Wavefronts pair up (w, w^1) over the pair's two 32-row groups, and wave w scores the key
-    // blocks of parity w & 1 for both groups: every K fragment read from LDS feeds two MFMAs (half
-    // the LDS reads per row, four independent accumulation chains). Each wave keeps a partial
-    // (max, sum) per group over its blocks and records each block's own maximum; afterwards the
-    // partner's partial is merged through LDS (fp32-rounding-level difference from the
-    // sequential sum) and the block maxima are turned into the exact running maxima pass 2 needs.
-    // K: blocks 2j and 2j+1 are staged together (K tile and the idle V^T tile), one barrier each.
-    const int pg = w ^ 1, par = w & 1;
-    bf16x8_t qf2[8];   // the partner group's Q fragments
-    {
-      const int prow = row_beg + tile * BQ + pg * 32 + ql;
-      const uint16_t* qp = a.Q + int64_t(prow) * ldq + head * kD + half * 8;
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        Pack8 p;
-        p.q = prow < row_end ? *reinterpret_cast<const uint4*>(qp + 16 * s) : make_uint4(0, 0, 0, 0);
-        qf2[s] = p.v;
-      }
-    }
-    float* const mt_par = sp.m + pg * (kMaxBlk2 * 32) + ql;
-    float pm[2] = {-FLT_MAX, -FLT_MAX}, pl[2] = {0.f, 0.f};   // [own group, partner group]
-    uint4 kreg1[KCH];
-    auto fetch_k1 = [&](int kb) {
-      const int key0 = kb * kBK;
-#pragma unroll
-      for (int it = 0; it < KCH; ++it) {
-        const int c = tid + NT * it;
-        const int key = c >> 4, dc = c & 15;
-        kreg1[it] = (key0 + key < Lk) ? *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8)
-                                      : make_uint4(0, 0, 0, 0);
-      }
     };
-    auto stage_k1 = [&]() {
+    // pass 2's accumulator state, carried from chunk to chunk
+    float m_prev = -FLT_MAX;
+    int blk_prev = -1;
+    auto pass2 = [&](int kb0, int ngrp) {
+      // ---- pass 2 ---- over the groups of blocks kb0 .. (ngrp groups, read before the barrier
+      // that precedes this call)
+      const int npb = (ngrp + 3) >> 2;
+      // slots past the last group (the tail of the last 64-slot block) were never written
+      auto slot_key = [&](int sl) -> int {
+        const int kr = sl < ngrp * 16 ? int(sp.keys[sl]) : -1;
+        return kr < 0 ? -1 : kb0 * kBK + kr;
+      };
+      auto load_meta2 = [&](int pb) {
+        if (pb >= npb) return;
 #pragma unroll
-      for (int it = 0; it < KCH; ++it) {
-        const int c = tid + NT * it;
-        const int key = c >> 4, dc = c & 15;
-        *reinterpret_cast<uint4*>(&vt_lds[key * kKStride + dc * 8]) = kreg1[it];
-      }
-    };
-    if (nkb > 1) fetch_k1(1);
-    for (int j = 0; 2 * j < nkb; ++j) {
-      stage_k(k_lds);
-      if (2 * j + 1 < nkb) stage_k1();
-      __syncthreads();
-      if (2 * j + 2 < nkb) fetch_k(2 * j + 2);
-      if (2 * j + 3 < nkb) fetch_k1(2 * j + 3);
-      const int kb = 2 * j + par;
-      if (kb < nkb) {
-        const uint16_t* kt = par ? vt_lds : k_lds;
-        f32x16_t sa[2][2];   // [group][32-key half]
+        for (int it = 0; it < VIT; ++it) {
+          const int kq = (tid + NT * it) & 15;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sa[0][t][r] = sa[1][t][r] = 0.f;
-#pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(&kt[(t * 32 + ql) * kKStride + 16 * s + half * 8]);
-            sa[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sa[0][t], 0, 0, 0);
-            sa[1][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf2[s], sa[1][t], 0, 0, 0);
+          for (int j = 0; j < 4; ++j) {
+            const int key = slot_key(pb * kBK + 4 * kq + j);
+            meta_slot[it][j] = key < 0 ? -1 : (ks_b ? ks_b[key] : key);
           }
         }
+      };
+      auto fetch2 = [&](int pb) {
+#pragma unroll
+        for (int it = 0; it < KCH; ++it) {
+          const int c = tid + NT * it;
+          const int key = slot_key(pb * kBK + (c >> 4)), dc = c & 15;
+          kreg[it] = key >= 0 ? *reinterpret_cast<const uint4*>(Kb + int64_t(key) * ldkv + dc * 8) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int it = 0; it < VIT; ++it) {
+          const int dc = (tid + NT * it) >> 4;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int64_t r = meta_slot[it][j];
+            vreg[it][j] = (r >= 0) ? *reinterpret_cast<const uint4*>(Vb + r * ldkv + dc * 8) : make_uint4(0, 0, 0, 0);
+          }
+        }
+      };
+      mask_next = ~0ull;
+      load_meta2(0);
+      if (npb > 0) fetch2(0);
+      load_meta2(1);
+      for (int pb = 0; pb < npb; ++pb) {
+        stage();
+        __syncthreads();
+        if (pb + 1 < npb) fetch2(pb + 1);
+        load_meta2(pb + 2);
+        f32x16_t sa[2];
+        qk(sa, k_lds);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int g = pb * 4 + t * 2 + u;
+            if (g >= ngrp) continue;
+            const int blkl = __builtin_amdgcn_readfirstlane(int(sp.gblk[g]));
+            const int blk = kb0 + blkl;
+            const float m_g = m_tab[blkl * 32];
+            if (blk != blk_prev) {
+              const float f = __builtin_amdgcn_exp2f((m_prev - m_g) * c2);
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o_acc[i][r] *= f;
+              m_prev = m_g;
+              blk_prev = blk;
+            }
+            const float m2 = m_g * c2;
+            Pack8 p;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[t][8 * u + 2 * j], c2, -m2));
+              const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[t][8 * u + 2 * j + 1], c2, -m2));
+              p.u[j] = pack_bf16x2(e0, e1);
+            }
+            const int kofs = t * 32 + u * 16 + half * 4;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+              const uint16_t* vr = &vt_lds[(dt * 32 + ql) * kVStride + kofs];
+              Pack4 lo, hi;
+              lo.d = *reinterpret_cast<const uint2*>(vr);
+              hi.d = *reinterpret_cast<const uint2*>(vr + 8);
+              Pack8 va;
+              va.u[0] = lo.u[0];
+              va.u[1] = lo.u[1];
+              va.u[2] = hi.u[0];
+              va.u[3] = hi.u[1];
+              o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, p.v, o_acc[dt], 0, 0, 0);
+            }
+          }
+        __syncthreads();
+      }
+    };
+    if (!CHUNKED || nkb <= kMaxBlk2) {
+      if (nkb > 0) fetch_k(0);   // in flight while the group list is built
+      build_groups(0, nkb);
+      // Wavefronts pair up (w, w^1) over the pair's two 32-row groups, and wave w scores the key
+      // blocks of parity w & 1 for both groups: every K fragment read from LDS feeds two MFMAs (half
+      // the LDS reads per row, four independent accumulation chains). Each wave keeps a partial
+      // (max, sum) per group over its blocks and records each block's own maximum; afterwards the
+      // partner's partial is merged through LDS (fp32-rounding-level difference from the
+      // sequential sum) and the block maxima are turned into the exact running maxima pass 2 needs.
+      // K: blocks 2j and 2j+1 are staged together (K tile and the idle V^T tile), one barrier each.
+      const int pg = w ^ 1, par = w & 1;
+      bf16x8_t qf2[8];   // the partner group's Q fragments
+      {
+        const int prow = row_beg + tile * BQ + pg * 32 + ql;
+        const uint16_t* qp = a.Q + int64_t(prow) * ldq + head * kD + half * 8;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          Pack8 p;
+          p.q = prow < row_end ? *reinterpret_cast<const uint4*>(qp + 16 * s) : make_uint4(0, 0, 0, 0);
+          qf2[s] = p.v;
+        }
+      }
+      float* const mt_par = sp.m + pg * (kMaxBlk2 * 32) + ql;
+      float pm[2] = {-FLT_MAX, -FLT_MAX}, pl[2] = {0.f, 0.f};   // [own group, partner group]
+      uint4 kreg1[KCH];
+      auto fetch_k1 = [&](int kb) {
         const int key0 = kb * kBK;
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          if (key0 + kBK > Lk) {  // ragged last block only
+        for (int it = 0; it < KCH; ++it) {
+          const int c = tid + NT * it;
+          const int key = c >> 4, dc = c & 15;
+          kreg1[it] = (key0 + key < Lk) ? *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8)
+                                        : make_uint4(0, 0, 0, 0);
+        }
+      };
+      auto stage_k1 = [&]() {
+#pragma unroll
+        for (int it = 0; it < KCH; ++it) {
+          const int c = tid + NT * it;
+          const int key = c >> 4, dc = c & 15;
+          *reinterpret_cast<uint4*>(&vt_lds[key * kKStride + dc * 8]) = kreg1[it];
+        }
+      };
+      if (nkb > 1) fetch_k1(1);
+      for (int j = 0; 2 * j < nkb; ++j) {
+        stage_k(k_lds);
+        if (2 * j + 1 < nkb) stage_k1();
+        __syncthreads();
+        if (2 * j + 2 < nkb) fetch_k(2 * j + 2);
+        if (2 * j + 3 < nkb) fetch_k1(2 * j + 3);
+        const int kb = 2 * j + par;
+        if (kb < nkb) {
+          const uint16_t* kt = par ? vt_lds : k_lds;
+          f32x16_t sa[2][2];   // [group][32-key half]
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sa[0][t][r] = sa[1][t][r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+              const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(&kt[(t * 32 + ql) * kKStride + 16 * s + half * 8]);
+              sa[0][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sa[0][t], 0, 0, 0);
+              sa[1][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf2[s], sa[1][t], 0, 0, 0);
+            }
+          }
+          const int key0 = kb * kBK;
+#pragma unroll
+          for (int g = 0; g < 2; ++g) {
+            if (key0 + kBK > Lk) {  // ragged last block only
+#pragma unroll
+              for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                  const int key = key0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                  if (key >= Lk) sa[g][t][r] = -FLT_MAX;
+                }
+            }
+            float bm = sa[g][0][0];
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-              for (int r = 0; r < 16; ++r) {
-                const int key = key0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-                if (key >= Lk) sa[g][t][r] = -FLT_MAX;
+              for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sa[g][t][r]);
+            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            const float m_new = fmaxf(pm[g], bm);
+            const float rescale = __builtin_amdgcn_exp2f((pm[g] - m_new) * c2);
+            const float m2 = m_new * c2;
+            pm[g] = m_new;
+            float psum = 0.f;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+              for (int r = 0; r < 16; r += 2) {
+                const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[g][t][r], c2, -m2));
+                const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[g][t][r + 1], c2, -m2));
+                psum += e0 + e1;
               }
+            pl[g] = pl[g] * rescale + psum;
+            if (half == 0) (g == 0 ? m_tab : mt_par)[kb * 32] = bm;   // the block's own maximum
           }
-          float bm = sa[g][0][0];
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sa[g][t][r]);
-          bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-          const float m_new = fmaxf(pm[g], bm);
-          const float rescale = __builtin_amdgcn_exp2f((pm[g] - m_new) * c2);
-          const float m2 = m_new * c2;
-          pm[g] = m_new;
-          float psum = 0.f;
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) {
-              const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[g][t][r], c2, -m2));
-              const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[g][t][r + 1], c2, -m2));
-              psum += e0 + e1;
-            }
-          pl[g] = pl[g] * rescale + psum;
-          if (half == 0) (g == 0 ? m_tab : mt_par)[kb * 32] = bm;   // the block's own maximum
         }
+        __syncthreads();
       }
+      // merge the partner's partial for this wave's group; running maxima of the group's blocks
+      // (the maximum is shared by both half-waves, the sum is per lane: each half holds other keys)
+      sp.xch[pg * 96 + lane] = pl[1];
+      if (half == 0) sp.xch[pg * 96 + 64 + ql] = pm[1];
       __syncthreads();
-    }
-    // merge the partner's partial for this wave's group; running maxima of the group's blocks
-    // (the maximum is shared by both half-waves, the sum is per lane: each half holds other keys)
-    sp.xch[pg * 96 + lane] = pl[1];
-    if (half == 0) sp.xch[pg * 96 + 64 + ql] = pm[1];
-    __syncthreads();
-    {
-      const float mb = sp.xch[w * 96 + 64 + ql], lb = sp.xch[w * 96 + lane];
-      m_run = fmaxf(pm[0], mb);
-      l_run = pl[0] * __builtin_amdgcn_exp2f((pm[0] - m_run) * c2) + lb * __builtin_amdgcn_exp2f((mb - m_run) * c2);
-      if (half == 0) {
-        float run = -FLT_MAX;
-        for (int kb = 0; kb < nkb; ++kb) {
-          run = fmaxf(run, m_tab[kb * 32]);
-          m_tab[kb * 32] = run;
+      {
+        const float mb = sp.xch[w * 96 + 64 + ql], lb = sp.xch[w * 96 + lane];
+        m_run = fmaxf(pm[0], mb);
+        l_run = pl[0] * __builtin_amdgcn_exp2f((pm[0] - m_run) * c2) + lb * __builtin_amdgcn_exp2f((mb - m_run) * c2);
+        if (half == 0) {
+          float run = -FLT_MAX;
+          for (int kb = 0; kb < nkb; ++kb) {
+            run = fmaxf(run, m_tab[kb * 32]);
+            m_tab[kb * 32] = run;
+          }
         }
       }
-    }
-    __syncthreads();
-    // (the last barrier also ends pass 1's reads of both tiles before pass 2 restages them)
+      const int ngrp = *sp.ngrp;
+      __syncthreads();
+      // (the last barrier also ends pass 1's reads of both tiles before pass 2 restages them)
+      pass2(0, ngrp);
 
-    // ---- pass 2 ----
-    const int ngrp = *sp.ngrp;
-    const int npb = (ngrp + 3) >> 2;
-    // slots past the last group (the tail of the last 64-slot block) were never written
-    auto slot_key = [&](int sl) -> int { return sl < ngrp * 16 ? int(sp.keys[sl]) : -1; };
-    auto load_meta2 = [&](int pb) {
-      if (pb >= npb) return;
+    } else if constexpr (CHUNKED) {
+        // chunked: pass 1 scores one 32-row group per wavefront (no pairing: pass 2's accumulator
+        // stays live through the next chunk's pass 1, which leaves no registers for a second group)
+        float m_carry = -FLT_MAX;   // running maximum after the previous chunk (half 0 lanes)
+        float pm1 = -FLT_MAX, pl1 = 0.f;
+        for (int kb0 = 0; kb0 < nkb; kb0 += kMaxBlk2) {
+          const int nkc = min(kMaxBlk2, nkb - kb0);
+          fetch_k(kb0);
+          build_groups(kb0, nkc);
+          for (int kbl = 0; kbl < nkc; ++kbl) {
+            stage_k(k_lds);
+            __syncthreads();
+            if (kbl + 1 < nkc) fetch_k(kb0 + kbl + 1);
+            f32x16_t sa[2];
+            qk(sa, k_lds);
+            const int key0 = (kb0 + kbl) * kBK;
+            if (key0 + kBK > Lk) {  // ragged last block only
 #pragma unroll
-      for (int it = 0; it < VIT; ++it) {
-        const int kq = (tid + NT * it) & 15;
+              for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = slot_key(pb * kBK + 4 * kq + j);
-          meta_slot[it][j] = key < 0 ? -1 : (ks_b ? ks_b[key] : key);
-        }
-      }
-    };
-    auto fetch2 = [&](int pb) {
+                for (int r = 0; r < 16; ++r) {
+                  const int key = key0 + t * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+                  if (key >= Lk) sa[t][r] = -FLT_MAX;
+                }
+            }
+            float bm = sa[0][0];
 #pragma unroll
-      for (int it = 0; it < KCH; ++it) {
-        const int c = tid + NT * it;
-        const int key = slot_key(pb * kBK + (c >> 4)), dc = c & 15;
-        kreg[it] = key >= 0 ? *reinterpret_cast<const uint4*>(Kb + int64_t(key) * ldkv + dc * 8) : make_uint4(0, 0, 0, 0);
-      }
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int it = 0; it < VIT; ++it) {
-        const int dc = (tid + NT * it) >> 4;
+              for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sa[t][r]);
+            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            const float m_new = fmaxf(pm1, bm);
+            const float rescale = __builtin_amdgcn_exp2f((pm1 - m_new) * c2);
+            const float m2 = m_new * c2;
+            pm1 = m_new;
+            float psum = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t r = meta_slot[it][j];
-          vreg[it][j] = (r >= 0) ? *reinterpret_cast<const uint4*>(Vb + r * ldkv + dc * 8) : make_uint4(0, 0, 0, 0);
-        }
-      }
-    };
-    mask_next = ~0ull;
-    load_meta2(0);
-    if (npb > 0) fetch2(0);
-    load_meta2(1);
-    float m_prev = -FLT_MAX;
-    int blk_prev = -1;
-    for (int pb = 0; pb < npb; ++pb) {
-      stage();
-      __syncthreads();
-      if (pb + 1 < npb) fetch2(pb + 1);
-      load_meta2(pb + 2);
-      f32x16_t sa[2];
-      qk(sa, k_lds);
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int g = pb * 4 + t * 2 + u;
-          if (g >= ngrp) continue;
-          const int blk = __builtin_amdgcn_readfirstlane(int(sp.gblk[g]));
-          const float m_g = m_tab[blk * 32];
-          if (blk != blk_prev) {
-            const float f = __builtin_amdgcn_exp2f((m_prev - m_g) * c2);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-              for (int r = 0; r < 16; ++r) o_acc[i][r] *= f;
-            m_prev = m_g;
-            blk_prev = blk;
+              for (int r = 0; r < 16; r += 2) {
+                const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[t][r], c2, -m2));
+                const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[t][r + 1], c2, -m2));
+                psum += e0 + e1;
+              }
+            pl1 = pl1 * rescale + psum;
+            if (half == 0) m_tab[kbl * 32] = bm;   // the block's own maximum
+            __syncthreads();
           }
-          const float m2 = m_g * c2;
-          Pack8 p;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[t][8 * u + 2 * j], c2, -m2));
-            const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[t][8 * u + 2 * j + 1], c2, -m2));
-            p.u[j] = pack_bf16x2(e0, e1);
+          // the chunk's group count, read before the barrier below (wave 0 rewrites it for the next
+          // chunk only after that barrier)
+          const int ngrp = *sp.ngrp;
+          // running maxima of the chunk's blocks, continuing from the previous chunk
+          if (half == 0) {
+            float run = m_carry;
+            for (int kbl = 0; kbl < nkc; ++kbl) {
+              run = fmaxf(run, m_tab[kbl * 32]);
+              m_tab[kbl * 32] = run;
+            }
+            m_carry = run;
           }
-          const int kofs = t * 32 + u * 16 + half * 4;
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const uint16_t* vr = &vt_lds[(dt * 32 + ql) * kVStride + kofs];
-            Pack4 lo, hi;
-            lo.d = *reinterpret_cast<const uint2*>(vr);
-            hi.d = *reinterpret_cast<const uint2*>(vr + 8);
-            Pack8 va;
-            va.u[0] = lo.u[0];
-            va.u[1] = lo.u[1];
-            va.u[2] = hi.u[0];
-            va.u[3] = hi.u[1];
-            o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, p.v, o_acc[dt], 0, 0, 0);
-          }
+          __syncthreads();
+          pass2(kb0, ngrp);
         }
-      __syncthreads();
+        m_run = pm1;
+        l_run = pl1;
     }
     // the blocks after the last salient one rescale the accumulator to the final max
     {
@@ -749,7 +833,7 @@ attention_kernel(AttnArgs a) {
 // column-sparse tiles of all other queries in one launch, so the two run concurrently. The
 // row-sparse tiles come first (n_rs_pad of them, a multiple of 8, the excess returning at once),
 // each range remapped XCD-major on its own.
-template <int NW>
+template <int NW, bool CHUNKED>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_step_kernel(
     AttnArgs rs, AttnArgs cs, int n_rs, int n_rs_pad) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
@@ -764,8 +848,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     const int t = xcd_remap(wg, n_rs_pad);
     if (t < n_rs) attention_tile<AttnMode::RowSparse, NW>(rs, t, k_lds, vt_lds, ColSparseLds{});
   } else {
-    attention_tile<AttnMode::ColSparse, NW>(cs, xcd_remap(wg - n_rs_pad, int(gridDim.x) - n_rs_pad), k_lds, vt_lds,
-                                            ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds, xch_lds});
+    attention_tile<AttnMode::ColSparse, NW, CHUNKED>(cs, xcd_remap(wg - n_rs_pad, int(gridDim.x) - n_rs_pad), k_lds,
+                                                     vt_lds, ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds, xch_lds});
   }
 }
 
@@ -960,7 +1044,7 @@ static bool attn_aligned(const AttnArgs& a) {
 
 int attention_kernel_info(int dim, int64_t* out) {
   hipFuncAttributes fa{};
-  const void* fn = reinterpret_cast<const void*>(&attention_step_kernel<4>);
+  const void* fn = reinterpret_cast<const void*>(&attention_step_kernel<4, false>);
   if (hipFuncGetAttributes(&fa, fn) != hipSuccess) return fail("hipFuncGetAttributes failed for attention_step_kernel");
   int blocks = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 256, 0) != hipSuccess)
@@ -1008,7 +1092,12 @@ int launch_attention_step(const AttnArgs& rs0, int max_rows_rs, const AttnArgs& 
   const int64_t n_cs = int64_t(cs.tiles_per_seq) * cs.H * cs.B;
   DYLLM_REQUIRE(n_rs_pad + n_cs < (int64_t(1) << 31), "grid too large");
   if (n_rs_pad + n_cs == 0) return 0;
-  attention_step_kernel<4><<<unsigned(n_rs_pad + n_cs), 256, 0, s>>>(rs, cs, int(n_rs), int(n_rs_pad));
+  // sequences longer than the LDS max table (kMaxBlk2 key blocks) take the chunked two-pass
+  // instantiation; the other one keeps its registers for the paired pass 1
+  if (cs.nblk > kMaxBlk2)
+    attention_step_kernel<4, true><<<unsigned(n_rs_pad + n_cs), 256, 0, s>>>(rs, cs, int(n_rs), int(n_rs_pad));
+  else
+    attention_step_kernel<4, false><<<unsigned(n_rs_pad + n_cs), 256, 0, s>>>(rs, cs, int(n_rs), int(n_rs_pad));
   return check_launch("attention_step_kernel");
 }
 

@@ -62,15 +62,23 @@ def _setup(dev, q_pruned, H=4, Hkv=2, lens=((48, 80), (16, 200), (64, 64)), seed
                 t=t, md=md, H=H, Hkv=Hkv, Lq=Lq, Lk=Lk)
 
 
-@pytest.mark.parametrize("q_pruned,sal_counts", [(True, None), (False, None), (True, [0, 7, 64]), (False, [0, 0, 0]),
-                                                  (True, [80, 200, 64]), (True, [1, 0, 1])])
-def test_attention_forward_sparse_step(dev, q_pruned, sal_counts):
+# sequences longer than one 4096-key chunk of the two-pass column-sparse tiles (ragged: 2 and 3
+# chunks) beside a short one
+LONG = ((256, 4200), (64, 8300), (16, 300))
+
+
+@pytest.mark.parametrize("q_pruned,sal_counts,lens", [(True, None, None), (False, None, None), (True, [0, 7, 64], None),
+                                                       (False, [0, 0, 0], None), (True, [80, 200, 64], None),
+                                                       (True, [1, 0, 1], None), (True, [300, 500, 10], LONG),
+                                                       (False, [120, 0, 64], LONG)])
+def test_attention_forward_sparse_step(dev, q_pruned, sal_counts, lens):
     """Sparse step at layer level; the salient sets include a sequence with no salient row, no
-    salient row at all, every response row salient, and single rows."""
+    salient row at all, every response row salient, and single rows; sequences of up to 8364 keys
+    (several key chunks of the two-pass column-sparse tiles)."""
     from dyllm_amd.utils.context import set_context
 
-    print(f"[layer] q_pruned={q_pruned} sal_counts={sal_counts}", flush=True)
-    s = _setup(dev, q_pruned, sal_counts=sal_counts)
+    print(f"[layer] q_pruned={q_pruned} sal_counts={sal_counts} lens={lens}", flush=True)
+    s = _setup(dev, q_pruned, sal_counts=sal_counts, **({"lens": lens} if lens else {}))
     t, md = s["t"], s["md"]
     # oracle inputs: packed caches as the reference's get_seqs / get_seqs_block return them
     c_old = s["o_full"][torch.from_numpy(s["resp"])] if q_pruned else s["o_full"]
