@@ -482,7 +482,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
             for (int t = 0; t < 2; ++t)
 #pragma unroll
               for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sa[g][t][r]);
-            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            bm = half_swap_max(bm);
             const float m_new = fmaxf(pm[g], bm);
             const float rescale = __builtin_amdgcn_exp2f((pm[g] - m_new) * c2);
             const float m2 = m_new * c2;
@@ -554,7 +554,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
             for (int t = 0; t < 2; ++t)
 #pragma unroll
               for (int r = 0; r < 16; ++r) bm = fmaxf(bm, sa[t][r]);
-            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+            bm = half_swap_max(bm);
             const float m_new = fmaxf(pm1, bm);
             const float rescale = __builtin_amdgcn_exp2f((pm1 - m_new) * c2);
             const float m2 = m_new * c2;
@@ -639,7 +639,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) bm = fmaxf(bm, s_acc[t][r]);
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    bm = half_swap_max(bm);
     const float m_new = fmaxf(m_run, bm);
     const float rescale = __builtin_amdgcn_exp2f((m_run - m_new) * c2);
     const float m2 = m_new * c2;
@@ -694,7 +694,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
   }
 
   // ---- epilogue ---------------------------------------------------------------------------
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = half_swap_sum(l_run);
   const float inv = 1.0f / l_tot;
   if constexpr (MODE == AttnMode::RowSparse) {
     if (a.cu_q) {
@@ -728,9 +728,9 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
             }
           }
       }
-      dot += __shfl_xor(dot, 32, 64);
-      nn += __shfl_xor(nn, 32, 64);
-      oo += __shfl_xor(oo, 32, 64);
+      dot = half_swap_sum(dot);
+      nn = half_swap_sum(nn);
+      oo = half_swap_sum(oo);
       if (row_ok && half == 0) {
         a.part[(int64_t(head) * 3 + 0) * a.Tq + qrow] = dot;
         a.part[(int64_t(head) * 3 + 1) * a.Tq + qrow] = nn;
@@ -794,9 +794,9 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
           }
         }
     }
-    dot += __shfl_xor(dot, 32, 64);
-    nn += __shfl_xor(nn, 32, 64);
-    oo += __shfl_xor(oo, 32, 64);
+    dot = half_swap_sum(dot);
+    nn = half_swap_sum(nn);
+    oo = half_swap_sum(oo);
     if (own && half == 0) {
       a.part[(int64_t(head) * 3 + 0) * a.Tq + row] = dot;
       a.part[(int64_t(head) * 3 + 1) * a.Tq + row] = nn;

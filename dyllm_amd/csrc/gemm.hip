@@ -533,22 +533,12 @@ int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, int
   if (epi == GemmEpi::SwiGLU) {
     DYLLM_REQUIRE(g.N == 2 * g.half_n, "SwiGLU weight must hold gate rows then up rows (N = 2 * intermediate)");
     DYLLM_REQUIRE(g.half_n % (kGemmBN / 2) == 0, "SwiGLU intermediate size must be a multiple of 128");
-#ifdef DYLLM_GEMM_W4
-    if (tile_m == 256) return launch_gemm_cfg<256, 256, 2, GemmEpi::SwiGLU>(g, mt, 1, s);
-    if (tile_m == 192) return launch_gemm_cfg<192, 256, 2, GemmEpi::SwiGLU>(g, mt, 1, s);
-#else
     if (tile_m == 256) return launch_gemm_cfg<256, 256, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
     if (tile_m == 192) return launch_gemm_cfg<192, 256, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
-#endif
     return launch_gemm_cfg<128, 256, 4, GemmEpi::SwiGLU>(g, mt, 1, s);
   }
-#ifdef DYLLM_GEMM_W4
-  if (tile_m == 256) return launch_gemm_cfg<256, 256, 2, GemmEpi::Store>(g, mt, ksplit, s);
-  if (tile_m == 192) return launch_gemm_cfg<192, 256, 2, GemmEpi::Store>(g, mt, ksplit, s);
-#else
   if (tile_m == 256) return launch_gemm_cfg<256, 256, 4, GemmEpi::Store>(g, mt, ksplit, s);
   if (tile_m == 192) return launch_gemm_cfg<192, 256, 4, GemmEpi::Store>(g, mt, ksplit, s);
-#endif
   return launch_gemm_cfg<128, 256, 4, GemmEpi::Store>(g, mt, ksplit, s);
 }
 
