@@ -410,6 +410,64 @@ def profile_gate_up(cfg, reps=3):
           file=sys.stderr)
 
 
+def profile_attention(cfg, reps=5):
+    """Counter-collection workload for the two tile kinds of the fused attention kernel, each as
+    its standalone launch at the config-1 Q-pruned shape (6144 queried rows of 8 x 1024 keys, 15 %
+    salient): the row-sparse tiles (attention_kernel<RowSparse>: the salient queries against all
+    keys and the updated V) and the two-pass column-sparse tiles (attention_kernel<ColSparse,4>:
+    QK^T and the row statistics over all keys, PV over the salient keys' dV). Prints the HIP-event
+    time of each; run under rocprofv3 --pmc for the instruction and cycle counters."""
+    import torch
+
+    from dyllm_amd import ops
+
+    dev = "cuda"
+    B, P, R = cfg["batch"], cfg["prompt"], cfg["response"]
+    L = P + R
+    H, Hkv, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    Tq, Tk = B * R, B * L
+    n_per = int(round(cfg["perturb"] * R))
+    g = torch.Generator(device=dev).manual_seed(4)
+    gcpu = torch.Generator().manual_seed(4)
+    rnd = lambda *sh, std=1.0: torch.empty(*sh, device=dev).normal_(0.0, std, generator=g).to(torch.bfloat16)
+    q, k, v, c = rnd(Tq, H, D), rnd(Tk, Hkv, D), rnd(Tk, Hkv, D), rnd(Tq, H, D)
+    sq, sk = [], []
+    for b in range(B):
+        sel = torch.randperm(R, generator=gcpu)[:n_per].sort().values
+        sq += (b * R + sel).tolist()
+        sk += (b * L + P + sel).tolist()
+    idx_q = torch.tensor(sq, dtype=torch.int32, device=dev)
+    idx_k = torch.tensor(sk, dtype=torch.int32, device=dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    cu_q = torch.arange(B + 1, **i32) * R
+    cu_k = torch.arange(B + 1, **i32) * L
+    cu_s = torch.arange(B + 1, **i32) * n_per
+    dv = rnd(len(sk), Hkv, D, std=0.1)
+
+    def rowsparse():
+        return ops.flash_attn_varlen_func(q, k, v, cu_s, cu_k, n_per, L, q_rows=idx_q)
+
+    o_sal = rowsparse()
+
+    def colsparse():
+        ops.attention_colsparse_cached(q, k, None, dv, c, None, o_sal, cu_q, cu_k, R, L, Tk, idx_q, idx_k,
+                                       cfg["tau"], c_inplace=False)
+
+    colsparse()
+    torch.cuda.synchronize()
+    out = {}
+    for name, fn in (("row-sparse tiles", rowsparse), ("column-sparse tiles", colsparse)):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(e0.elapsed_time(e1) / reps * 1e3, 2)
+    print(f"[bench] standalone attention tiles at the config-1 Q-pruned shape ({len(sk)} salient rows), "
+          f"us per launch: {out}", file=sys.stderr)
+
+
 def time_dense_attention(cfg, reps=5):
     """Dense full-sequence attention (the full steps, attention.py:39-62: attention_kernel<Dense>)
     at the config-1 shape, T = 8192 rows, HIP events on the launching stream."""
@@ -600,6 +658,8 @@ def main():
     ap.add_argument("--no-other-configs", action="store_true", help="skip the config-2 / config-4 step lines")
     ap.add_argument("--profile-gate-up", action="store_true",
                     help="run only the gate_up GEMM + a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-attention", action="store_true",
+                    help="run only the standalone row-sparse and column-sparse attention tiles (for rocprofv3 --pmc)")
     ap.add_argument("--profile-hbm", action="store_true",
                     help="run only the standalone HBM-bound kernels at the config-1 shape and print their GB/s")
     args = ap.parse_args()
@@ -619,6 +679,9 @@ def main():
         return
     if args.profile_hbm:
         profile_hbm(cfg)
+        return
+    if args.profile_attention:
+        profile_attention(cfg)
         return
     layers = args.layers or cfg["layers"]
     dev = "cuda:0"
