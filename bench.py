@@ -366,6 +366,17 @@ def profile_hbm(cfg, reps=5):
     sel32 = sel.to(torch.int32)
     cases[-1] = (cases[-1][0], lambda: ops.kv_rope_scatter(kv, Hkv, positions, cos, sin, k_cache, idx_k, cu_k, starts,
                                                            seq_ids, pos_idx=sel32), cases[-1][2])
+    # size references: the same gather over every queried row, and torch's contiguous device copy
+    # of the salient-row bytes and of the full-size bytes (what one launch of that size reaches)
+    all_rows = torch.randperm(Tq, device=dev, generator=g)
+    src_s, dst_s = randn(n_sal, hid), randn(n_sal, hid)
+    src_f, dst_f = randn(Tq, hid), randn(Tq, hid)
+    cases += [
+        ("row_map_copy_kernel<Gather> (every queried row, permuted)", lambda: ops.gather_rows_2D(x, all_rows),
+         Tq * 2 * row),
+        ("reference: torch copy_ of the salient-row bytes", lambda: dst_s.copy_(src_s), n_sal * 2 * row),
+        ("reference: torch copy_ of the queried-row bytes", lambda: dst_f.copy_(src_f), Tq * 2 * row),
+    ]
     print("| kernel | algorithmic bytes per launch | us per launch (HIP events, back to back) | GB/s | of 8 TB/s |")
     print("|---|---:|---:|---:|---:|")
     for name, fn, nbytes in cases:

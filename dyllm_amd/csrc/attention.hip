@@ -985,7 +985,7 @@ __global__ __launch_bounds__(256) void step_salient_kernel(uint16_t* __restrict_
   const int lane = threadIdx.x & 63;
   if (j >= n) return;
   const int64_t k = idx_k64[j];
-  const int bq = find_segment(cu_k, B + 1, k);
+  const int bq = find_segment_wave(cu_k, B + 1, k);
   const int b = bq < B ? bq : B - 1;
   const int64_t off = k - cu_k[b];
   const int64_t dest = v_seq_starts[seq_ids[b]] + off;

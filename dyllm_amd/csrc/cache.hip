@@ -20,13 +20,13 @@ __device__ __forceinline__ bool map_row(const RowMapArgs& a, int64_t r, int64_t&
     return src_row >= 0 && src_row < a.src_rows;
   } else if constexpr (M == RowMap::Scatter) {
     const int64_t k = a.row_idx[r];
-    const int b = find_segment(a.cu, a.B + 1, k);
+    const int b = find_segment_wave(a.cu, a.B + 1, k);
     if (b >= a.B || k < a.cu[b] || k >= a.cu[b + 1]) return false;
     src_row = r;
     dst_row = a.seq_starts[a.seq_ids[b]] + (k - a.cu[b]);
     return true;
   } else if constexpr (M == RowMap::GetSeqs || M == RowMap::ResetFull) {
-    const int b = find_segment(a.cu, a.B + 1, r);
+    const int b = find_segment_wave(a.cu, a.B + 1, r);
     if (b >= a.B || r >= a.cu[b + 1]) return false;
     const int64_t cache_row = a.seq_starts[a.seq_ids[b]] + (r - a.cu[b]);
     if constexpr (M == RowMap::GetSeqs) {
@@ -38,7 +38,7 @@ __device__ __forceinline__ bool map_row(const RowMapArgs& a, int64_t r, int64_t&
     }
     return true;
   } else {  // GetBlock / ResetBlock: the tail Lq rows of each cached sequence
-    const int b = find_segment(a.cu_q, a.B + 1, r);
+    const int b = find_segment_wave(a.cu_q, a.B + 1, r);
     if (b >= a.B || r >= a.cu_q[b + 1]) return false;
     const int64_t Lq = a.cu_q[b + 1] - a.cu_q[b];
     const int64_t Lk = a.cu[b + 1] - a.cu[b];

@@ -87,6 +87,22 @@ __device__ __forceinline__ int find_segment(const T* cu, int n, int64_t r) {
   return lo;
 }
 
+// find_segment for a row index that is the same in every lane of the (fully active) wavefront:
+// each lane compares one prefix entry, one coalesced load per 64 entries, and the ballot count
+// replaces the binary search's chain of dependent loads. Same result as find_segment (0 when
+// r < cu[0]).
+template <typename T>
+__device__ __forceinline__ int find_segment_wave(const T* cu, int n, int64_t r) {
+  const int lane = threadIdx.x & 63;
+  int cnt = 0;
+  for (int base = 0; base < n - 1; base += 64) {
+    const int i = base + lane;
+    const bool le = i < n - 1 && int64_t(cu[i]) <= r;
+    cnt += __popcll(__ballot(le));
+  }
+  return cnt > 0 ? cnt - 1 : 0;
+}
+
 __host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---- host-side error plumbing -------------------------------------------------------

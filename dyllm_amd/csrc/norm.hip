@@ -22,7 +22,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(NormArgs a) 
   const int nch = a.hidden / 8;
   int64_t xrow = row;
   if (a.x_seq_starts) {   // the row lives in a cache slab (uniform across the workgroup)
-    const int b = find_segment(a.x_cu_q, a.x_batch + 1, row);
+    const int b = find_segment_wave(a.x_cu_q, a.x_batch + 1, row);
     xrow = a.x_seq_starts[a.x_seq_ids[b]] + (a.x_cu_k[b + 1] - a.x_cu_k[b]) - (a.x_cu_q[b + 1] - a.x_cu_q[b]) +
            (row - a.x_cu_q[b]);
   }

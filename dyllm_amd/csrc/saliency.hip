@@ -52,7 +52,29 @@ __global__ __launch_bounds__(256) void saliency_rows_kernel(const uint16_t* __re
   const uint4* po = reinterpret_cast<const uint4*>(c_old + t * D);
   float dot = 0.f, nn = 0.f, oo = 0.f;
   const int64_t n16 = D >> 3;
-  for (int64_t i = lane; i < n16; i += 64) {
+  int64_t i0 = lane;
+  // 4 passes' loads in flight per lane before the (unchanged, ascending) accumulation
+  for (; i0 + 3 * 64 < n16; i0 += 4 * 64) {
+    uint4 an[4], bo[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      an[u] = pn[i0 + u * 64];
+      bo[u] = po[i0 + u * 64];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t av[4] = {an[u].x, an[u].y, an[u].z, an[u].w}, bv[4] = {bo[u].x, bo[u].y, bo[u].z, bo[u].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float n0 = __uint_as_float(av[j] << 16), n1 = __uint_as_float(av[j] & 0xffff0000u);
+        const float o0 = __uint_as_float(bv[j] << 16), o1 = __uint_as_float(bv[j] & 0xffff0000u);
+        dot += n0 * o0 + n1 * o1;
+        nn += n0 * n0 + n1 * n1;
+        oo += o0 * o0 + o1 * o1;
+      }
+    }
+  }
+  for (int64_t i = i0; i < n16; i += 64) {
     const uint4 a = pn[i], b = po[i];
     const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
