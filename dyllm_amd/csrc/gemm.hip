@@ -118,7 +118,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
       row = m;
       if (g.a_ids) {
         const int64_t id = g.a_ids[m];
-        row = (id < g.id_limit) ? id / g.a_div : 0;
+        row = (id >= 0 && id < g.id_limit) ? id / g.a_div : 0;   // padding or out-of-range ids read row 0
       }
     }
     a_vo[i] = uint32_t((row * g.lda + lane_chunk) * 2);
@@ -312,7 +312,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     int64_t id = m;
     if (g.a_ids) {
       id = g.a_ids[m];
-      if (id >= g.id_limit) continue;
+      if (id < 0 || id >= g.id_limit) continue;
       if (g.c_by_id) drow = id;
     }
     if (g.c_rows) drow = g.c_rows[m];
@@ -404,7 +404,7 @@ __global__ __launch_bounds__(256) void gemm_partial_reduce_kernel(GemmArgs g) {
     int64_t drow = m, id = m;
     if (g.a_ids) {
       id = g.a_ids[m];
-      if (id >= g.id_limit) continue;
+      if (id < 0 || id >= g.id_limit) continue;
       if (g.c_by_id) drow = id;
     }
     if (g.c_rows) drow = g.c_rows[m];

@@ -87,74 +87,112 @@ int launch_moe_router(const uint16_t* x, const int32_t* rows, const uint16_t* wr
 }
 
 // ---- align: one workgroup of 1024 threads -----------------------------------------------
-// Pass 1 counts slots per expert (LDS atomics). Then padded bucket starts. Pass 2 walks
-// the slots in order, 1024 per round; inside a round each wavefront finds the lanes that
-// share its expert with six ballots and ranks them by lane order, and per-(wave, expert)
-// counts are prefix-summed across the 16 wavefronts: the placement is stable.
+// The slots are cut into 16 contiguous ranges, one per wavefront. Pass 1: each wavefront walks
+// its range 64 slots at a time; six ballots group the lanes that share an expert, and the
+// first lane of each group adds the group's size to the wavefront's per-expert count in LDS
+// (distinct experts per leader lane: no conflicts). After one barrier the per-expert totals give
+// the padded bucket starts and every (wavefront, expert) pair its base in the bucket. Pass 2
+// walks the ranges again and writes each slot at base + its rank among the lanes that share its
+// expert, then the leaders advance their bases. Slots keep ascending order inside a bucket
+// (ranges, rounds and lanes in order); only two workgroup barriers separate the passes, and the
+// ids of 8 rounds are loaded at once.
 __global__ __launch_bounds__(1024) void moe_align_kernel(const int32_t* __restrict__ ids, int64_t S, int E, int bm,
                                                          int32_t* __restrict__ sorted_ids, int64_t cap,
                                                          int32_t* __restrict__ tile_expert,
                                                          int32_t* __restrict__ num_post_pad) {
+  constexpr int NWV = 16;
+  __shared__ int wcnt[NWV][64];
+  __shared__ int wbase[NWV][64];
+  __shared__ int start[65];
   __shared__ int cnt[64];
-  __shared__ int start[64];
-  __shared__ int run[64];
-  __shared__ int wcnt[16][64];
-  __shared__ int total_sh;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  if (tid < 64) cnt[tid] = 0;
+  for (int x = tid; x < NWV * 64; x += 1024) (&wcnt[0][0])[x] = 0;
   __syncthreads();
   // expert ids are clamped to [0, E): an out-of-range id from a caller can never index past the
   // 64-entry LDS tables (its slot is then routed to the nearest valid expert)
   auto expert_of = [&](int64_t i) { return min(max(int(ids[i]), 0), E - 1); };
-  for (int64_t i = tid; i < S; i += 1024) atomicAdd(&cnt[expert_of(i)], 1);
+  const int64_t per = (S + NWV - 1) / NWV;
+  const int64_t c0 = int64_t(wid) * per, c1 = min(S, c0 + per);
+  // lanes of this round that share the expert e (ok lanes only)
+  auto group = [&](bool ok, int e) -> unsigned long long {
+    unsigned long long same = __ballot(ok);
+#pragma unroll
+    for (int bit = 0; bit < 6; ++bit) {
+      const unsigned long long bb = __ballot(ok && ((e >> bit) & 1));
+      same &= ((e >> bit) & 1) ? bb : ~bb;
+    }
+    return same;
+  };
+  const unsigned long long lt = (1ull << lane) - 1;
+  // the ids of kBatch rounds are loaded together (one memory latency per kBatch rounds)
+  constexpr int kBatch = 8;
+  for (int64_t r0 = c0; r0 < c1; r0 += 64 * kBatch) {
+    int ev[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t i = r0 + 64 * u + lane;
+      ev[u] = i < c1 ? expert_of(i) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const bool ok = ev[u] >= 0;
+      const int e = ok ? ev[u] : 0;
+      const unsigned long long same = group(ok, e);
+      if (ok && (same & lt) == 0) wcnt[wid][e] += __popcll(same);
+    }
+  }
+  __syncthreads();
+  if (tid < 64) {
+    int c = 0;
+    if (tid < E)
+      for (int w = 0; w < NWV; ++w) c += wcnt[w][tid];
+    cnt[tid] = c;
+  }
   __syncthreads();
   if (tid == 0) {
     int acc = 0;
     for (int e = 0; e < E; ++e) {
       start[e] = acc;
-      run[e] = 0;
       acc += (cnt[e] + bm - 1) / bm * bm;
     }
+    start[E] = acc;
     num_post_pad[0] = acc;
-    total_sh = acc;
   }
   __syncthreads();
-  const int total = total_sh;
-  // sentinel fill + tile experts
-  for (int64_t i = tid; i < cap; i += 1024) sorted_ids[i] = int32_t(S);
+  if (tid < E) {
+    int bse = start[tid];
+    for (int w = 0; w < NWV; ++w) {
+      wbase[w][tid] = bse;
+      bse += wcnt[w][tid];
+    }
+  }
+  const int total = start[E];
+  // sentinels in the padding of every bucket and past the last one (disjoint from the slots
+  // written below); the expert of every tile
   for (int e = 0; e < E; ++e) {
-    const int nt = (cnt[e] + bm - 1) / bm;
+    const int p0 = start[e] + cnt[e], p1 = start[e + 1];
+    for (int x = p0 + tid; x < p1; x += 1024) sorted_ids[x] = int32_t(S);
+    const int nt = (p1 - start[e]) / bm;
     for (int t = tid; t < nt; t += 1024) tile_expert[start[e] / bm + t] = e;
   }
+  for (int64_t x = total + tid; x < cap; x += 1024) sorted_ids[x] = int32_t(S);
   for (int64_t t = total / bm + tid; t < cap / bm; t += 1024) tile_expert[t] = 0;
   __syncthreads();
-  for (int64_t r0 = 0; r0 < S; r0 += 1024) {
-    const int64_t i = r0 + tid;
-    const bool ok = i < S;
-    const int e = ok ? expert_of(i) : 63;
-    unsigned long long same = __ballot(ok);
+  for (int64_t r0 = c0; r0 < c1; r0 += 64 * kBatch) {
+    int ev[kBatch];
 #pragma unroll
-    for (int bit = 0; bit < 6; ++bit) {
-      const unsigned long long b = __ballot(ok && ((e >> bit) & 1));
-      same &= ((e >> bit) & 1) ? b : ~b;
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t i = r0 + 64 * u + lane;
+      ev[u] = i < c1 ? expert_of(i) : -1;
     }
-    const int rank = __popcll(same & ((1ull << lane) - 1));
-    for (int x = tid; x < 16 * 64; x += 1024) (&wcnt[0][0])[x] = 0;
-    __syncthreads();
-    if (ok && rank == 0) wcnt[wid][e] = __popcll(same);
-    __syncthreads();
-    if (ok) {
-      int before = 0;
-      for (int ww = 0; ww < wid; ++ww) before += wcnt[ww][e];
-      sorted_ids[start[e] + run[e] + before + rank] = int32_t(i);
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const bool ok = ev[u] >= 0;
+      const int e = ok ? ev[u] : 0;
+      const unsigned long long same = group(ok, e);
+      if (ok) sorted_ids[wbase[wid][e] + __popcll(same & lt)] = int32_t(r0 + 64 * u + lane);
+      if (ok && (same & lt) == 0) wbase[wid][e] += __popcll(same);
     }
-    __syncthreads();
-    if (tid < E) {
-      int tot = 0;
-      for (int ww = 0; ww < 16; ++ww) tot += wcnt[ww][tid];
-      run[tid] += tot;
-    }
-    __syncthreads();
   }
 }
 
