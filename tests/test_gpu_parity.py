@@ -85,6 +85,42 @@ def test_cache_ops_exact(dev, D):
     assert torch.equal(got[[0, 3]], cache[[3, 2]]) and not got[[1, 2]].any()
 
 
+def test_cache_ops_many_sequences(dev):
+    """Row lookups over more than 64 sequences (the ballot search takes the prefix array in 64-entry
+    chunks), with empty sequences (equal prefix entries): every map bit-exact against the oracle."""
+    ops = _ops()
+    g = _gen(11)
+    rng = np.random.default_rng(11)
+    B, D = 150, 256
+    lens_k = rng.integers(0, 9, size=B)
+    lens_k[[0, 70, 149]] = 0
+    lens_q = np.minimum(lens_k, rng.integers(0, 5, size=B))
+    seq_ids = rng.permutation(200)[:B]
+    starts = torch.full((200,), -1, dtype=torch.long)
+    pos = 1
+    for sid, L in zip(seq_ids, lens_k):
+        starts[int(sid)] = pos
+        pos += int(L) + 2
+    cache = _randn(g, pos + 3, D)
+    cu_k = torch.tensor(np.concatenate([[0], np.cumsum(lens_k)]), dtype=torch.int32)
+    cu_q = torch.tensor(np.concatenate([[0], np.cumsum(lens_q)]), dtype=torch.int32)
+    sids = torch.tensor(seq_ids, dtype=torch.long)
+    Tk, Tq = int(cu_k[-1]), int(cu_q[-1])
+    c_d, st_d, id_d, cuk_d, cuq_d = (t.to(dev) for t in (cache, starts, sids, cu_k, cu_q))
+    assert torch.equal(ops.get_seqs_cuda(c_d, st_d, cuk_d, id_d, Tk).cpu(), ref.get_seqs(cache, starts, cu_k, sids, Tk))
+    assert torch.equal(ops.get_block_cuda(c_d, st_d, cuk_d, cuq_d, id_d, Tq).cpu(),
+                       ref.get_block(cache, starts, cu_k, cu_q, sids, Tq))
+    xin = _randn(g, Tk, D)
+    c2 = c_d.clone()
+    ops.reset_full_cuda(c2, xin.to(dev), st_d, cuk_d, id_d, Tk)
+    assert torch.equal(c2.cpu(), ref.reset_full(cache, xin, starts, cu_k, sids))
+    rows = torch.from_numpy(np.sort(rng.choice(Tk, size=min(Tk, 97), replace=False))).long()
+    nv = _randn(g, rows.numel(), D)
+    c4 = c_d.clone()
+    ops.scatter_update_cuda(c4, nv.to(dev), rows.to(dev), cuk_d, st_d, id_d)
+    assert torch.equal(c4.cpu(), ref.scatter_update(cache, nv, rows, cu_k, starts, sids))
+
+
 # ---------------------------------------------------------------------------------------
 # saliency, tau test, compaction
 # ---------------------------------------------------------------------------------------
