@@ -161,13 +161,25 @@ def build_workload(cfg, layers, device, seed=0):
             st["attn"].context_cache.cache.copy_(st["c_saved"])
             st["attn"].v_cache.cache.copy_(st["v_saved"])
 
-    def step(events=None, n_sal=None, refresh=False):
+    kv_proj = {}
+
+    def step(events=None, n_sal=None, refresh=False, with_kv_proj=False):
         ctx = set_sparse_context(refresh)
         T = Tk if refresh else Tq
+        if with_kv_proj and not kv_proj:
+            # salient-row K/V projection operands: layer inputs of every K row and 4 weight copies
+            # cycled over the layers (so the weights come from HBM, as across 32 layers)
+            kv_proj["x"] = randn(Tk, hid)
+            kv_proj["w"] = [randn(2 * Hkv * D, hid, std=0.02) for _ in range(4)]
         for li, st in enumerate(state):
             idx = ctx.idx_salient_row
             if n_sal is not None:
                 n_sal.append(idx.numel())
+            if with_kv_proj:
+                # the projection GEMM of the salient rows (dyllm_linear, llada.py:108); its output
+                # is not consumed: the epilogue below keeps the stand-in rows, so the salient fraction
+                # of the workload stays as built
+                ops.linear(kv_proj["x"], kv_proj["w"][li % 4], rows_idx=ctx.idx_salient_row_i32)
             # the projection's [k | v] rows of the salient set (stand-in: a gather), then the fused
             # epilogue: RoPE + K-cache scatter of k, the compact v of the step
             kidx = ctx.idx_salient_row if refresh else ctx.idx_salient_row_k
@@ -567,7 +579,7 @@ def _read_attn_timer():
     return ms.value, n.value
 
 
-def _run_cadence(wl, steps, period, layers):
+def _run_cadence(wl, steps, period, layers, with_kv_proj=False):
     """Timed denoise steps of a built workload: step i is a refresh step when i % period ==
     period - 1, a Q-pruned step otherwise. Per step kind: wall times, salient rows per layer, the
     fused attention launches (library HIP events) and the gate_up / down launches (HIP events on
@@ -589,7 +601,7 @@ def _run_cadence(wl, steps, period, layers):
                for li in range(0, layers, EVENT_STRIDE)}
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        wl["step"](events=evs, n_sal=k["n_sal"], refresh=refresh)
+        wl["step"](events=evs, n_sal=k["n_sal"], refresh=refresh, with_kv_proj=with_kv_proj)
         torch.cuda.synchronize()
         k["ms"].append((time.perf_counter() - t0) * 1e3)
         k["gate"] += [e["gate_up"][0].elapsed_time(e["gate_up"][1]) for e in evs.values()]
@@ -707,6 +719,13 @@ def main():
     kinds = _run_cadence(wl, args.steps, 4, layers)
     total_ms = sum(kinds[False]["ms"]) + sum(kinds[True]["ms"])
     ms_per_step = total_ms / args.steps
+    # the same cadence with the salient-row K/V projection GEMM added per layer (the model's step
+    # includes it; `value` covers the path of the saliency layer, attention through FFN)
+    wl["restore"]()
+    wl["step"](refresh=False, with_kv_proj=True)
+    torch.cuda.synchronize()
+    kinds_kv = _run_cadence(wl, args.steps, 4, layers, with_kv_proj=True)
+    ms_kv = (sum(kinds_kv[False]["ms"]) + sum(kinds_kv[True]["ms"])) / args.steps
     Tq, Tk = wl["Tq"], wl["Tk"]
     value = Tq / (ms_per_step / 1e3)     # B x Lq denoised tokens per step, at the config-1 cadence
 
@@ -759,6 +778,13 @@ def main():
                                  "roofline_attention": rf("attention_step_kernel<4> (fused refresh step, every row "
                                                           "queried)", r["attn_flops"], r["attn_ms"])}
     extra["q_pruned_step"] = {"ms_per_step": round(q["ms"], 4), "tokens_per_s": round(Tq / (q["ms"] / 1e3), 1)}
+    extra["step_with_kv_projection"] = {
+        "ms_per_step": round(ms_kv, 4), "tokens_per_s": round(Tq / (ms_kv / 1e3), 1),
+        "note": "the same cadence with the salient-row K/V projection GEMM (dyllm_linear) added per layer, "
+                "as the model's sparse step runs it; its output is not consumed (the K/V epilogue keeps "
+                "the stand-in rows, so the salient fraction stays as built)"}
+    print(f"[bench] with the K/V projection: {ms_kv:.3f} ms/step, {Tq / (ms_kv / 1e3):.0f} tokens/s",
+          file=sys.stderr, flush=True)
     del wl
     torch.cuda.empty_cache()
     extra["roofline_down"] = rf_down
