@@ -945,7 +945,7 @@ int dyllm_moe_gate(const void* x, const int32_t* rows_idx, int64_t tokens, int h
 int dyllm_moe_align_block_size(const int32_t* topk_ids, int64_t slots, int num_experts, int block,
                                int32_t* sorted_token_ids, int64_t capacity, int32_t* tile_expert,
                                int32_t* num_post_pad, void* stream) {
-  DYLLM_NONNULL(topk_ids);
+  if (slots > 0) DYLLM_NONNULL(topk_ids);   // no slots: only the sentinels and the count are written
   DYLLM_NONNULL(sorted_token_ids);
   DYLLM_NONNULL(tile_expert);
   DYLLM_NONNULL(num_post_pad);

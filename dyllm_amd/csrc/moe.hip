@@ -86,33 +86,69 @@ int launch_moe_router(const uint16_t* x, const int32_t* rows, const uint16_t* wr
   return check_launch("moe_router_kernel");
 }
 
-// ---- align: one workgroup of 1024 threads -----------------------------------------------
-// The slots are cut into 16 contiguous ranges, one per wavefront. Pass 1: each wavefront walks
-// its range 64 slots at a time; six ballots group the lanes that share an expert, and the
-// first lane of each group adds the group's size to the wavefront's per-expert count in LDS
-// (distinct experts per leader lane: no conflicts). After one barrier the per-expert totals give
-// the padded bucket starts and every (wavefront, expert) pair its base in the bucket. Pass 2
-// walks the ranges again and writes each slot at base + its rank among the lanes that share its
-// expert, then the leaders advance their bases. Slots keep ascending order inside a bucket
-// (ranges, rounds and lanes in order); only two workgroup barriers separate the passes, and the
-// ids of 8 rounds are loaded at once.
-__global__ __launch_bounds__(1024) void moe_align_kernel(const int32_t* __restrict__ ids, int64_t S, int E, int bm,
-                                                         int32_t* __restrict__ sorted_ids, int64_t cap,
-                                                         int32_t* __restrict__ tile_expert,
-                                                         int32_t* __restrict__ num_post_pad) {
-  constexpr int NWV = 16;
+// ---- align: G workgroups of 1024 threads, no communication between them ----------------
+// Workgroup g owns the contiguous slot chunk [g0, g1). Every workgroup first builds, with LDS
+// atomics over a coalesced read of all slot ids (L2-resident, a few hundred KB at most), the
+// per-expert totals and the per-expert counts of the slots before its chunk; all workgroups
+// derive the same padded bucket starts from the same integers, so the chunks' bases follow
+// without any inter-workgroup exchange. Inside a chunk: 16 contiguous per-wavefront ranges;
+// pass 1 counts per (wavefront, expert) with six ballots that group the lanes sharing an expert
+// (the group's first lane adds the group size: distinct experts per leader, no conflicts);
+// pass 2 writes each slot at its base + its rank among the lanes of its group. Slots keep
+// ascending order inside a bucket (chunks, ranges, rounds and lanes in order). The bucket
+// padding and tile experts of expert e are written by workgroup e % G, the tail past the last
+// bucket striped over all workgroups.
+constexpr int kAlignThreads = 1024;
+constexpr int kAlignMaxGroups = 64;
+constexpr int kAlignMinChunk = 512;
+
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int32_t* __restrict__ ids, int64_t S, int E,
+                                                                  int bm, int32_t* __restrict__ sorted_ids,
+                                                                  int64_t cap, int32_t* __restrict__ tile_expert,
+                                                                  int32_t* __restrict__ num_post_pad) {
+  constexpr int NWV = kAlignThreads / 64;
   __shared__ int wcnt[NWV][64];
   __shared__ int wbase[NWV][64];
   __shared__ int start[65];
-  __shared__ int cnt[64];
+  __shared__ int tot[64];
+  __shared__ int pre[64];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  for (int x = tid; x < NWV * 64; x += 1024) (&wcnt[0][0])[x] = 0;
+  const int G = gridDim.x, g = blockIdx.x;
+  for (int x = tid; x < NWV * 64; x += kAlignThreads) (&wcnt[0][0])[x] = 0;
+  if (tid < 64) {
+    tot[tid] = 0;
+    pre[tid] = 0;
+  }
   __syncthreads();
   // expert ids are clamped to [0, E): an out-of-range id from a caller can never index past the
   // 64-entry LDS tables (its slot is then routed to the nearest valid expert)
   auto expert_of = [&](int64_t i) { return min(max(int(ids[i]), 0), E - 1); };
-  const int64_t per = (S + NWV - 1) / NWV;
-  const int64_t c0 = int64_t(wid) * per, c1 = min(S, c0 + per);
+  const int64_t per_g = (S + G - 1) / G;
+  const int64_t g0 = min(S, int64_t(g) * per_g), g1 = min(S, g0 + per_g);
+  // totals and the counts before this chunk; the ids of kBatch rounds are loaded together
+  constexpr int kBatch = 8;
+  // (each workgroup starts its scan at its own chunk: concurrent workgroups read different lines
+  // instead of all requesting the same ones from one L2 channel)
+  for (int64_t r0 = 0; r0 < S; r0 += int64_t(kAlignThreads) * kBatch) {
+    int ev[kBatch];
+    bool before[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t i = r0 + int64_t(kAlignThreads) * u + tid;
+      int64_t j = i + g0;
+      if (j >= S) j -= S;
+      ev[u] = i < S ? expert_of(j) : -1;
+      before[u] = j < g0;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (ev[u] < 0) continue;
+      atomicAdd(&tot[ev[u]], 1);
+      if (before[u]) atomicAdd(&pre[ev[u]], 1);
+    }
+  }
+  const int64_t per = (g1 - g0 + NWV - 1) / NWV;
+  const int64_t c0 = min(g1, g0 + int64_t(wid) * per), c1 = min(g1, c0 + per);
   // lanes of this round that share the expert e (ok lanes only)
   auto group = [&](bool ok, int e) -> unsigned long long {
     unsigned long long same = __ballot(ok);
@@ -124,8 +160,6 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int32_t* __restri
     return same;
   };
   const unsigned long long lt = (1ull << lane) - 1;
-  // the ids of kBatch rounds are loaded together (one memory latency per kBatch rounds)
-  constexpr int kBatch = 8;
   for (int64_t r0 = c0; r0 < c1; r0 += 64 * kBatch) {
     int ev[kBatch];
 #pragma unroll
@@ -142,41 +176,40 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int32_t* __restri
     }
   }
   __syncthreads();
-  if (tid < 64) {
-    int c = 0;
-    if (tid < E)
-      for (int w = 0; w < NWV; ++w) c += wcnt[w][tid];
-    cnt[tid] = c;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int e = 0; e < E; ++e) {
-      start[e] = acc;
-      acc += (cnt[e] + bm - 1) / bm * bm;
+  if (tid < 64) {   // padded bucket starts: an exclusive scan over the experts in wavefront 0
+    const int pad = tid < E ? (tot[tid] + bm - 1) / bm * bm : 0;
+    int inc = pad;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(inc, o, 64);
+      if (tid >= o) inc += v;
     }
-    start[E] = acc;
-    num_post_pad[0] = acc;
+    if (tid < E) start[tid] = inc - pad;
+    if (tid == 63) {
+      start[E] = inc;
+      if (g == 0) num_post_pad[0] = inc;
+    }
   }
   __syncthreads();
   if (tid < E) {
-    int bse = start[tid];
+    int bse = start[tid] + pre[tid];
     for (int w = 0; w < NWV; ++w) {
       wbase[w][tid] = bse;
       bse += wcnt[w][tid];
     }
   }
   const int total = start[E];
-  // sentinels in the padding of every bucket and past the last one (disjoint from the slots
-  // written below); the expert of every tile
-  for (int e = 0; e < E; ++e) {
-    const int p0 = start[e] + cnt[e], p1 = start[e + 1];
-    for (int x = p0 + tid; x < p1; x += 1024) sorted_ids[x] = int32_t(S);
+  // sentinels in the padding of this workgroup's experts' buckets (disjoint from every slot
+  // written below) and their tiles' expert; the tail past the last bucket
+  for (int e = g; e < E; e += G) {
+    const int p0 = start[e] + tot[e], p1 = start[e + 1];
+    for (int x = p0 + tid; x < p1; x += kAlignThreads) sorted_ids[x] = int32_t(S);
     const int nt = (p1 - start[e]) / bm;
-    for (int t = tid; t < nt; t += 1024) tile_expert[start[e] / bm + t] = e;
+    for (int t = tid; t < nt; t += kAlignThreads) tile_expert[start[e] / bm + t] = e;
   }
-  for (int64_t x = total + tid; x < cap; x += 1024) sorted_ids[x] = int32_t(S);
-  for (int64_t t = total / bm + tid; t < cap / bm; t += 1024) tile_expert[t] = 0;
+  const int64_t stride = int64_t(G) * kAlignThreads;
+  for (int64_t x = total + int64_t(g) * kAlignThreads + tid; x < cap; x += stride) sorted_ids[x] = int32_t(S);
+  for (int64_t t = total / bm + int64_t(g) * kAlignThreads + tid; t < cap / bm; t += stride) tile_expert[t] = 0;
   __syncthreads();
   for (int64_t r0 = c0; r0 < c1; r0 += 64 * kBatch) {
     int ev[kBatch];
@@ -199,8 +232,11 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(const int32_t* __restri
 int launch_moe_align(const int32_t* ids, int64_t S, int E, int bm, int32_t* sorted_ids, int64_t cap,
                      int32_t* tile_expert, int32_t* num_post_pad, hipStream_t s) {
   DYLLM_REQUIRE(E >= 1 && E <= 64, "align supports 1..64 experts");
+  DYLLM_REQUIRE(S >= 0 && S < (int64_t(1) << 31), "slot count out of range");
   DYLLM_REQUIRE(bm > 0 && cap % bm == 0 && cap >= S + int64_t(E) * (bm - 1), "sorted-id capacity too small");
-  moe_align_kernel<<<1, 1024, 0, s>>>(ids, S, E, bm, sorted_ids, cap, tile_expert, num_post_pad);
+  DYLLM_REQUIRE(cap < (int64_t(1) << 31), "sorted-id capacity out of range");
+  const int G = int(std::min<int64_t>(kAlignMaxGroups, std::max<int64_t>(1, cdiv(S, kAlignMinChunk))));
+  moe_align_kernel<<<G, kAlignThreads, 0, s>>>(ids, S, E, bm, sorted_ids, cap, tile_expert, num_post_pad);
   return check_launch("moe_align_kernel");
 }
 

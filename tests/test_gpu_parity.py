@@ -372,6 +372,28 @@ def test_moe_align_clamps_out_of_range_ids(dev):
     assert np.array_equal(tile_e.cpu().numpy()[:n_ref // 4], e_ref)
 
 
+@pytest.mark.parametrize("S,E,bm,skew", [(0, 8, 4, 0.0), (1, 64, 128, 0.0), (511, 64, 16, 0.0), (513, 7, 32, 3.0),
+                                          (5000, 64, 128, 2.0), (29488, 64, 128, 0.5), (70001, 13, 64, 1.0)])
+def test_moe_align_workgroups(dev, S, E, bm, skew):
+    """Alignment over 1 to 64 workgroups (chunks of >= 512 slots; uneven last chunks, experts with
+    no slots, skewed loads): the buckets equal the oracle's, the padding and the tail past the last
+    bucket hold the sentinel, and every tile past the last bucket is assigned expert 0."""
+    ops = _ops()
+    g = _gen(40 + S)
+    logits = torch.randn(E, generator=g) * skew
+    p = torch.softmax(logits, 0)
+    ids = torch.multinomial(p, S, replacement=True, generator=g).to(torch.int32) if S else torch.zeros(0, dtype=torch.int32)
+    ids2 = ids.reshape(-1, 1)
+    sorted_ids, tile_e, npp = ops.moe_align_block_size(ids2.to(dev), bm, E)
+    s_ref, e_ref, n_ref = ref.moe_align_block_size(ids2.numpy(), bm, E)
+    got_s, got_e = sorted_ids.cpu().numpy(), tile_e.cpu().numpy()
+    assert int(npp.item()) == n_ref
+    assert np.array_equal(got_s[:n_ref], s_ref)
+    assert np.array_equal(got_e[:n_ref // bm], e_ref)
+    assert (got_s[n_ref:] == S).all()
+    assert (got_e[n_ref // bm:] == 0).all()
+
+
 def test_attention_kernel_info(dev):
     """attention.cpp:205-208 mirror: [regs, local_bytes, static_smem, dynamic_smem, tb_size,
     max_active_blocks_per_sm, block_q, block_k, d_split, ok]."""
