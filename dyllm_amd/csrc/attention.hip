@@ -86,6 +86,10 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
   const int ql = lane & 31, half = lane >> 5;
   const int row = row_beg + tile * BQ + w * 32 + ql;  // compact row of this lane
   const bool row_ok = row < row_end;
+  // Waves whose 32 rows all lie past the sequence's last row (the tail tile of a sequence) take
+  // part in the tile's staging and barriers only: their scores and accumulators would be discarded
+  // by the row-guarded epilogue, so skipping them frees the SIMD for the co-resident workgroup.
+  const bool wave_live = __builtin_amdgcn_readfirstlane(int(row_beg + tile * BQ + w * 32 < row_end)) != 0;
   int64_t qrow = row;
   if constexpr (MODE == AttnMode::RowSparse) qrow = row_ok ? a.q_rows[row] : 0;
 
@@ -354,6 +358,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
         __syncthreads();
         if (pb + 1 < npb) fetch2(pb + 1);
         load_meta2(pb + 2);
+        if (wave_live) {
         f32x16_t sa[2];
         qk(sa, k_lds);
 #pragma unroll
@@ -397,6 +402,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
               o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, p.v, o_acc[dt], 0, 0, 0);
             }
           }
+        }
         __syncthreads();
       }
     };
@@ -411,6 +417,8 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       // sequential sum) and the block maxima are turned into the exact running maxima pass 2 needs.
       // K: blocks 2j and 2j+1 are staged together (K tile and the idle V^T tile), one barrier each.
       const int pg = w ^ 1, par = w & 1;
+      // the pair scores both of its groups: it is idle only when both lie past the last row
+      const bool pair_live = __builtin_amdgcn_readfirstlane(int(row_beg + tile * BQ + (w & ~1) * 32 < row_end)) != 0;
       bf16x8_t qf2[8];   // the partner group's Q fragments
       {
         const int prow = row_beg + tile * BQ + pg * 32 + ql;
@@ -451,7 +459,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
         if (2 * j + 2 < nkb) fetch_k(2 * j + 2);
         if (2 * j + 3 < nkb) fetch_k1(2 * j + 3);
         const int kb = 2 * j + par;
-        if (kb < nkb) {
+        if (kb < nkb && pair_live) {
           const uint16_t* kt = par ? vt_lds : k_lds;
           f32x16_t sa[2][2];   // [group][32-key half]
 #pragma unroll
@@ -537,6 +545,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
             stage_k(k_lds);
             __syncthreads();
             if (kbl + 1 < nkc) fetch_k(kb0 + kbl + 1);
+            if (wave_live) {
             f32x16_t sa[2];
             qk(sa, k_lds);
             const int key0 = (kb0 + kbl) * kBK;
@@ -570,6 +579,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
               }
             pl1 = pl1 * rescale + psum;
             if (half == 0) m_tab[kbl * 32] = bm;   // the block's own maximum
+            }
             __syncthreads();
           }
           // the chunk's group count, read before the barrier below (wave 0 rewrites it for the next
@@ -610,6 +620,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     __syncthreads();
     if (kb + 1 < nkb) fetch(kb + 1);
     load_meta(kb + 2);
+    if (wave_live) {
 
     // ---- S^T = K Q^T for two 32-key tiles --------------------------------------------
     f32x16_t s_acc[2];
@@ -688,6 +699,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
             o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, pf[t][u], o_acc[dt], 0, 0, 0);
           }
         }
+    }
     }
     __syncthreads();
   }
