@@ -817,15 +817,8 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
   }
 }
 
-// The 2-wavefront column-sparse kernel (small grids only) holds the two-pass state and the larger
-// per-thread staging of its 128-thread workgroup in 1 wavefront per SIMD (its accumulators go to
-// AGPRs); it measured within ±5 % of the single-pass variant, which spills at 2 per SIMD.
 template <AttnMode MODE, int NW>
-constexpr int kAttnWaves = (MODE == AttnMode::ColSparse && NW == 2) ? 1 : 2;
-
-template <AttnMode MODE, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(kAttnWaves<MODE, NW>, 2))) void
-attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBK * kKStride];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
   if constexpr (MODE == AttnMode::ColSparse) {
@@ -1072,21 +1065,19 @@ int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hip
   DYLLM_REQUIRE(attn_aligned(a), "Q, K, V and context buffers must be 16-byte aligned (output 8-byte)");
   DYLLM_REQUIRE(max_rows_per_seq >= 0, "bad row bound");
   if (max_rows_per_seq == 0) return 0;
-  DYLLM_REQUIRE(cdiv(max_rows_per_seq, 64) * a.H * a.B < (int64_t(1) << 31), "grid too large");
-  // 4-wave workgroups (128 rows) when the grid has enough of them to fill 256 CUs twice,
-  // otherwise 2-wave workgroups (64 rows) for twice the parallelism on few rows.
-  const bool wide = cdiv(max_rows_per_seq, 128) * a.H * a.B >= 512;
+  DYLLM_REQUIRE(cdiv(max_rows_per_seq, 128) * a.H * a.B < (int64_t(1) << 31), "grid too large");
+  // 4-wave workgroups (128 rows) at every grid size: 2-wave workgroups on small grids (twice the
+  // workgroups, each staging every K/V block for half the rows, and spilling at 256 VGPRs) measured
+  // slower in every case tried, from 16 to 384 rows per sequence
   switch (mode) {
     case AttnMode::Dense:
-      wide ? launch_mode<AttnMode::Dense, 4>(a, max_rows_per_seq, s) : launch_mode<AttnMode::Dense, 2>(a, max_rows_per_seq, s);
+      launch_mode<AttnMode::Dense, 4>(a, max_rows_per_seq, s);
       break;
     case AttnMode::RowSparse:
-      wide ? launch_mode<AttnMode::RowSparse, 4>(a, max_rows_per_seq, s)
-           : launch_mode<AttnMode::RowSparse, 2>(a, max_rows_per_seq, s);
+      launch_mode<AttnMode::RowSparse, 4>(a, max_rows_per_seq, s);
       break;
     case AttnMode::ColSparse:
-      wide ? launch_mode<AttnMode::ColSparse, 4>(a, max_rows_per_seq, s)
-           : launch_mode<AttnMode::ColSparse, 2>(a, max_rows_per_seq, s);
+      launch_mode<AttnMode::ColSparse, 4>(a, max_rows_per_seq, s);
       break;
   }
   return check_launch("attention_kernel");
