@@ -448,8 +448,11 @@ static int launch_gemm_cfg(const GemmArgs& g0, int64_t m_tiles, int ksplit, hipS
   const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (BN / 2)) : int(cdiv(g.N, BN));
   const int64_t tiles = m_tiles * n_tiles * ksplit;
   if (tiles == 0) return 0;
+  // a multiple of 8 workgroups (one range per XCD), rounded up: with fewer tiles than CUs every
+  // workgroup then takes at most one tile (rounding down would push the last few tiles into a
+  // second round), the workgroups past a range's end exit at once
   int64_t nwg = tiles < num_cus() ? tiles : num_cus();
-  if (nwg >= 8) nwg &= ~int64_t(7);
+  if (nwg >= 8) nwg = std::min<int64_t>(cdiv(nwg, 8) * 8, num_cus() & ~7);
   const size_t lds = lds_bytes(BM, BN);
   static bool attr_set = false;
   if (!attr_set) {
