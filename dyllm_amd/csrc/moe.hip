@@ -247,15 +247,25 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const uint16_t* __rest
   const int lane = threadIdx.x & 63;
   if (t >= T) return;
   const int64_t d = dst_rows ? dst_rows[t] : t;
+  // the slots' pieces are loaded kBatch at a time before they are summed (in slot order): one
+  // memory round trip per batch instead of one per slot
+  constexpr int kBatch = 8;
   for (int c = lane; c < Hd / 8; c += 64) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int k = 0; k < top_k; ++k) {
-      const uint4 v = reinterpret_cast<const uint4*>(y + (t * top_k + k) * Hd)[c];
-      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    for (int k0 = 0; k0 < top_k; k0 += kBatch) {
+      uint4 v[kBatch];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[2 * j] += __uint_as_float(vv[j] << 16);
-        acc[2 * j + 1] += __uint_as_float(vv[j] & 0xffff0000u);
+      for (int u = 0; u < kBatch; ++u)
+        v[u] = (k0 + u < top_k) ? reinterpret_cast<const uint4*>(y + (t * top_k + k0 + u) * Hd)[c] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (k0 + u >= top_k) break;
+        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[2 * j] += __uint_as_float(vv[j] << 16);
+          acc[2 * j + 1] += __uint_as_float(vv[j] & 0xffff0000u);
+        }
       }
     }
     uint4 o;
