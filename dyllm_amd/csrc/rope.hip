@@ -45,8 +45,6 @@ __global__ __launch_bounds__(256) void kv_rope_scatter_kernel(KvRopeArgs a) {
   // row-uniform chain
   // positions are clamped to the table, as the reference does before its table lookup
   // (rotary_embedding.py:45-48); the engine refuses sequences longer than the table
-  // positions are clamped to the table, as the reference does before its table lookup
-  // (rotary_embedding.py:45-48); the engine refuses sequences longer than the table
   int64_t pos = a.positions[a.pos_idx ? int64_t(a.pos_idx[j]) : j];
   pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
   int64_t dest = j;   // in-place mode (no cache mapping): row j of the output
