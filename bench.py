@@ -553,6 +553,14 @@ def time_moe(reps=6, copies=4):
         e1.record()
     torch.cuda.synchronize()
     us = sum(e0.elapsed_time(e1) for e0, e1 in evs) / reps * 1e3
+    # the router (moe_gate: fp32 logits, softmax, top-k) of the same rows, timed on its own
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record()
+    for _ in range(reps):
+        ops.moe_gate(x, wr, top_k)
+    r1.record()
+    torch.cuda.synchronize()
+    router_us = r0.elapsed_time(r1) / reps * 1e3
     flops = 6.0 * n * top_k * hid * inter
     tf = flops / (us * 1e-6) / 1e12
     load = torch.bincount(ids.reshape(-1).long(), minlength=E)
@@ -560,7 +568,8 @@ def time_moe(reps=6, copies=4):
             "bound": "mfma", "rows": n, "slots": n * top_k, "max_expert_load": int(load.max()),
             "mean_expert_load": round(float(load.float().mean()), 1), "avg_launch_us": round(us, 2),
             "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop_per_launch": flops, "traffic": None}
+            "frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop_per_launch": flops, "traffic": None,
+            "router_us": round(router_us, 2)}
 
 
 def _attn_flops(T, L, HD, n, n_seq_sal):

@@ -344,7 +344,8 @@ int dyllm_rms_norm_cache_rows(const void* cache, int64_t ld_cache, const int64_t
 /* ---- MoE ------------------------------------------------------------------------------- */
 
 /* Router: topk_weights (bf16) / topk_ids (int32) [tokens, top_k] from fp32 softmax of
- * x[rows_idx[t] or t] . router_w^T; router_w: [num_experts, hidden] bf16; num_experts <= 64. */
+ * x[rows_idx[t] or t] . router_w^T; router_w: [num_experts, hidden] bf16; num_experts <= 64,
+ * hidden a multiple of 16. */
 int dyllm_moe_gate(const void* x, const int32_t* rows_idx, int64_t tokens, int hidden, const void* router_w,
                    int num_experts, int top_k, int renormalize, void* topk_weights, int32_t* topk_ids, void* stream);
 
