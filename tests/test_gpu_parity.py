@@ -359,6 +359,27 @@ def test_moe_gate_align_experts(dev):
     assert_bf16_close(out, want.to(BF), what="fused experts")
 
 
+@pytest.mark.parametrize("T,hidden,E,top_k,renorm", [(1, 48, 8, 2, False), (33, 48, 8, 2, True), (70, 272, 13, 4, False),
+                                                     (257, 2048, 64, 8, True)])
+def test_moe_gate_shapes(dev, T, hidden, E, top_k, renorm):
+    """Router over token counts that leave a partial 32-token tile, hidden sizes whose 16-wide
+    steps do not divide evenly over the 8 slices of the hidden dimension (48: some slices empty),
+    expert counts below 64 and renormalised weights: the expert sets equal the oracle's wherever
+    its k-th and (k+1)-th probabilities are separated, and the weights agree within one bf16 ulp."""
+    ops = _ops()
+    g = _gen(60 + T)
+    x = _randn(g, T, hidden)
+    wr = _randn(g, E, hidden, scale=hidden ** -0.5)
+    w, ids = ops.moe_gate(x.to(dev), wr.to(dev), top_k, renormalize=renorm)
+    w_ref, ids_ref = ref.moe_gate(x, wr, top_k, renormalize=renorm)
+    probs = torch.softmax(x.float() @ wr.float().t(), dim=-1)
+    top = probs.topk(min(top_k + 1, E), dim=-1).values
+    clear = (top[:, top_k - 1] - top[:, top_k]) > 1e-5 if top_k < E else torch.ones(T, dtype=torch.bool)
+    assert clear.float().mean() > 0.9
+    assert torch.equal(ids.cpu()[clear], ids_ref[clear])
+    assert_routing_weights(w.cpu()[clear], w_ref[clear])
+
+
 def test_moe_align_clamps_out_of_range_ids(dev):
     """Expert ids outside [0, E) are clamped on the device (never index past the LDS tables):
     the result equals the alignment of the clamped ids."""
