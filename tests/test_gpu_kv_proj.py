@@ -124,8 +124,10 @@ def test_kv_rope_scatter_device_count(dev):
     assert torch.equal(v.cpu()[:17].view(17, kvs), kv[:17, kvs:])
 
 
+# (200, 3584, 512): 14 output-column tiles, a tile count below the CU count and not a multiple of 8
 @pytest.mark.parametrize("rows,n_out,k_in,bias", [(920, 8192, 4096, False), (37, 1024, 3584, True),
-                                                  (300, 4096, 12288, False), (1, 264, 128, True)])
+                                                  (300, 4096, 12288, False), (1, 264, 128, True),
+                                                  (200, 3584, 512, True)])
 def test_linear_gathered_matches_oracle(dev, rows, n_out, k_in, bias):
     ops = _ops()
     print(f"[linear] rows={rows} n={n_out} k={k_in} bias={bias}", flush=True)
