@@ -204,7 +204,7 @@ def test_flash_attn_dense_and_rowsparse(dev, H, Hkv):
     rng = np.random.default_rng(H)
     rows, cu_s = [], [0]
     for b in range(len(lens)):
-        sel = np.sort(rng.choice(np.arange(cu_q[b], cu_q[b + 1]), size=max(1, lens[b][0] // 3), replace=False))
+        sel = np.sort(rng.choice(np.arange(int(cu_q[b]), int(cu_q[b + 1])), size=max(1, lens[b][0] // 3), replace=False))
         rows += sel.tolist()
         cu_s.append(len(rows))
     rows_t = torch.tensor(rows, dtype=torch.int32)
