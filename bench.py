@@ -692,6 +692,9 @@ def main():
                     help="run only the gate_up GEMM + a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--profile-attention", action="store_true",
                     help="run only the standalone row-sparse and column-sparse attention tiles (for rocprofv3 --pmc)")
+    ap.add_argument("--perturb", type=float, default=None,
+                    help="config 1's perturbed fraction of the response rows (default 0.15); the PMC traffic "
+                         "figures apply to the default only")
     ap.add_argument("--profile-hbm", action="store_true",
                     help="run only the standalone HBM-bound kernels at the config-1 shape and print their GB/s")
     args = ap.parse_args()
@@ -706,6 +709,12 @@ def main():
     from dyllm_amd import _lib
 
     cfg = dict(CONFIG1)
+    if args.perturb is not None:
+        if not 0.0 < args.perturb < 1.0:
+            print("bench.py: --perturb must lie in (0, 1)", file=sys.stderr)
+            sys.exit(2)
+        cfg["perturb"] = args.perturb
+    default_mix = cfg["perturb"] == CONFIG1["perturb"]
     if args.profile_gate_up:
         profile_gate_up(cfg)
         return
@@ -767,11 +776,13 @@ def main():
         return d
 
     rf_attn = rf("attention_step_kernel<4> (fused Q-pruned step: row-sparse + column-sparse tiles)",
-                 q["attn_flops"], q["attn_ms"], ATTN_TRAFFIC_BYTES, 345.0e6,
+                 q["attn_flops"], q["attn_ms"], ATTN_TRAFFIC_BYTES if default_mix else None,
+                 345.0e6 if default_mix else None,
                  "bound by its VALU plus MFMA issue (softmax over all query-key pairs); frac counts algorithmic "
                  "MFMA work only")
     rf_gate = rf(f"gemm_kernel<{gate_bm},4,SwiGLU> (gathered gate_up + SiLU*up, tile {gate_bm}x256)",
-                 q["gu_flops"], q["gate_ms"], GATE_UP_TRAFFIC_BYTES, 231.4e6)
+                 q["gu_flops"], q["gate_ms"], GATE_UP_TRAFFIC_BYTES if default_mix else None,
+                 231.4e6 if default_mix else None)
     rf_down = rf(f"gemm_kernel<{down_bm},4,Store> down + FFN-cache scatter (+ split-K reduction)",
                  q["dn_flops"], q["down_ms"])
     # the dominant kernel (longest mean launch) carries "roofline", the other one rides along
@@ -832,12 +843,13 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random-init N(0,0.02) weights, N(0,1) K/V/Q, 15% perturbed response rows)",
+        "data": f"synthetic (random-init N(0,0.02) weights, N(0,1) K/V/Q, {cfg['perturb'] * 100:g}% perturbed "
+                "response rows)",
         "config": {"workload": "config1: LLaDA-8B shape, sparse denoise steps over 32 layers at the config-1 "
                                "cadence (3 Q-pruned : 1 refresh)",
                    "layers": layers, "batch": cfg["batch"], "seq_len": L, "response_len": cfg["response"],
                    "hidden": hid, "heads": cfg["heads"], "ffn": inter, "tau": cfg["tau"],
-                   "q_pruned_steps": len(kinds[False]["ms"]), "refresh_steps": len(kinds[True]["ms"]),
+                   "perturbed": cfg["perturb"], "q_pruned_steps": len(kinds[False]["ms"]), "refresh_steps": len(kinds[True]["ms"]),
                    "avg_salient_rows_per_layer": round(avg_n, 1)},
         "roofline": rf_main,
         rf_other_key: rf_other,
