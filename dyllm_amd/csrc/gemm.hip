@@ -452,7 +452,7 @@ static int launch_gemm_cfg(const GemmArgs& g0, int64_t m_tiles, int ksplit, hipS
   // workgroup then takes at most one tile (rounding down would push the last few tiles into a
   // second round), the workgroups past a range's end exit at once
   int64_t nwg = tiles < num_cus() ? tiles : num_cus();
-  if (nwg >= 8) nwg = std::min<int64_t>(cdiv(nwg, 8) * 8, num_cus() & ~7);
+  if (nwg >= 8) nwg = std::min<int64_t>(cdiv(nwg, 8) * 8, std::max(8, num_cus() & ~7));
   const size_t lds = lds_bytes(BM, BN);
   static bool attr_set = false;
   if (!attr_set) {
