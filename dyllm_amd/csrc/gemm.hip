@@ -73,9 +73,35 @@ constexpr int waitcnt_lgkm0() { return 15 | (3 << 14) | (7 << 4); }
 __device__ __forceinline__ int swz_chunk(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 __device__ __forceinline__ int swz(int row, int chunk) { return row * kGemmBK + (swz_chunk(row, chunk) << 3); }
 
-// One BM x BN output tile (K slice kz of ksplit).
+// Source rows of the A blocks a lane loads for M tile mt: the gathered row of each tile row; rows
+// past M, padding and out-of-range ids read row 0, whose products are never stored.
+template <int BM, int WGN>
+__device__ __forceinline__ void gemm_tile_rows(const GemmArgs& g, int64_t M, int mt, int w, int lrow,
+                                               int64_t (&rows)[BM / (16 * WGN)]) {
+  constexpr int NW = 2 * WGN, CA = BM / (8 * NW);
+#pragma unroll
+  for (int i = 0; i < CA; ++i) {
+    const int64_t m = int64_t(mt) * BM + (w + NW * i) * 8 + lrow;
+    int64_t row = 0;
+    if (m < M) {
+      row = m;
+      if (g.a_ids) {
+        const int64_t id = g.a_ids[m];
+        row = (id >= 0 && id < g.id_limit) ? id / g.a_div : 0;
+      }
+    }
+    rows[i] = row;
+  }
+}
+
+// One BM x BN output tile (K slice kz of ksplit). The SwiGLU instantiation takes the tile's source
+// rows from its caller (rows) and looks up the next tile's (mt_next >= 0, into rows_next) during
+// its K loop, so a tile boundary does not wait on the row lookups; the Store instantiation looks
+// its rows up itself.
 template <int BM, int BN, int WGN, GemmEpi EPI>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, int nt, int kz) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, int nt, int kz,
+                                          const int64_t (&rows)[BM / (16 * WGN)], int mt_next,
+                                          int64_t (&rows_next)[BM / (16 * WGN)]) {
   extern __shared__ __attribute__((aligned(16))) uint16_t gsm[];
   constexpr int NW = 2 * WGN;                 // wavefronts: 2 along M x WGN along N
   constexpr int WM = BM / 2, WN = BN / WGN;   // wave tile (rows of A, rows of W)
@@ -110,18 +136,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   // address arithmetic. Offsets are 32-bit: every operand spans less than 4 GiB (checked on the
   // host where the extent is known).
   uint32_t a_vo[CA];
+  if constexpr (EPI == GemmEpi::SwiGLU) {
 #pragma unroll
-  for (int i = 0; i < CA; ++i) {
-    const int64_t m = m0 + (w + NW * i) * 8 + lrow;
-    int64_t row = 0;
-    if (m < M) {
-      row = m;
-      if (g.a_ids) {
-        const int64_t id = g.a_ids[m];
-        row = (id >= 0 && id < g.id_limit) ? id / g.a_div : 0;   // padding or out-of-range ids read row 0
-      }
-    }
-    a_vo[i] = uint32_t((row * g.lda + lane_chunk) * 2);
+    for (int i = 0; i < CA; ++i) a_vo[i] = uint32_t((rows[i] * g.lda + lane_chunk) * 2);
+  } else {
+    int64_t own[CA];
+    gemm_tile_rows<BM, WGN>(g, M, mt, w, lrow, own);
+#pragma unroll
+    for (int i = 0; i < CA; ++i) a_vo[i] = uint32_t((own[i] * g.lda + lane_chunk) * 2);
   }
   uint32_t w_vo[CW];
 #pragma unroll
@@ -236,6 +258,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   __builtin_amdgcn_s_barrier();
+  // the next tile's source rows: issued before every load of the K loop, so the loop's vmcnt
+  // waits complete them as well
+  if constexpr (EPI == GemmEpi::SwiGLU) {
+    if (mt_next >= 0) gemm_tile_rows<BM, WGN>(g, M, mt_next, w, lrow, rows_next);
+  }
   int wcur = 0;   // kt % 3
   // The last K substep of each slice is carried across the slice's barrier: its fragments are
   // read before the barrier and its MFMAs issued after it, while the first fragment reads of the
@@ -384,12 +411,24 @@ void gemm_kernel(GemmArgs g) {
     t_end = total;
     stride = P;
   }
+  constexpr int CA = BM / (16 * WGN);
+  int64_t rows[CA], rows_next[CA];
+  if constexpr (EPI == GemmEpi::SwiGLU) {
+    if (t < t_end)
+      gemm_tile_rows<BM, WGN>(g, M, int(t % mtr), __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6),
+                              (threadIdx.x & 63) >> 3, rows);
+  }
   for (; t < t_end; t += stride) {
     const int mt = int(t % mtr);
     const int64_t rest = t / mtr;
     const int nt = int(rest % n_tiles);
     const int kz = int(rest / n_tiles);
-    gemm_tile<BM, BN, WGN, EPI>(g, M, mt, nt, kz);
+    const int mt_next = (EPI == GemmEpi::SwiGLU && t + stride < t_end) ? int((t + stride) % mtr) : -1;
+    gemm_tile<BM, BN, WGN, EPI>(g, M, mt, nt, kz, rows, mt_next, rows_next);
+    if constexpr (EPI == GemmEpi::SwiGLU) {
+#pragma unroll
+      for (int i = 0; i < CA; ++i) rows[i] = rows_next[i];
+    }
   }
 }
 
