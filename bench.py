@@ -180,17 +180,16 @@ def build_workload(cfg, layers, device, seed=0):
                 # is not consumed: the epilogue below keeps the stand-in rows, so the salient fraction
                 # of the workload stays as built
                 ops.linear(kv_proj["x"], kv_proj["w"][li % 4], rows_idx=ctx.idx_salient_row_i32)
-            # the projection's [k | v] rows of the salient set (stand-in: a gather), then the fused
-            # epilogue: RoPE + K-cache scatter of k, the compact v of the step
-            kidx = ctx.idx_salient_row if refresh else ctx.idx_salient_row_k
-            kv = ops.gather_rows_2D(st["kv_all"], kidx)
-            v_sal = st["k_cache"].scatter_kv_rope(md.running_seqs_tensor, kidx, kv, Hkv, pos0,
-                                                  rope_cos, rope_sin, ctx.idx_salient_row_i32)
-            k_full = st["k_cache"].get_seqs(md.running_seqs_tensor, md.running_seqs).view(-1, Hkv, D)
+            # the projection's [k | v] rows of the salient set (stand-in: rows of pre-generated
+            # [k | v] addressed by K-space index); the step's first launch applies their epilogue
+            # (RoPE + K-cache row of k) and takes v from them
+            kidx32 = ctx.idx_salient_row_i32 if refresh else ctx.idx_salient_row_k_i32
+            v_sal = st["k_cache"].kv_rows(st["kv_all"], Hkv, pos0, rope_cos, rope_sin, ctx.idx_salient_row_i32,
+                                          kv_rows=kidx32)
             ev = events.get(li) if events is not None else None
             if ev is not None:   # time the fused attention kernel of this layer's step call
                 _lib.load().dyllm_attention_timer(1)
-            o = st["attn"](st["q_full"] if refresh else st["q"], k_full, v_sal)
+            o = st["attn"](st["q_full"] if refresh else st["q"], None, v_sal)
             if ev is not None:
                 _lib.load().dyllm_attention_timer(0)
             # the FFN rows stay in the FFN cache (the next layer's norm reads them in place)

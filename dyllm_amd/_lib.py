@@ -15,6 +15,26 @@ _P = c_void_p
 _I = c_int
 _L = c_int64
 
+
+
+class KvEpilogue(ctypes.Structure):
+    """dyllm_kv_epilogue (include/dyllm_hip.h), field for field."""
+    _fields_ = [
+        ("kv", c_void_p),
+        ("ld_kv", c_int64),
+        ("kv_rows", c_void_p),
+        ("positions", c_void_p),
+        ("pos_idx", c_void_p),
+        ("cos_table", c_void_p),
+        ("sin_table", c_void_p),
+        ("max_position", c_int),
+        ("k_norm_weight", c_void_p),
+        ("eps", c_float),
+        ("k_cache", c_void_p),
+        ("k_seq_starts", c_void_p),
+    ]
+
+
 # name -> argtypes (all return int status unless listed in _RET)
 SIGNATURES = {
     "dyllm_last_error": [],
@@ -35,6 +55,9 @@ SIGNATURES = {
     "dyllm_sparse_attention_step": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I, _L, _L,
                                     _I, _I, _P, _P, _P, _P, c_float, c_float, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                     _P, _P, _P, _P, c_size_t, _P],
+    "dyllm_sparse_attention_step_kv": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I,
+                                       _L, _L, _I, _I, _P, _P, _P, _P, c_float, c_float, _P, _P, _P, _P, _P, _P, _P,
+                                       _P, _P, _P, _P, _P, _P, c_size_t, _P],
     "dyllm_sparse_step_scratch_bytes": [],
     "dyllm_sparse_attention_step_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _I, _I,
                                             _L, _L, _I, _I, _P, _P, _P, _P, c_float, c_float, _P, _P, _P, _P, _P,

@@ -43,6 +43,10 @@ struct ColSparseLds {
   uint8_t* gblk;     // [4 * kMaxBlk2] key block of each group
   int* ngrp;         // number of groups
   float* xch;        // [NW][96] pass-1 partials exchanged between the waves of a pair (64 sums, 32 maxima)
+  // maps built from the compact salient lists (AttnArgs::sal_k):
+  unsigned long long* kbits;  // [kMaxBlk2] salient-key bits of the chunk's blocks
+  int* sblk;                  // [kMaxBlk2] dV row of group slot sl in block kb = cu_sal[b] + sblk[kb] + sl
+  uint32_t* rowflag;          // [NW] salient bits of the tile's query rows (32 per wavefront)
 };
 
 union Pack8 {
@@ -62,7 +66,7 @@ __device__ __forceinline__ int xcd_remap(int wg, int nwg) {
 
 // One (sequence, head, query tile) of NW*32 rows. wg is the tile index after the XCD remap
 // (all query tiles of one (sequence, kv-head) land on the same XCD and share its L2).
-template <AttnMode MODE, int NW, bool CHUNKED = false>
+template <AttnMode MODE, int NW, bool CHUNKED = false, bool LISTS = false>
 __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16_t* __restrict__ k_lds,
                                                uint16_t* __restrict__ vt_lds, const ColSparseLds& sp) {
   constexpr int NT = NW * 64;              // threads
@@ -80,7 +84,11 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
   const int row_beg = a.cu_rows[b], row_end = a.cu_rows[b + 1];
   if (row_beg + tile * BQ >= row_end) return;
   const int k_beg = a.cu_k[b], Lk = a.cu_k[b + 1] - k_beg;
-  const int64_t kv0 = a.kv_start ? a.kv_start[b] : int64_t(k_beg);
+  const int64_t sid = a.seq_ids ? a.seq_ids[b] : 0;
+  const int64_t kv0 = a.k_seq_starts ? a.k_seq_starts[sid] : (a.kv_start ? a.kv_start[b] : int64_t(k_beg));
+  // salient lists of this sequence (fused step: the column-sparse maps are built from them)
+  constexpr bool lists = MODE == AttnMode::ColSparse && LISTS;
+  const int s_beg = lists ? a.cu_sal[b] : 0, s_end = lists ? a.cu_sal[b + 1] : 0;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int ql = lane & 31, half = lane >> 5;
@@ -116,7 +124,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
   const float c2 = a.scale_log2;
 
   const uint16_t* Kb = a.K + kv0 * ldkv + kvh * kD;
-  const int64_t v0 = a.kslot ? 0 : (a.v_start ? a.v_start[b] : kv0);
+  const int64_t v0 = (a.kslot || lists) ? 0 : (a.v_seq_starts ? a.v_seq_starts[sid] : (a.v_start ? a.v_start[b] : kv0));
   const uint16_t* Vb = a.V + v0 * ldkv + kvh * kD;
   const int32_t* ks_b = a.kslot ? a.kslot + k_beg : nullptr;
   const int nkb = (Lk + kBK - 1) / kBK;
@@ -284,21 +292,53 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     // blocks relative to kb0)
     auto build_groups = [&](int kb0, int nkc) {
       if (w != 0) return;
+      int keys_before = 0;   // lists: salient keys of the sequence before this chunk
+      if constexpr (lists) {
+        // the chunk's salient-key bits (and, for the first chunk, the tile's salient query rows)
+        // from the sequence's list segment, in LDS; one wavefront, so no barrier is needed
+        if (lane < nkc) sp.kbits[lane] = 0;
+        if (kb0 == 0 && lane < NW) sp.rowflag[lane] = 0;
+        __threadfence_block();
+        const int key_lo = kb0 * kBK, key_hi = min(Lk, (kb0 + nkc) * kBK);
+        const int r0 = row_beg + tile * BQ;
+        for (int i0 = s_beg; i0 < s_end; i0 += 64) {
+          const int i = i0 + lane;
+          bool bef = false;
+          if (i < s_end) {
+            const int key = a.sal_k[i] - k_beg;
+            if (key >= key_lo && key < key_hi) atomicOr(&sp.kbits[(key - key_lo) >> 6], 1ull << (key & 63));
+            bef = key >= 0 && key < key_lo;
+            if (kb0 == 0) {
+              const int r = a.sal_q[i] - r0;
+              if (r >= 0 && r < BQ) atomicOr(&sp.rowflag[r >> 5], 1u << (r & 31));
+            }
+          }
+          keys_before += __popcll(__ballot(bef));
+        }
+        __threadfence_block();
+      }
       uint64_t word = 0;
       int grp = 0;
       if (lane < nkc) {
-        word = a.kmask[int64_t(b) * a.nblk + kb0 + lane];
+        word = lists ? sp.kbits[lane] : a.kmask[int64_t(b) * a.nblk + kb0 + lane];
         if (kb0 + lane == nkb - 1 && (Lk & (kBK - 1))) word &= (1ull << (Lk & (kBK - 1))) - 1;   // keys < Lk only
         grp = (__popcll(word) + 15) >> 4;
       }
       int inc = grp;
+      int pinc = __popcll(word);
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const int v = __shfl_up(inc, o, 64);
-        if (lane >= o) inc += v;
+        const int pv = __shfl_up(pinc, o, 64);
+        if (lane >= o) {
+          inc += v;
+          pinc += pv;
+        }
       }
       const int g0 = inc - grp;
       if (lane == 63) *sp.ngrp = inc;
+      // dV row of group slot sl of this block: the key's rank among the sequence's salient keys
+      if (lists && lane < nkc) sp.sblk[lane] = keys_before + (pinc - __popcll(word)) - 16 * g0;
       int n = 0;
       while (word) {
         sp.keys[g0 * 16 + n] = int16_t(lane * kBK + __builtin_ctzll(word));
@@ -327,8 +367,9 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
           const int kq = (tid + NT * it) & 15;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const int key = slot_key(pb * kBK + 4 * kq + j);
-            meta_slot[it][j] = key < 0 ? -1 : (ks_b ? ks_b[key] : key);
+            const int sl = pb * kBK + 4 * kq + j;
+            const int key = slot_key(sl);
+            meta_slot[it][j] = key < 0 ? -1 : (lists ? s_beg + sp.sblk[sp.gblk[sl >> 4]] + sl : (ks_b ? ks_b[key] : key));
           }
         }
       };
@@ -714,7 +755,8 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       // rewritten, statistics from the bf16 output vs the cached row (attention_aux_kernels.cu:22-72)
       float dot = 0.f, nn = 0.f, oo = 0.f;
       if (row_ok) {
-        const int64_t crow = a.c_start[b] + (qrow - a.cu_q[b]);
+        const int64_t crow = (a.c_seq_starts ? a.c_seq_starts[sid] + (Lk - (a.cu_q[b + 1] - a.cu_q[b])) : a.c_start[b]) +
+                             (qrow - a.cu_q[b]);
         uint16_t* cp = const_cast<uint16_t*>(a.C) + crow * ldq + head * kD + half * 4;
         uint16_t* op = a.O + qrow * ldq + head * kD + half * 4;
 #pragma unroll
@@ -765,12 +807,17 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       }
   } else {
     float dot = 0.f, nn = 0.f, oo = 0.f;
-    const int slot = row_ok ? a.sal_slot[row] : -1;
+    int slot;
+    if constexpr (lists)   // fused step: only whether the row is salient matters (its row-sparse tile finishes it)
+      slot = (row_ok && ((sp.rowflag[w] >> ql) & 1u)) ? 0 : -1;
+    else
+      slot = row_ok ? a.sal_slot[row] : -1;
     // salient rows are finished by the row-sparse tiles of the fused step (every lane stays for
     // the half-wave reductions below)
     const bool own = row_ok && !(a.skip_salient && slot >= 0);
     if (own) {
-      const int64_t crow = a.c_start ? a.c_start[b] + (row - row_beg) : int64_t(row);
+      const int64_t crow = a.c_seq_starts ? a.c_seq_starts[sid] + (Lk - (row_end - row_beg)) + (row - row_beg)
+                                          : (a.c_start ? a.c_start[b] + (row - row_beg) : int64_t(row));
       uint16_t* cp = const_cast<uint16_t*>(a.C) + crow * ldq + head * kD + half * 4;
       uint16_t* op = a.O + int64_t(row) * ldq + head * kD + half * 4;
       const uint16_t* sp = slot >= 0 ? a.o_sal + int64_t(slot) * ldq + head * kD + half * 4 : nullptr;
@@ -848,13 +895,18 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   __shared__ uint8_t gblk_lds[4 * kMaxBlk2];
   __shared__ int ngrp_lds;
   __shared__ float xch_lds[NW * 96];
+  __shared__ unsigned long long kbits_lds[kMaxBlk2];
+  __shared__ int sblk_lds[kMaxBlk2];
+  __shared__ uint32_t rowflag_lds[NW];
   const int wg = blockIdx.x;
   if (wg < n_rs_pad) {
     const int t = xcd_remap(wg, n_rs_pad);
     if (t < n_rs) attention_tile<AttnMode::RowSparse, NW>(rs, t, k_lds, vt_lds, ColSparseLds{});
   } else {
-    attention_tile<AttnMode::ColSparse, NW, CHUNKED>(cs, xcd_remap(wg - n_rs_pad, int(gridDim.x) - n_rs_pad), k_lds,
-                                                     vt_lds, ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds, xch_lds});
+    attention_tile<AttnMode::ColSparse, NW, CHUNKED, true>(cs, xcd_remap(wg - n_rs_pad, int(gridDim.x) - n_rs_pad), k_lds,
+                                                     vt_lds,
+                                                     ColSparseLds{m_lds, key_lds, gblk_lds, &ngrp_lds, xch_lds, kbits_lds,
+                                                                  sblk_lds, rowflag_lds});
   }
 }
 
@@ -885,18 +937,6 @@ __global__ __launch_bounds__(256) void colsparse_scatter_kernel(const int32_t* _
   atomicOr(&kmask[int64_t(b) * nblk + off / kBK], 1ull << (off % kBK));
 }
 
-// bf16 x 8 difference new - old, each element rounded once (the dV of attention.py:67-74)
-__device__ __forceinline__ uint4 bf16x8_sub(uint4 nw, uint4 o) {
-  const uint32_t ov[4] = {o.x, o.y, o.z, o.w}, nv[4] = {nw.x, nw.y, nw.z, nw.w};
-  uint32_t d[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float lo = __fsub_rn(__uint_as_float(nv[e] << 16), __uint_as_float(ov[e] << 16));
-    const float hi = __fsub_rn(__uint_as_float(nv[e] & 0xffff0000u), __uint_as_float(ov[e] & 0xffff0000u));
-    d[e] = pack_bf16x2(lo, hi);
-  }
-  return make_uint4(d[0], d[1], d[2], d[3]);
-}
 
 // dV = bf16(v_new - v_cache[row]) then v_cache[row] = v_new (attention.py:67-74, 89-96),
 // one wavefront per salient row, 16-byte lanes.
@@ -942,93 +982,6 @@ int launch_seq_row_starts(const int64_t* seq_starts, const int64_t* seq_ids, con
   if (B <= 0) return 0;
   seq_row_starts_kernel<<<unsigned(cdiv(B, 256)), 256, 0, s>>>(seq_starts, seq_ids, cu_k, cu_q, B, out);
   return check_launch("seq_row_starts_kernel");
-}
-
-// ---- native sparse step: preparation and per-salient-row work -----------------------------
-__global__ __launch_bounds__(256) void step_prep_kernel(StepPrepArgs a) {
-  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i < a.Tq) a.slot[i] = -1;
-  if (i < a.nmask) a.kmask[i] = 0;
-  if (i < a.Tk) a.kslot[i] = -1;
-  if (i < a.B) {
-    const int64_t sid = a.seq_ids[i];
-    a.v_start[i] = a.v_seq_starts[sid];
-    int64_t c = a.c_seq_starts[sid];
-    if (a.q_pruned) c += int64_t(a.cu_k[i + 1] - a.cu_k[i]) - int64_t(a.cu_q[i + 1] - a.cu_q[i]);
-    a.c_start[i] = c;
-  }
-}
-
-int launch_step_prep(const StepPrepArgs& a, hipStream_t s) {
-  int64_t n = a.Tq > a.nmask ? a.Tq : a.nmask;
-  if (a.Tk > n) n = a.Tk;
-  if (a.B > n) n = a.B;
-  if (n < 1) n = 1;
-  step_prep_kernel<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(a);
-  return check_launch("step_prep_kernel");
-}
-
-// dV = bf16(v_new - v_cache[row]), v_cache[row] = v_new for salient row j, spread over kSalQ
-// wavefronts per row (each a contiguous quarter of the row, all of its loads issued before its
-// stores: enough bytes in flight for a few hundred rows); lane 0 of the row's first wavefront
-// records the row in the slot maps and the salient-key bit of its 64-key block.
-constexpr int kSalQ = 4;
-
-__global__ __launch_bounds__(256) void step_salient_kernel(uint16_t* __restrict__ v_cache,
-                                                           const uint16_t* __restrict__ v_new,
-                                                           uint16_t* __restrict__ dv, int64_t row_elems,
-                                                           const int64_t* __restrict__ idx_k64,
-                                                           const int32_t* __restrict__ idx_q32, int n,
-                                                           const int32_t* __restrict__ cu_k, int B, int nblk,
-                                                           const int64_t* __restrict__ v_seq_starts,
-                                                           const int64_t* __restrict__ seq_ids,
-                                                           int32_t* __restrict__ slot,
-                                                           unsigned long long* __restrict__ kmask,
-                                                           int32_t* __restrict__ kslot) {
-  const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int j = wid / kSalQ, q = wid % kSalQ;
-  const int lane = threadIdx.x & 63;
-  if (j >= n) return;
-  const int64_t k = idx_k64[j];
-  const int bq = find_segment_wave(cu_k, B + 1, k);
-  const int b = bq < B ? bq : B - 1;
-  const int64_t off = k - cu_k[b];
-  const int64_t dest = v_seq_starts[seq_ids[b]] + off;
-  const int64_t n16 = row_elems / 8, per = (n16 + kSalQ - 1) / kSalQ;
-  const int64_t beg = q * per, end = beg + per < n16 ? beg + per : n16;
-  uint4* cr = reinterpret_cast<uint4*>(v_cache + dest * row_elems);
-  const uint4* nr = reinterpret_cast<const uint4*>(v_new + int64_t(j) * row_elems);
-  uint4* dr = reinterpret_cast<uint4*>(dv + int64_t(j) * row_elems);
-  int64_t i = beg + lane;
-  for (; i + 64 < end; i += 128) {
-    const uint4 o0 = cr[i], n0 = nr[i], o1 = cr[i + 64], n1 = nr[i + 64];
-    dr[i] = bf16x8_sub(n0, o0);
-    dr[i + 64] = bf16x8_sub(n1, o1);
-    cr[i] = n0;
-    cr[i + 64] = n1;
-  }
-  for (; i < end; i += 64) {
-    const uint4 o = cr[i], nw = nr[i];
-    dr[i] = bf16x8_sub(nw, o);
-    cr[i] = nw;
-  }
-  if (q == 0 && lane == 0) {
-    slot[idx_q32[j]] = j;
-    kslot[k] = j;
-    if (bq < B && off < cu_k[b + 1] - cu_k[b]) atomicOr(&kmask[int64_t(b) * nblk + off / kBK], 1ull << (off % kBK));
-  }
-}
-
-int launch_step_salient(uint16_t* v_cache, const uint16_t* v_new, uint16_t* dv, int64_t row_elems,
-                        const int64_t* idx_k64, const int32_t* idx_q32, int n, const int32_t* cu_k, int B, int nblk,
-                        const int64_t* v_seq_starts, const int64_t* seq_ids, int32_t* slot, uint64_t* kmask,
-                        int32_t* kslot, hipStream_t s) {
-  DYLLM_REQUIRE(row_elems % 8 == 0, "V row width must be a multiple of 8");
-  if (n <= 0) return 0;
-  step_salient_kernel<<<unsigned(cdiv(int64_t(n) * kSalQ, 4)), 256, 0, s>>>(
-      v_cache, v_new, dv, row_elems, idx_k64, idx_q32, n, cu_k, B, nblk, v_seq_starts, seq_ids, slot,
-      reinterpret_cast<unsigned long long*>(kmask), kslot);
-  return check_launch("step_salient_kernel");
 }
 
 template <AttnMode MODE, int NW>

@@ -107,7 +107,7 @@ int dyllm_attention_timer_read(float* total_ms, int* launches) {
   tm.used = 0;
   return 0;
 }
-int dyllm_abi_version(void) { return 3; }
+int dyllm_abi_version(void) { return 4; }
 
 // ---------------------------------------------------------------------------------------
 size_t dyllm_attention_sparse_workspace_bytes(int batch, int num_heads, int64_t total_q, int max_seqlen_k) {
@@ -150,8 +150,7 @@ static int colsparse_impl(const void* q, const void* k, const int64_t* kv_start,
                           int64_t total_k, int num_salient, const int32_t* idx_salient_q,
                           const int32_t* idx_salient_k, float* cosine_stats, uint8_t* cosine_out, float threshold,
                           void* workspace, size_t workspace_bytes, bool compact_dv, void* stream,
-                          bool maps_ready = false, bool reduce = true, const AttnArgs* fused_rs = nullptr,
-                          int fused_rs_rows = 0) {
+                          bool maps_ready = false, bool reduce = true) {
   DYLLM_NONNULL(q);
   DYLLM_NONNULL(k);
   DYLLM_NONNULL(c);
@@ -211,27 +210,7 @@ static int colsparse_impl(const void* q, const void* k, const int64_t* kv_start,
   a.Tq = total_q;
   // the reference uses rsqrt(head_dim) here, not the layer's scale (sm80.cu:166-168)
   a.scale_log2 = (1.0f / sqrtf(float(head_dim))) * kLog2e;
-  if (fused_rs) {
-    // salient rows are finished by the row-sparse tiles launched together with these
-    a.skip_salient = 1;
-    AttnTimer& tm = g_attn_timer;
-    hipEvent_t e1 = nullptr;
-    if (tm.enabled) {
-      if (tm.used == tm.ev.size()) {
-        hipEvent_t a0 = nullptr, a1 = nullptr;
-        if (hipEventCreate(&a0) != hipSuccess || hipEventCreate(&a1) != hipSuccess)
-          return fail("hipEventCreate failed (attention timer)");
-        tm.ev.emplace_back(a0, a1);
-      }
-      if (hipEventRecord(tm.ev[tm.used].first, s) != hipSuccess) return fail("hipEventRecord failed (attention timer)");
-      e1 = tm.ev[tm.used].second;
-      ++tm.used;
-    }
-    if (int rc = launch_attention_step(*fused_rs, fused_rs_rows, a, max_seqlen_q, s)) return rc;
-    if (e1 && hipEventRecord(e1, s) != hipSuccess) return fail("hipEventRecord failed (attention timer)");
-  } else {
-    if (int rc = launch_attention(AttnMode::ColSparse, a, max_seqlen_q, s)) return rc;
-  }
+  if (int rc = launch_attention(AttnMode::ColSparse, a, max_seqlen_q, s)) return rc;
   if (!reduce) return 0;
   return launch_saliency_reduce(part, cosine_stats, cosine_out, total_q, num_heads, threshold, s);
 }
@@ -268,10 +247,201 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
 
 size_t dyllm_sparse_step_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim, int64_t total_q,
                                          int64_t total_k, int max_seqlen_k, int64_t num_salient) {
+  (void)batch;
+  (void)total_k;
+  (void)max_seqlen_k;
   const size_t n = size_t(num_salient > 0 ? num_salient : 0);
-  return align256(n * num_kv_heads * head_dim * 2) + align256(n * num_heads * head_dim * 2) +
-         2 * align256(size_t(batch) * 8) + align256(size_t(cdiv(total_q, 256)) * 4) +
-         dyllm_attention_colsparse_workspace_bytes(batch, num_heads, total_q, total_k, max_seqlen_k);
+  return align256(n * num_kv_heads * head_dim * 2) + align256(size_t(cdiv(total_q > 0 ? total_q : 1, 256)) * 4) +
+         align256(size_t(num_heads) * 3 * size_t(total_q > 0 ? total_q : 0) * 4);
+}
+
+// the fused attention launch, bracketed by the attention timer's events when it is enabled
+static int timed_attention_step(const AttnArgs& rs, int rs_rows, const AttnArgs& cs, int cs_rows, hipStream_t s) {
+  AttnTimer& tm = g_attn_timer;
+  hipEvent_t e1 = nullptr;
+  if (tm.enabled) {
+    if (tm.used == tm.ev.size()) {
+      hipEvent_t a0 = nullptr, a1 = nullptr;
+      if (hipEventCreate(&a0) != hipSuccess || hipEventCreate(&a1) != hipSuccess)
+        return fail("hipEventCreate failed (attention timer)");
+      tm.ev.emplace_back(a0, a1);
+    }
+    if (hipEventRecord(tm.ev[tm.used].first, s) != hipSuccess) return fail("hipEventRecord failed (attention timer)");
+    e1 = tm.ev[tm.used].second;
+    ++tm.used;
+  }
+  if (int rc = launch_attention_step(rs, rs_rows, cs, cs_rows, s)) return rc;
+  if (e1 && hipEventRecord(e1, s) != hipSuccess) return fail("hipEventRecord failed (attention timer)");
+  return 0;
+}
+
+// Body of dyllm_sparse_attention_step(_kv): three launches and the compaction pair.
+//   1. step_rows_kernel: per salient row, [K/V epilogue], dV (at the key's rank within its
+//      sequence) and the V-cache update;
+//   2. attention_step_kernel: row-sparse tiles of the salient queries + column-sparse tiles of
+//      the others (their salient maps built in LDS from the lists);
+//   3. reduce_stats_kernel + compact_blocks_kernel: tau test and the next salient set.
+static int sparse_step(const dyllm_kv_epilogue* epi, const void* q, const void* k, const int64_t* k_start,
+                       void* v_cache, const int64_t* v_seq_starts, const void* v_new, void* c_cache,
+                       const int64_t* c_seq_starts, const int64_t* seq_ids, int batch, int num_heads, int num_kv_heads,
+                       int head_dim, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                       const int32_t* cu_promptlens, int max_seqlen_q, int max_seqlen_k, int64_t total_q,
+                       int64_t total_k, int num_salient, int max_salientlen, const int32_t* cu_salientlens,
+                       const int32_t* idx_q32, const int64_t* idx_k64, const int32_t* idx_k32, float softmax_scale,
+                       float threshold, void* out, float* cosine_stats, uint8_t* cosine_out, int64_t* next_idx64,
+                       int32_t* next_idx32, int64_t* next_idx_k64, int32_t* next_idx_k32,
+                       int32_t* next_cu_salientlens, int32_t* next_count, const int64_t* dest_seq_starts,
+                       int64_t* next_dest_rows, int32_t* host_meta, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  (void)idx_k64;
+  DYLLM_NONNULL(q);
+  DYLLM_NONNULL(v_cache);
+  DYLLM_NONNULL(v_seq_starts);
+  DYLLM_NONNULL(c_cache);
+  DYLLM_NONNULL(c_seq_starts);
+  DYLLM_NONNULL(seq_ids);
+  DYLLM_NONNULL(out);
+  DYLLM_NONNULL(cu_seqlens_q);
+  DYLLM_NONNULL(cu_seqlens_k);
+  DYLLM_NONNULL(cu_salientlens);
+  DYLLM_NONNULL(cosine_stats);
+  DYLLM_NONNULL(cosine_out);
+  DYLLM_NONNULL(next_idx64);
+  DYLLM_NONNULL(next_cu_salientlens);
+  DYLLM_NONNULL(next_count);
+  DYLLM_REQUIRE(head_dim == 128, "supported head dimension is 128, got " + std::to_string(head_dim));
+  DYLLM_REQUIRE(batch >= 1, "batch must be >= 1");
+  DYLLM_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
+                "query heads must be a positive multiple of KV heads");
+  DYLLM_REQUIRE(total_q > 0 && total_k > 0 && total_q < (int64_t(1) << 31) && total_k < (int64_t(1) << 31),
+                "token counts out of range");
+  DYLLM_REQUIRE(max_seqlen_q > 0 && max_seqlen_q <= total_q && max_seqlen_k > 0, "bad maximum sequence lengths");
+  DYLLM_REQUIRE(num_salient >= 0 && num_salient <= total_q, "num_salient out of range");
+  DYLLM_REQUIRE(num_salient == 0 || (idx_q32 && idx_k32), "salient rows need the int32 Q and K index lists");
+  DYLLM_REQUIRE(cu_promptlens == nullptr || next_idx_k64 != nullptr, "Q-pruned steps need next_idx_k64");
+  if (epi) {
+    DYLLM_REQUIRE(k == nullptr && k_start == nullptr && v_new == nullptr,
+                  "with a K/V epilogue, K comes from its cache and v from its rows (k, k_start, v_new must be NULL)");
+    DYLLM_REQUIRE(epi->k_cache && epi->k_seq_starts && epi->positions && epi->cos_table && epi->sin_table,
+                  "the K/V epilogue needs k_cache, k_seq_starts, positions and the cos / sin tables");
+    DYLLM_REQUIRE(num_salient == 0 || epi->kv, "the K/V epilogue needs the kv rows");
+    DYLLM_REQUIRE(epi->max_position >= 1, "max_position must be positive");
+    DYLLM_REQUIRE(epi->ld_kv >= int64_t(2) * num_kv_heads * head_dim && epi->ld_kv % 8 == 0,
+                  "kv row stride must be >= 2 * num_kv_heads * 128 and a multiple of 8");
+    DYLLM_REQUIRE(aligned_to(16, {epi->kv, epi->cos_table, epi->sin_table, epi->k_norm_weight, epi->k_cache}),
+                  "kv, the cos / sin tables, k_norm_weight and k_cache must be 16-byte aligned");
+  } else {
+    DYLLM_NONNULL(k);
+    DYLLM_REQUIRE(num_salient == 0 || v_new, "salient rows need v_new");
+  }
+  const size_t need = dyllm_sparse_step_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, total_q, total_k,
+                                                        max_seqlen_k, num_salient);
+  DYLLM_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need " + std::to_string(need) + " bytes");
+  const hipStream_t s = DYLLM_STREAM(stream);
+  int32_t* host_meta_dev = nullptr;
+  if (host_meta) {
+    void* p = nullptr;
+    DYLLM_REQUIRE(hipHostGetDevicePointer(&p, host_meta, 0) == hipSuccess && p != nullptr,
+                  "host_meta must be pinned host memory (hipHostMalloc)");
+    host_meta_dev = static_cast<int32_t*>(p);
+  }
+  const int64_t kv_size = int64_t(num_kv_heads) * head_dim;
+  const size_t n = size_t(num_salient);
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* dv = reinterpret_cast<uint16_t*>(ws);
+  ws += align256(n * kv_size * 2);
+  int32_t* block_counts = reinterpret_cast<int32_t*>(ws);  // salient rows per 256-row block
+  ws += align256(size_t(cdiv(total_q, 256)) * 4);
+  float* part = reinterpret_cast<float*>(ws);
+  const bool q_pruned = cu_promptlens != nullptr;
+  const int nblk = int(cdiv(max_seqlen_k, 64));
+
+  // 1. per salient row: [K/V epilogue], dV, V-cache update (attention.py:67-74, 89-96; llada.py:103-146)
+  if (num_salient > 0) {
+    StepRowsArgs ra{};
+    ra.n = num_salient;
+    ra.B = batch;
+    ra.cu_sal = cu_salientlens;
+    ra.idx_k32 = idx_k32;
+    ra.cu_k = cu_seqlens_k;
+    ra.seq_ids = seq_ids;
+    ra.v_cache = static_cast<uint16_t*>(v_cache);
+    ra.v_seq_starts = v_seq_starts;
+    ra.kv_size = kv_size;
+    ra.Hkv = num_kv_heads;
+    ra.v_new = static_cast<const uint16_t*>(v_new);
+    if (epi) {
+      ra.kv = static_cast<const uint16_t*>(epi->kv);
+      ra.ld_kv = epi->ld_kv;
+      ra.kv_rows = epi->kv_rows;
+      ra.positions = epi->positions;
+      ra.pos_idx = epi->pos_idx;
+      ra.cos = epi->cos_table;
+      ra.sin = epi->sin_table;
+      ra.max_position = epi->max_position;
+      ra.k_norm = static_cast<const uint16_t*>(epi->k_norm_weight);
+      ra.eps = epi->eps;
+      ra.k_cache = static_cast<uint16_t*>(epi->k_cache);
+      ra.k_seq_starts = epi->k_seq_starts;
+    }
+    ra.dv = dv;
+    if (int rc = launch_step_rows(ra, s)) return rc;
+  }
+  // 2. row-sparse attention of the salient queries vs the full cached K/V (attention.py:76-87),
+  // launched together with the column-sparse attention of the other rows (statistics + tau
+  // inputs, context cache updated in place); each salient row's tile writes its final output,
+  // context row and statistics itself (attention_aux_kernels.cu:22-72)
+  AttnArgs rs{};
+  rs.Q = static_cast<const uint16_t*>(q);
+  rs.K = static_cast<const uint16_t*>(epi ? epi->k_cache : k);
+  rs.V = static_cast<const uint16_t*>(v_cache);
+  rs.C = static_cast<const uint16_t*>(c_cache);
+  rs.O = static_cast<uint16_t*>(out);
+  rs.cu_rows = cu_salientlens;
+  rs.cu_k = cu_seqlens_k;
+  rs.cu_q = cu_seqlens_q;
+  rs.kv_start = k_start;
+  rs.seq_ids = seq_ids;
+  rs.k_seq_starts = epi ? epi->k_seq_starts : nullptr;
+  rs.v_seq_starts = v_seq_starts;
+  rs.c_seq_starts = c_seq_starts;
+  rs.c_inplace = 1;
+  rs.q_rows = idx_q32;
+  rs.part = part;
+  rs.Tq = total_q;
+  rs.B = batch;
+  rs.H = num_heads;
+  rs.Hkv = num_kv_heads;
+  rs.scale_log2 = softmax_scale * kLog2e;
+  AttnArgs cs = rs;
+  cs.V = dv;
+  cs.cu_rows = cu_seqlens_q;
+  cs.cu_q = nullptr;
+  cs.q_rows = nullptr;
+  cs.v_seq_starts = nullptr;
+  cs.skip_salient = 1;
+  cs.nblk = nblk;
+  cs.cu_sal = cu_salientlens;
+  cs.sal_q = num_salient > 0 ? idx_q32 : nullptr;
+  cs.sal_k = num_salient > 0 ? idx_k32 : nullptr;
+  // the reference's column-sparse kernel uses rsqrt(head_dim), not the layer's scale (sm80.cu:166-168)
+  cs.scale_log2 = (1.0f / sqrtf(float(head_dim))) * kLog2e;
+  const int rs_rows = num_salient > 0 ? (max_salientlen > 0 ? max_salientlen : max_seqlen_q) : 0;
+  if (num_salient == 0) {
+    // no salient key: every column-sparse row is C_old + 0 (an empty list drives the same LDS path)
+    cs.sal_q = idx_q32 ? idx_q32 : reinterpret_cast<const int32_t*>(cu_salientlens);
+    cs.sal_k = idx_k32 ? idx_k32 : reinterpret_cast<const int32_t*>(cu_salientlens);
+  }
+  if (int rc = timed_attention_step(rs, rs_rows, cs, max_seqlen_q, s)) return rc;
+  // 3. statistics reduction, tau test and compaction of the next salient set (attention.py:141-173)
+  if (int rc = launch_reduce_stats(part, cosine_stats, cosine_out, total_q, num_heads, threshold, block_counts, s))
+    return rc;
+  DYLLM_REQUIRE(next_dest_rows == nullptr || dest_seq_starts != nullptr, "next_dest_rows needs dest_seq_starts");
+  CompactDest dd{};
+  if (next_dest_rows) dd = CompactDest{dest_seq_starts, seq_ids, cu_seqlens_k, next_dest_rows};
+  return launch_compact_blocks(cosine_out, total_q, block_counts, cu_seqlens_q, batch, cu_promptlens, next_idx64,
+                               next_idx32, q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr,
+                               next_cu_salientlens, next_count, host_meta_dev, s, dd);
 }
 
 int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_start, void* v_cache,
@@ -287,109 +457,34 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                 int32_t* next_cu_salientlens, int32_t* next_count, const int64_t* dest_seq_starts,
                                 int64_t* next_dest_rows, int32_t* host_meta, void* workspace, size_t workspace_bytes,
                                 void* stream) {
-  DYLLM_NONNULL(v_cache);
-  DYLLM_NONNULL(v_seq_starts);
-  DYLLM_NONNULL(c_seq_starts);
-  DYLLM_NONNULL(seq_ids);
-  DYLLM_NONNULL(next_idx64);
-  DYLLM_NONNULL(next_cu_salientlens);
-  DYLLM_NONNULL(next_count);
-  DYLLM_REQUIRE(num_salient >= 0, "num_salient must be non-negative");
-  DYLLM_REQUIRE(num_salient == 0 || (v_new && cu_salientlens && idx_q32 && idx_k64 && idx_k32),
-                "salient rows need v_new, cu_salientlens and the Q/K index lists");
-  DYLLM_REQUIRE(cu_promptlens == nullptr || next_idx_k64 != nullptr, "Q-pruned steps need next_idx_k64");
-  const size_t need = dyllm_sparse_step_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, total_q, total_k,
-                                                        max_seqlen_k, num_salient);
-  DYLLM_REQUIRE(workspace && workspace_bytes >= need, "workspace too small: need " + std::to_string(need) + " bytes");
-  const hipStream_t s = DYLLM_STREAM(stream);
-  int32_t* host_meta_dev = nullptr;
-  if (host_meta) {
-    void* p = nullptr;
-    DYLLM_REQUIRE(hipHostGetDevicePointer(&p, host_meta, 0) == hipSuccess && p != nullptr,
-                  "host_meta must be pinned host memory (hipHostMalloc)");
-    host_meta_dev = static_cast<int32_t*>(p);
-  }
-  const size_t n = size_t(num_salient);
-  char* ws = static_cast<char*>(workspace);
-  uint16_t* dv = reinterpret_cast<uint16_t*>(ws);
-  ws += align256(n * num_kv_heads * head_dim * 2);
-  uint16_t* o_sal = reinterpret_cast<uint16_t*>(ws);
-  ws += align256(n * num_heads * head_dim * 2);
-  int64_t* v_start = reinterpret_cast<int64_t*>(ws);
-  ws += align256(size_t(batch) * 8);
-  int64_t* c_start = reinterpret_cast<int64_t*>(ws);
-  ws += align256(size_t(batch) * 8);
-  int32_t* block_counts = reinterpret_cast<int32_t*>(ws);  // salient rows per 256-row block
-  ws += align256(size_t(cdiv(total_q, 256)) * 4);
-  const size_t cs_bytes = workspace_bytes - size_t(ws - static_cast<char*>(workspace));
-  const bool q_pruned = cu_promptlens != nullptr;
+  return sparse_step(nullptr, q, k, k_start, v_cache, v_seq_starts, v_new, c_cache, c_seq_starts, seq_ids, batch,
+                     num_heads, num_kv_heads, head_dim, cu_seqlens_q, cu_seqlens_k, cu_promptlens, max_seqlen_q,
+                     max_seqlen_k, total_q, total_k, num_salient, max_salientlen, cu_salientlens, idx_q32, idx_k64,
+                     idx_k32, softmax_scale, threshold, out, cosine_stats, cosine_out, next_idx64, next_idx32,
+                     next_idx_k64, next_idx_k32, next_cu_salientlens, next_count, dest_seq_starts, next_dest_rows,
+                     host_meta, workspace, workspace_bytes, stream);
+}
 
-  // reset the maps, first V-cache / context-cache row of every sequence (one launch)
-  const int nblk = int(cdiv(max_seqlen_k, 64));
-  const ColsWs cw = cols_ws(ws, batch, num_heads, total_q, nblk, true);
-  StepPrepArgs pa{};
-  pa.slot = cw.slot;
-  pa.Tq = total_q;
-  pa.kmask = cw.kmask;
-  pa.nmask = int64_t(batch) * nblk;
-  pa.kslot = cw.kslot;
-  pa.Tk = total_k;
-  pa.v_seq_starts = v_seq_starts;
-  pa.c_seq_starts = c_seq_starts;
-  pa.seq_ids = seq_ids;
-  pa.cu_k = cu_seqlens_k;
-  pa.cu_q = cu_seqlens_q;
-  pa.q_pruned = q_pruned ? 1 : 0;
-  pa.B = batch;
-  pa.v_start = v_start;
-  pa.c_start = c_start;
-  if (int rc = launch_step_prep(pa, s)) return rc;
-  if (num_salient > 0) {
-    // dV of the salient keys + V-cache update (attention.py:67-74, 89-96) and the salient maps
-    if (int rc = launch_step_salient(static_cast<uint16_t*>(v_cache), static_cast<const uint16_t*>(v_new), dv,
-                                     int64_t(num_kv_heads) * head_dim, idx_k64, idx_q32, num_salient, cu_seqlens_k,
-                                     batch, nblk, v_seq_starts, seq_ids, cw.slot, cw.kmask, cw.kslot, s))
-      return rc;
-  }
-  // row-sparse attention of the salient queries vs the full cached K/V (attention.py:76-87),
-  // launched together with the column-sparse attention of the other rows (statistics + tau
-  // inputs, context cache updated in place); each salient row's tile writes its final output,
-  // context row and statistics itself (attention_aux_kernels.cu:22-72)
-  AttnArgs rs{};
-  rs.Q = static_cast<const uint16_t*>(q);
-  rs.K = static_cast<const uint16_t*>(k);
-  rs.V = static_cast<const uint16_t*>(v_cache);
-  rs.C = static_cast<const uint16_t*>(c_cache);
-  rs.O = static_cast<uint16_t*>(out);
-  rs.cu_rows = cu_salientlens;
-  rs.cu_k = cu_seqlens_k;
-  rs.cu_q = cu_seqlens_q;
-  rs.kv_start = k_start;
-  rs.v_start = v_start;
-  rs.c_start = c_start;
-  rs.c_inplace = 1;
-  rs.q_rows = idx_q32;
-  rs.part = cw.part;
-  rs.Tq = total_q;
-  rs.B = batch;
-  rs.H = num_heads;
-  rs.Hkv = num_kv_heads;
-  rs.scale_log2 = softmax_scale * kLog2e;
-  const int rs_rows = num_salient > 0 ? (max_salientlen > 0 ? max_salientlen : max_seqlen_q) : 0;
-  if (int rc = colsparse_impl(q, k, k_start, num_salient ? dv : nullptr, c_cache, c_start, 1, o_sal, out, batch,
-                              num_heads, num_kv_heads, head_dim, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
-                              max_seqlen_k, total_q, total_k, num_salient, idx_q32, idx_k32, cosine_stats,
-                              cosine_out, threshold, ws, cs_bytes, true, stream, true, false, &rs, rs_rows))
-    return rc;
-  // statistics reduction, tau test and compaction of the next salient set (attention.py:141-173)
-  if (int rc = launch_reduce_stats(cw.part, cosine_stats, cosine_out, total_q, num_heads, threshold, block_counts, s))
-    return rc;
-  DYLLM_REQUIRE(next_dest_rows == nullptr || dest_seq_starts != nullptr, "next_dest_rows needs dest_seq_starts");
-  CompactDest dd{};
-  if (next_dest_rows) dd = CompactDest{dest_seq_starts, seq_ids, cu_seqlens_k, next_dest_rows};
-  return launch_compact_blocks(cosine_out, total_q, block_counts, cu_seqlens_q, batch, cu_promptlens, next_idx64,
-                               next_idx32, q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr,
-                               next_cu_salientlens, next_count, host_meta_dev, s, dd);
+int dyllm_sparse_attention_step_kv(const dyllm_kv_epilogue* kv_epilogue, const void* q, const void* k,
+                                   const int64_t* k_start, void* v_cache, const int64_t* v_seq_starts,
+                                   const void* v_new, void* c_cache, const int64_t* c_seq_starts,
+                                   const int64_t* seq_ids, int batch, int num_heads, int num_kv_heads, int head_dim,
+                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                   const int32_t* cu_promptlens, int max_seqlen_q, int max_seqlen_k, int64_t total_q,
+                                   int64_t total_k, int num_salient, int max_salientlen,
+                                   const int32_t* cu_salientlens, const int32_t* idx_q32, const int64_t* idx_k64,
+                                   const int32_t* idx_k32, float softmax_scale, float threshold, void* out,
+                                   float* cosine_stats, uint8_t* cosine_out, int64_t* next_idx64, int32_t* next_idx32,
+                                   int64_t* next_idx_k64, int32_t* next_idx_k32, int32_t* next_cu_salientlens,
+                                   int32_t* next_count, const int64_t* dest_seq_starts, int64_t* next_dest_rows,
+                                   int32_t* host_meta, void* workspace, size_t workspace_bytes, void* stream) {
+  DYLLM_NONNULL(kv_epilogue);
+  return sparse_step(kv_epilogue, q, k, k_start, v_cache, v_seq_starts, v_new, c_cache, c_seq_starts, seq_ids, batch,
+                     num_heads, num_kv_heads, head_dim, cu_seqlens_q, cu_seqlens_k, cu_promptlens, max_seqlen_q,
+                     max_seqlen_k, total_q, total_k, num_salient, max_salientlen, cu_salientlens, idx_q32, idx_k64,
+                     idx_k32, softmax_scale, threshold, out, cosine_stats, cosine_out, next_idx64, next_idx32,
+                     next_idx_k64, next_idx_k32, next_cu_salientlens, next_count, dest_seq_starts, next_dest_rows,
+                     host_meta, workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------------------------------

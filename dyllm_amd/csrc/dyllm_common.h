@@ -103,6 +103,19 @@ __device__ __forceinline__ int find_segment_wave(const T* cu, int n, int64_t r) 
   return cnt > 0 ? cnt - 1 : 0;
 }
 
+// bf16 x 8 difference new - old, each element rounded once (the dV of attention.py:67-74)
+__device__ __forceinline__ uint4 bf16x8_sub(uint4 nw, uint4 o) {
+  const uint32_t ov[4] = {o.x, o.y, o.z, o.w}, nv[4] = {nw.x, nw.y, nw.z, nw.w};
+  uint32_t d[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = __fsub_rn(__uint_as_float(nv[e] << 16), __uint_as_float(ov[e] << 16));
+    const float hi = __fsub_rn(__uint_as_float(nv[e] & 0xffff0000u), __uint_as_float(ov[e] & 0xffff0000u));
+    d[e] = pack_bf16x2(lo, hi);
+  }
+  return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
 __host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---- host-side error plumbing -------------------------------------------------------

@@ -125,6 +125,19 @@ struct AttnArgs {
   int nblk;                 // kmask row stride
   int64_t Tq;               // ColSparse: rows of part
   float scale_log2;
+  // fused step: cache rows through the per-sequence-id start tables (instead of kv_start /
+  // v_start / c_start). K row of key k of batch entry b: k_seq_starts[seq_ids[b]] + k; V row
+  // likewise; context row of Q row r: c_seq_starts[seq_ids[b]] + (Lk_b - Lq_b) + (r - first Q row).
+  const int64_t* seq_ids;       // [B]
+  const int64_t* k_seq_starts;  // optional
+  const int64_t* v_seq_starts;  // optional
+  const int64_t* c_seq_starts;  // optional
+  // ColSparse, fused step: the salient maps are built in LDS by each workgroup from the compact
+  // lists (no global maps): sal_q / sal_k entries of sequence b are [cu_sal[b], cu_sal[b+1]).
+  // dV row of a salient key = cu_sal[b] + its rank among the sequence's salient keys.
+  const int32_t* cu_sal;        // [B+1]
+  const int32_t* sal_q;         // Q-space rows
+  const int32_t* sal_k;         // K-space rows (packed by cu_k)
 };
 int launch_attention(AttnMode mode, const AttnArgs& a, int max_rows_per_seq, hipStream_t s);
 // Row-sparse tiles (fused output) and column-sparse tiles in one launch (4-wave workgroups).
@@ -163,32 +176,39 @@ int attention_kernel_info(int dim, int64_t* out);
 int launch_colsparse_prep(const int32_t* idx_q, const int32_t* idx_k, int n_sal, const int32_t* cu_k, int B,
                           int nblk, int32_t* slot, int64_t Tq, uint64_t* kmask, int32_t* kslot, int64_t Tk,
                           hipStream_t s);
-// Native sparse step, preparation (one launch): slot / salient-key maps reset, first V-cache
-// and context-cache row of every sequence.
-struct StepPrepArgs {
-  int32_t* slot;                // [Tq] -> -1
-  int64_t Tq;
-  uint64_t* kmask;              // [nmask] -> 0
-  int64_t nmask;
-  int32_t* kslot;               // [Tk] -> -1
-  int64_t Tk;
-  const int64_t* v_seq_starts;  // V-cache first row per sequence id
-  const int64_t* c_seq_starts;  // context-cache first row per sequence id
-  const int64_t* seq_ids;       // [B]
-  const int32_t* cu_k;          // [B+1]
-  const int32_t* cu_q;          // [B+1] (Q-pruned: the context rows start at the queried tail block)
-  int q_pruned;
+// Native sparse step, per salient row (one launch, rope.hip): the optional K/V epilogue (k ->
+// k_norm -> RoPE -> K-cache row), dV = bf16(v_new - v_cache[row]) stored at row cu_sal[b] + the
+// key's rank among the salient keys of its sequence (the order the column-sparse tiles visit
+// them in), and the V-cache row = v_new. Workgroup 0 also zeroes `zero[0..nzero)`.
+struct StepRowsArgs {
+  int n;                        // salient rows (list entries)
   int B;
-  int64_t* v_start;             // [B] out
-  int64_t* c_start;             // [B] out
+  const int32_t* cu_sal;        // [B+1]
+  const int32_t* idx_k32;       // [n] K-space rows (packed by cu_k)
+  const int32_t* cu_k;          // [B+1]
+  const int64_t* seq_ids;       // [B]
+  uint16_t* v_cache;            // rows of kv_size elements
+  const int64_t* v_seq_starts;
+  int64_t kv_size;              // Hkv * 128
+  int Hkv;
+  const uint16_t* v_new;        // [n, kv_size] in list order; NULL: v is the second half of the kv rows
+  const uint16_t* kv;           // optional [*, ld_kv] = [k | v] of the projection (K/V epilogue)
+  int64_t ld_kv;
+  const int32_t* kv_rows;       // optional: kv row of list entry j (else j)
+  const int64_t* positions;
+  const int32_t* pos_idx;       // optional: index into positions of entry j (else j)
+  const float* cos;             // [max_position, 64]
+  const float* sin;
+  int64_t max_position;
+  const uint16_t* k_norm;       // optional [128]
+  float eps;
+  uint16_t* k_cache;            // rows of kv_size elements
+  const int64_t* k_seq_starts;
+  uint16_t* dv;                 // [n, kv_size] out
+  int32_t* zero;                // optional words zeroed by workgroup 0
+  int nzero;
 };
-int launch_step_prep(const StepPrepArgs& a, hipStream_t s);
-// Native sparse step, per salient row (one launch): dV = bf16(v_new - v_cache[row]), V-cache
-// update, and the slot / salient-key-bit / dV-slot maps of the column-sparse kernel.
-int launch_step_salient(uint16_t* v_cache, const uint16_t* v_new, uint16_t* dv, int64_t row_elems,
-                        const int64_t* idx_k64, const int32_t* idx_q32, int n, const int32_t* cu_k, int B, int nblk,
-                        const int64_t* v_seq_starts, const int64_t* seq_ids, int32_t* slot, uint64_t* kmask,
-                        int32_t* kslot, hipStream_t s);
+int launch_step_rows(const StepRowsArgs& a, hipStream_t s);
 int launch_v_delta_update(uint16_t* v_cache, const uint16_t* v_new, const int64_t* dest_rows, int64_t n,
                           int64_t row_elems, uint16_t* dv, hipStream_t s);
 int launch_seq_row_starts(const int64_t* seq_starts, const int64_t* seq_ids, const int32_t* cu_k,

@@ -35,50 +35,38 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 }
 __device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
-__global__ __launch_bounds__(256) void kv_rope_scatter_kernel(KvRopeArgs a) {
-  const int64_t j = blockIdx.x;
-  const int64_t n = a.rows_dev ? int64_t(a.rows_dev[0]) : a.rows;
-  if (j >= n) return;
+// k of one row (Hkv heads of 128) -> optional per-head RMSNorm -> neox rotation at pos -> crow.
+// Thread t of the 256-thread workgroup takes head t / 8 (heads beyond 32 loop) and the rotation
+// pairs (d, d + 64), d = 8 (t % 8) .. 8 (t % 8) + 7.
+__device__ __forceinline__ void rope_k_row(const uint16_t* __restrict__ krow, uint16_t* __restrict__ crow, int Hkv,
+                                           int64_t pos, const float* __restrict__ cos_t,
+                                           const float* __restrict__ sin_t, const uint16_t* __restrict__ k_norm,
+                                           float eps) {
   constexpr int D = 128, HALF = 64;
   const int t = threadIdx.x;
-
-  // row-uniform chain
-  // positions are clamped to the table, as the reference does before its table lookup
-  // (rotary_embedding.py:45-48); the engine refuses sequences longer than the table
-  int64_t pos = a.positions[a.pos_idx ? int64_t(a.pos_idx[j]) : j];
-  pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
-  int64_t dest = j;   // in-place mode (no cache mapping): row j of the output
-  if (a.k_rows) {
-    const int64_t kk = a.k_rows[j];
-    const int b = find_segment_wave(a.cu_k, a.B + 1, kk);
-    dest = a.seq_starts[a.seq_ids[b]] + (kk - a.cu_k[b]);
-  }
-  const uint16_t* krow = a.kv + j * a.ld_kv;
-  uint16_t* crow = a.k_cache + dest * a.ld_cache;
-
   const int d0 = (t & 7) * 8;
   float c[8], s[8];
-  *reinterpret_cast<float4*>(c) = *reinterpret_cast<const float4*>(a.cos + pos * HALF + d0);
-  *reinterpret_cast<float4*>(c + 4) = *reinterpret_cast<const float4*>(a.cos + pos * HALF + d0 + 4);
-  *reinterpret_cast<float4*>(s) = *reinterpret_cast<const float4*>(a.sin + pos * HALF + d0);
-  *reinterpret_cast<float4*>(s + 4) = *reinterpret_cast<const float4*>(a.sin + pos * HALF + d0 + 4);
+  *reinterpret_cast<float4*>(c) = *reinterpret_cast<const float4*>(cos_t + pos * HALF + d0);
+  *reinterpret_cast<float4*>(c + 4) = *reinterpret_cast<const float4*>(cos_t + pos * HALF + d0 + 4);
+  *reinterpret_cast<float4*>(s) = *reinterpret_cast<const float4*>(sin_t + pos * HALF + d0);
+  *reinterpret_cast<float4*>(s + 4) = *reinterpret_cast<const float4*>(sin_t + pos * HALF + d0 + 4);
   float w1[8], w2[8];
-  if (a.k_norm) {
-    unpack8(*reinterpret_cast<const uint4*>(a.k_norm + d0), w1);
-    unpack8(*reinterpret_cast<const uint4*>(a.k_norm + d0 + HALF), w2);
+  if (k_norm) {
+    unpack8(*reinterpret_cast<const uint4*>(k_norm + d0), w1);
+    unpack8(*reinterpret_cast<const uint4*>(k_norm + d0 + HALF), w2);
   }
-  for (int h = t >> 3; h < a.Hkv; h += 32) {
+  for (int h = t >> 3; h < Hkv; h += 32) {
     float x1[8], x2[8];
     unpack8(*reinterpret_cast<const uint4*>(krow + h * D + d0), x1);
     unpack8(*reinterpret_cast<const uint4*>(krow + h * D + d0 + HALF), x2);
-    if (a.k_norm) {
+    if (k_norm) {
       float ss = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
       ss += __shfl_xor(ss, 1, 64);
       ss += __shfl_xor(ss, 2, 64);
       ss += __shfl_xor(ss, 4, 64);
-      const float r = rsqrtf(ss / float(D) + a.eps);
+      const float r = rsqrtf(ss / float(D) + eps);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         x1[i] = bf16_round(__fmul_rn(bf16_round(x1[i] * r), w1[i]));
@@ -95,11 +83,92 @@ __global__ __launch_bounds__(256) void kv_rope_scatter_kernel(KvRopeArgs a) {
     *reinterpret_cast<uint4*>(crow + h * D + d0) = pack8(y1);
     *reinterpret_cast<uint4*>(crow + h * D + d0 + HALF) = pack8(y2);
   }
+}
+
+// positions are clamped to the table, as the reference does before its table lookup
+// (rotary_embedding.py:45-48); the engine refuses sequences longer than the table
+__device__ __forceinline__ int64_t clamp_pos(int64_t pos, int64_t max_position) {
+  return pos < 0 ? 0 : (pos >= max_position ? max_position - 1 : pos);
+}
+
+__global__ __launch_bounds__(256) void kv_rope_scatter_kernel(KvRopeArgs a) {
+  const int64_t j = blockIdx.x;
+  const int64_t n = a.rows_dev ? int64_t(a.rows_dev[0]) : a.rows;
+  if (j >= n) return;
+  const int t = threadIdx.x;
+  // row-uniform chain
+  const int64_t pos = clamp_pos(a.positions[a.pos_idx ? int64_t(a.pos_idx[j]) : j], a.max_position);
+  int64_t dest = j;   // in-place mode (no cache mapping): row j of the output
+  if (a.k_rows) {
+    const int64_t kk = a.k_rows[j];
+    const int b = find_segment_wave(a.cu_k, a.B + 1, kk);
+    dest = a.seq_starts[a.seq_ids[b]] + (kk - a.cu_k[b]);
+  }
+  const uint16_t* krow = a.kv + j * a.ld_kv;
+  rope_k_row(krow, a.k_cache + dest * a.ld_cache, a.Hkv, pos, a.cos, a.sin, a.k_norm, a.eps);
   // v: kv_size values -> v_out row j (16 bytes per thread per pass)
   if (!a.v_out) return;
   const uint4* vr = reinterpret_cast<const uint4*>(krow + a.kv_size);
   uint4* vo = reinterpret_cast<uint4*>(a.v_out + j * a.kv_size);
   for (int64_t i = t; i < a.kv_size / 8; i += 256) vo[i] = vr[i];
+}
+
+// One 256-thread workgroup per salient list entry j (StepRowsArgs). Every wavefront derives the
+// entry's sequence and its key's rank among the sequence's salient keys itself (ballot counts over
+// the sequence's list segment, a few hundred entries at most), so no workgroup waits on another.
+__global__ __launch_bounds__(256) void step_rows_kernel(StepRowsArgs a) {
+  const int j = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63;
+  if (j == 0)
+    for (int i = t; i < a.nzero; i += 256) a.zero[i] = 0;
+  if (j >= a.n) return;
+  const int b = find_segment_wave(a.cu_sal, a.B + 1, j);
+  const int64_t s0 = a.cu_sal[b], s1 = a.cu_sal[b + 1];
+  const int64_t kbeg = a.cu_k[b], Lk = a.cu_k[b + 1] - kbeg;
+  const int64_t off = int64_t(a.idx_k32[j]) - kbeg;
+  // an entry outside its sequence's keys updates nothing (the attention tiles ignore it as well)
+  if (off < 0 || off >= Lk) return;
+  int rank = 0;
+  for (int64_t base = s0; base < s1; base += 64) {
+    const int64_t i = base + lane;
+    bool lt = false;
+    if (i < s1) {
+      const int64_t kk = int64_t(a.idx_k32[i]) - kbeg;
+      lt = kk >= 0 && kk < off;
+    }
+    rank += __popcll(__ballot(lt));
+  }
+  const int64_t sid = a.seq_ids[b];
+  const uint16_t* src = a.kv ? a.kv + (a.kv_rows ? int64_t(a.kv_rows[j]) : int64_t(j)) * a.ld_kv : nullptr;
+  const uint4* nr = reinterpret_cast<const uint4*>(src ? src + a.kv_size : a.v_new + int64_t(j) * a.kv_size);
+  uint4* cr = reinterpret_cast<uint4*>(a.v_cache + (a.v_seq_starts[sid] + off) * a.kv_size);
+  uint4* dr = reinterpret_cast<uint4*>(a.dv + (s0 + rank) * a.kv_size);
+  const int64_t n16 = a.kv_size / 8;
+  int64_t i = t;
+  for (; i + 256 < n16; i += 512) {   // both loads of a pair in flight before the stores
+    const uint4 o0 = cr[i], n0 = nr[i], o1 = cr[i + 256], n1 = nr[i + 256];
+    dr[i] = bf16x8_sub(n0, o0);
+    dr[i + 256] = bf16x8_sub(n1, o1);
+    cr[i] = n0;
+    cr[i + 256] = n1;
+  }
+  for (; i < n16; i += 256) {
+    const uint4 o = cr[i], nw = nr[i];
+    dr[i] = bf16x8_sub(nw, o);
+    cr[i] = nw;
+  }
+  if (src) {
+    const int64_t pos = clamp_pos(a.positions[a.pos_idx ? int64_t(a.pos_idx[j]) : int64_t(j)], a.max_position);
+    rope_k_row(src, a.k_cache + (a.k_seq_starts[sid] + off) * a.kv_size, a.Hkv, pos, a.cos, a.sin, a.k_norm,
+               a.eps);
+  }
+}
+
+int launch_step_rows(const StepRowsArgs& a, hipStream_t s) {
+  const int grid = a.n > 1 ? a.n : 1;
+  if (a.n <= 0 && a.nzero <= 0) return 0;
+  step_rows_kernel<<<unsigned(grid), 256, 0, s>>>(a);
+  return check_launch("step_rows_kernel");
 }
 
 int launch_kv_rope_scatter(const KvRopeArgs& a, hipStream_t s) {

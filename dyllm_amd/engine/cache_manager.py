@@ -202,6 +202,15 @@ class CacheManager:
                                    self.seq_start_gpu, seq_ids, pos_idx=pos_idx, k_norm_weight=k_norm_weight,
                                    eps=eps)
 
+    def kv_rows(self, kv: torch.Tensor, num_kv_heads: int, positions: torch.Tensor, cos: torch.Tensor,
+                sin: torch.Tensor, pos_idx: torch.Tensor, kv_rows: Optional[torch.Tensor] = None,
+                k_norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6) -> "ops.KvRows":
+        """The salient rows' [k | v] projection output as the sparse step's ``v`` (ops.KvRows): the
+        step itself writes their rotated keys into this cache (scatter_update fused with k_norm /
+        RoPE, llada.py:108-143) before its attention reads them."""
+        return ops.KvRows(kv, num_kv_heads, positions, cos, sin, self._slab, self.seq_start_gpu, kv_rows=kv_rows,
+                          pos_idx=pos_idx, k_norm_weight=k_norm_weight, eps=eps)
+
     def finish(self, finished_seq_ids: List[int]):
         if len(finished_seq_ids) == 0:
             return False

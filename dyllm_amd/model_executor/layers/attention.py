@@ -47,12 +47,19 @@ class Attention(nn.Module):
         # the rows of the next salient set in it (the FFN's scatter targets)
         self.ffn_cache = None
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    def forward(self, q: torch.Tensor, k, v) -> torch.Tensor:
+        """``k``, ``v`` as the reference's (the V rows of the salient keys on a sparse step); or,
+        on a sparse step, ``k = None`` and ``v`` an ``ops.KvRows``: the salient-row projection
+        output whose K/V epilogue the step's first launch applies (K then read from its cache)."""
         ctx = get_context()
         md = get_metadata()
         q = q.contiguous()
-        k = k.contiguous()
-        v = v.contiguous()
+        kv_rows = isinstance(v, ops.KvRows)
+        if kv_rows and ctx.is_full:
+            raise RuntimeError("KvRows is for sparse steps; a full step takes the dense k and v")
+        if not kv_rows:
+            k = k.contiguous()
+            v = v.contiguous()
 
         if ctx.is_full:
             o = ops.flash_attn_varlen_func(q, k, v, ctx.cu_seqlens_q, ctx.cu_seqlens_k, ctx.max_seqlen_q,
@@ -73,7 +80,8 @@ class Attention(nn.Module):
             idx_k64, idx_k32 = ctx.idx_salient_row_k, ctx.idx_salient_row_k_i32
         else:
             idx_k64, idx_k32 = idx_q, idx_q32
-        Tq, Tk, B = q.shape[0], k.shape[0], seq_ids.numel()
+        Tq, B = q.shape[0], seq_ids.numel()
+        Tk = int(ctx.total_seqlen_k or ctx.cu_seqlens_k_cpu[-1]) if kv_rows else k.shape[0]
         key = (Tq, Tk, B, q_pruned, ctx.max_seqlen_k)
         bufs = self._bufs
         if bufs is None or bufs.key != key:
@@ -83,7 +91,8 @@ class Attention(nn.Module):
         # column-sparse attention + stats + tau test with the context cache updated in place
         # (:107-145, :153/:168), and compaction of the next salient set (:147-173)
         ops.sparse_attention_step(
-            bufs, q, k, self.v_cache._slab, self.v_cache.seq_start_gpu, v.view(n, self.num_kv_heads, self.head_dim),
+            bufs, q, k, self.v_cache._slab, self.v_cache.seq_start_gpu,
+            v if kv_rows else v.view(n, self.num_kv_heads, self.head_dim),
             self.context_cache._slab, self.context_cache.seq_start_gpu, seq_ids, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
             ctx.cu_promptlens if q_pruned else None, ctx.max_seqlen_q, ctx.max_seqlen_k, Tk, n, ctx.max_salientlen,
             ctx.cu_salientlens, idx_q32, idx_k64, idx_k32, self.scale, self.threshold,

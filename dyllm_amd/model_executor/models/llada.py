@@ -168,16 +168,15 @@ class LLaDAAttention(nn.Module):
             self.k_cache.reset_full(k.flatten(1), md.running_seqs_tensor, seq_ids_list=md.running_seqs)
             o = self.attn(q, k, v)
         else:
-            # salient-row K/V projection as one gathered GEMM, then one epilogue pass: k_norm,
-            # RoPE and the K-cache scatter of k, the compact v of the step (llada.py:108-143)
+            # salient-row K/V projection as one gathered GEMM; its epilogue (k_norm, RoPE, the
+            # K-cache row write, llada.py:108-146) runs in the sparse step's first launch, which
+            # also takes the v rows from it, and attention reads K from the cache in place
             idx = ctx.idx_salient_row_i32
             kv = ops.linear(hidden, self.kv_proj, self.kv_bias, rows_idx=idx)
-            kidx = ctx.idx_salient_row_k if ctx.idx_salient_row_k is not None else ctx.idx_salient_row
-            v = self.k_cache.scatter_kv_rope(md.running_seqs_tensor, kidx, kv, self.num_kv_heads, positions,
-                                             self.rotary.cos, self.rotary.sin, idx,
-                                             None if kn is None else kn.weight, 1e-6 if kn is None else kn.eps)
-            k_full = self.k_cache.get_seqs(md.running_seqs_tensor, md.running_seqs)
-            o = self.attn(q, k_full.view(-1, self.num_kv_heads, self.head_dim), v)
+            v = self.k_cache.kv_rows(kv, self.num_kv_heads, positions, self.rotary.cos, self.rotary.sin, idx,
+                                     k_norm_weight=None if kn is None else kn.weight,
+                                     eps=1e-6 if kn is None else kn.eps)
+            o = self.attn(q, None, v)
         out = F.linear(o.flatten(1), self.o_proj)
         self.k_cache.finish(md.finished_seqs)
         return out

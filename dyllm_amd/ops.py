@@ -298,6 +298,52 @@ class StepBuffers:
                          self.host_meta, self.dest_rows if self.dest_starts is not None else None, self.dest_starts)
 
 
+class KvRows:
+    """The salient-row K/V projection output, handed to ``Attention.forward`` in place of ``v``
+    (llada.py:108-147): its epilogue -- optional k_norm, neox RoPE, the K-cache row write
+    (CacheManager.scatter_update) -- and the v rows are consumed by the sparse step's first launch
+    (dyllm_sparse_attention_step_kv), so no compact v or separate scatter pass is needed.
+
+    kv: [rows, >= 2 * num_kv_heads * 128] bf16 = [k | v]; row j of the salient list reads row
+    kv_rows[j] (None: j); positions[pos_idx[j]] (None: positions[j]) is its rotary position;
+    k_cache / k_seq_starts: the K cache slab and its per-sequence-id first rows."""
+
+    def __init__(self, kv, num_kv_heads, positions, cos, sin, k_cache, k_seq_starts, kv_rows=None, pos_idx=None,
+                 k_norm_weight=None, eps=1e-6):
+        _check(kv, "kv", torch.bfloat16, 2)
+        kv_size = num_kv_heads * 128
+        if kv.shape[1] < 2 * kv_size or kv.stride(1) != 1 or kv.stride(0) % 8:
+            raise RuntimeError("kv rows must hold k then v (2 * num_kv_heads * 128 contiguous values, 16-byte rows)")
+        for t, n in ((cos, "cos"), (sin, "sin")):
+            _check(t, n, torch.float32, 2)
+            if t.shape[1] != 64 or not t.is_contiguous():
+                raise RuntimeError(f"{n} must be a contiguous [max_position, 64] fp32 table")
+        if cos.shape != sin.shape:
+            raise RuntimeError("cos and sin tables must have the same shape")
+        if k_cache.dtype != torch.bfloat16 or k_cache.dim() != 2 or k_cache.shape[1] != kv_size:
+            raise RuntimeError("k_cache must be bf16 [rows, num_kv_heads * 128]")
+        if k_norm_weight is not None:
+            _check(k_norm_weight, "k_norm_weight", torch.bfloat16, 1)
+            if k_norm_weight.numel() != 128:
+                raise RuntimeError("k_norm_weight must have head_dim (128) entries")
+        self.kv, self.num_kv_heads = kv, num_kv_heads
+        self.positions = _i64(positions)
+        self.cos, self.sin = cos, sin
+        self.k_cache, self.k_seq_starts = k_cache, k_seq_starts
+        self.kv_rows = None if kv_rows is None else _i32(kv_rows)
+        self.pos_idx = None if pos_idx is None else _i32(pos_idx)
+        self.k_norm_weight, self.eps = k_norm_weight, float(eps)
+
+    def struct(self):
+        e = _lib.KvEpilogue()
+        e.kv, e.ld_kv, e.kv_rows = _ptr(self.kv), self.kv.stride(0), _ptr(self.kv_rows)
+        e.positions, e.pos_idx = _ptr(self.positions), _ptr(self.pos_idx)
+        e.cos_table, e.sin_table, e.max_position = _ptr(self.cos), _ptr(self.sin), self.cos.shape[0]
+        e.k_norm_weight, e.eps = _ptr(self.k_norm_weight), self.eps
+        e.k_cache, e.k_seq_starts = _ptr(self.k_cache), _ptr(self.k_seq_starts)
+        return e
+
+
 def sparse_attention_step(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_seq_starts, seq_ids, cu_seqlens_q,
                           cu_seqlens_k, cu_promptlens, max_seqlen_q, max_seqlen_k, total_k, n_sal, max_salientlen,
                           cu_salientlens, idx_q32, idx_k64, idx_k32, softmax_scale, threshold, k_start=None,
@@ -305,12 +351,22 @@ def sparse_attention_step(bufs, q, k, v_cache, v_seq_starts, v_new, c_cache, c_s
     """The sparse branch of Attention.forward in one native call (dyllm_sparse_attention_step).
     Results land in ``bufs`` (out / stats / mask and the next salient set, left on the device);
     with ``dest_seq_starts`` (another per-layer cache's start table) also the rows of the next
-    salient set in that cache (``bufs.dest_rows``)."""
+    salient set in that cache (``bufs.dest_rows``). ``v_new`` may be a ``KvRows`` (then ``k`` and
+    ``k_start`` are None: K is read from its cache after the epilogue, through
+    dyllm_sparse_attention_step_kv)."""
     Tq, H, D = q.shape
-    Hkv = v_new.shape[1] if v_new.dim() == 3 else v_cache.shape[1] // D
     bufs.host_meta.fill_(-1)   # "not written yet" for Compacted.host()
     bufs.dest_starts = dest_seq_starts
-    _lib.call("dyllm_sparse_attention_step", _ptr(q), _ptr(k), _ptr(k_start), _ptr(v_cache), _ptr(v_seq_starts),
+    if isinstance(v_new, KvRows):
+        if k is not None or k_start is not None:
+            raise RuntimeError("with KvRows, K comes from the K cache: k and k_start must be None")
+        epi = v_new.struct()
+        head = ("dyllm_sparse_attention_step_kv", ctypes.addressof(epi), _ptr(q), None, None)
+        Hkv, v_new = v_new.num_kv_heads, None
+    else:
+        head = ("dyllm_sparse_attention_step", _ptr(q), _ptr(k), _ptr(k_start))
+        Hkv = v_new.shape[1] if v_new.dim() == 3 else v_cache.shape[1] // D
+    _lib.call(*head, _ptr(v_cache), _ptr(v_seq_starts),
               _ptr(v_new), _ptr(c_cache), _ptr(c_seq_starts), _ptr(seq_ids), seq_ids.numel(), H, Hkv, D,
               _ptr(cu_seqlens_q), _ptr(cu_seqlens_k), _ptr(cu_promptlens), int(max_seqlen_q), int(max_seqlen_k), Tq,
               int(total_k), int(n_sal), int(max_salientlen), _ptr(cu_salientlens), _ptr(idx_q32), _ptr(idx_k64),

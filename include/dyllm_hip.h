@@ -135,9 +135,9 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
                                      float* cosine_stats, uint8_t* cosine_out, float threshold, void* workspace,
                                      size_t workspace_bytes, void* stream);
 
-/* The whole sparse branch of Attention.forward (attention.py:64-178) in one call (five
+/* The whole sparse branch of Attention.forward (attention.py:64-178) in one call (four
  * launches that leave the host back to back): dV + V-cache update of the salient keys
- * (v_new rows follow idx_k64), row-sparse attention of the salient queries against the cached
+ * (v_new rows follow the idx_k32 list), row-sparse attention of the salient queries against the cached
  * K/V, column-sparse attention with statistics and the tau test (context cache updated in place,
  * new rows also written to `out` [total_q, H, D]), and compaction of the next salient set into
  * next_* (capacity total_q; next_count[0] = its size, left on the device). K is packed
@@ -145,6 +145,9 @@ int dyllm_attention_colsparse_cached(const void* q, const void* k_cache, const i
  * context caches are addressed through their seq_start tables (indexed by seq_ids[b]).
  * cu_promptlens != NULL selects a Q-pruned step (Q rows are the response rows; the next set is
  * also produced in K space); otherwise Q space == K space and idx_k* = idx_q*.
+ * The salient rows of sequence b are list entries [cu_salientlens[b], cu_salientlens[b+1]), in any
+ * order, each key at most once per sequence; an entry whose K row lies outside its sequence is
+ * ignored.
  * next_dest_rows (optional, capacity total_q) receives, for every row of the next salient set, its row in
  * another per-layer cache whose sequence starts are dest_seq_starts (indexed by seq_ids[b]): the
  * scatter_update address of its K-space row, i.e. where the layer's FFN writes that row's output
@@ -170,12 +173,52 @@ int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_s
                                 int64_t* next_dest_rows, int32_t* host_meta, void* workspace, size_t workspace_bytes,
                                 void* stream);
 
+/* Salient-row K/V epilogue carried into dyllm_sparse_attention_step_kv: the reference's K/V
+ * projection tail (llada.py:103-146, dream.py:99-141, lladamoe.py:204-239: optional k_norm,
+ * rotary_embedding.py:40-54 neox RoPE, CacheManager.scatter_update of k, cache_kernels.cu:388-426)
+ * and the v rows Attention.forward receives. Row j of the salient list reads kv row
+ * kv_rows[j] (NULL: j) = [k | v] (2 * num_kv_heads * 128 bf16 values, ld_kv apart) and position
+ * positions[pos_idx[j]] (pos_idx NULL: positions[j]), clamped to [0, max_position). The rotated k
+ * goes to K-cache row k_seq_starts[seq_ids[b]] + (K row - cu_seqlens_k[b]). */
+typedef struct dyllm_kv_epilogue {
+  const void* kv;
+  int64_t ld_kv;
+  const int32_t* kv_rows;
+  const int64_t* positions;
+  const int32_t* pos_idx;
+  const float* cos_table;      /* fp32 [max_position, 64] */
+  const float* sin_table;
+  int max_position;
+  const void* k_norm_weight;   /* optional bf16 [128] */
+  float eps;
+  void* k_cache;               /* bf16 rows of num_kv_heads * 128 */
+  const int64_t* k_seq_starts;
+} dyllm_kv_epilogue;
+
+/* dyllm_sparse_attention_step with the K/V epilogue fused into its first launch (the reference's
+ * scatter_kv + Attention.forward, llada.py:136-147 + attention.py:64-178): k, k_start and v_new
+ * must be NULL; K is read from kv_epilogue->k_cache through k_seq_starts (after the salient rows
+ * were rotated into it) and v from the kv rows. Same outputs otherwise. */
+int dyllm_sparse_attention_step_kv(const dyllm_kv_epilogue* kv_epilogue, const void* q, const void* k,
+                                   const int64_t* k_start, void* v_cache, const int64_t* v_seq_starts,
+                                   const void* v_new, void* c_cache, const int64_t* c_seq_starts,
+                                   const int64_t* seq_ids, int batch, int num_heads, int num_kv_heads, int head_dim,
+                                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                   const int32_t* cu_promptlens, int max_seqlen_q, int max_seqlen_k, int64_t total_q,
+                                   int64_t total_k, int num_salient, int max_salientlen,
+                                   const int32_t* cu_salientlens, const int32_t* idx_q32, const int64_t* idx_k64,
+                                   const int32_t* idx_k32, float softmax_scale, float threshold, void* out,
+                                   float* cosine_stats, uint8_t* cosine_out, int64_t* next_idx64, int32_t* next_idx32,
+                                   int64_t* next_idx_k64, int32_t* next_idx_k32, int32_t* next_cu_salientlens,
+                                   int32_t* next_count, const int64_t* dest_seq_starts, int64_t* next_dest_rows,
+                                   int32_t* host_meta, void* workspace, size_t workspace_bytes, void* stream);
+
 /* The same step as dyllm_sparse_attention_step without the workspace arguments: no counterpart
  * in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc): the workspace is a library-owned device
  * array of dyllm_sparse_step_scratch_bytes() (64 MiB) per GPU, held until the process ends.
  * Calls whose dyllm_sparse_step_workspace_bytes(...) exceeds it fail with an error (config 1,
- * 920 salient rows, needs about 18 MiB). The array keeps the last call's contents; every call on
+ * 920 salient rows, needs about 10 MiB). The array keeps the last call's contents; every call on
  * one GPU shares it, so calls that overlap on one GPU (concurrent streams or threads) race.
  * Allocates nothing: no hipMalloc / hipFree, no library allocation. */
 size_t dyllm_sparse_step_scratch_bytes(void);

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     assert len(names) >= 25
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/dyllm_hip.h but not exported"
-    assert lib.dyllm_abi_version() == 3
+    assert lib.dyllm_abi_version() == 4
 
 
 def _ctype_of(param):
@@ -136,3 +136,20 @@ def test_pinned_salient_count_poll(monkeypatch):
     stale = ops.Compacted(None, None, None, None, None, host_meta=torch.tensor([5, 0, -1, 5], dtype=torch.int32))
     with pytest.raises(RuntimeError, match="not written"):
         stale.host()
+
+
+def test_kv_epilogue_struct_matches_header():
+    """The ctypes mirror of dyllm_kv_epilogue has the header's fields, in order, with the same
+    C types (a mismatch shifts every later field and hands kernels wrong pointers)."""
+    import ctypes
+
+    from dyllm_amd import _lib
+
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    body = re.search(r"typedef struct dyllm_kv_epilogue \{(.*?)\} dyllm_kv_epilogue;", text, flags=re.S).group(1)
+    fields = [f.strip() for f in body.split(";") if f.strip()]
+    assert len(fields) == len(_lib.KvEpilogue._fields_)
+    for decl, (name, ctype) in zip(fields, _lib.KvEpilogue._fields_):
+        assert decl.split()[-1].lstrip("*") == name
+        assert _ctype_of(decl) is ctype, f"{decl}: bound as {ctype.__name__}"
+    assert ctypes.sizeof(_lib.KvEpilogue) == 96

@@ -72,8 +72,8 @@ def test_noalloc_step_refuses_oversize(dev):
 
     lib = _lib.load()
     cap = lib.dyllm_sparse_step_scratch_bytes()
-    # config-1 shape with every response row salient needs more than the scratch array holds
-    need = lib.dyllm_sparse_step_workspace_bytes(8, 32, 32, D, 6144, 8192, 1024, 6144)
+    # config-4 shape (2 x 8192 rows, refresh) with every row salient needs more than the scratch holds
+    need = lib.dyllm_sparse_step_workspace_bytes(2, 32, 32, D, 16384, 16384, 8192, 16384)
     assert need > cap
     c = _case(dev, 7, 1, 16, 48, 2, 2, 4, True)
     with pytest.raises(RuntimeError, match="scratch"):
