@@ -345,19 +345,22 @@ static int sparse_step(const dyllm_kv_epilogue* epi, const void* q, const void* 
                   "host_meta must be pinned host memory (hipHostMalloc)");
     host_meta_dev = static_cast<int32_t*>(p);
   }
+  DYLLM_REQUIRE(next_dest_rows == nullptr || dest_seq_starts != nullptr, "next_dest_rows needs dest_seq_starts");
   const int64_t kv_size = int64_t(num_kv_heads) * head_dim;
   const size_t n = size_t(num_salient);
   char* ws = static_cast<char*>(workspace);
   uint16_t* dv = reinterpret_cast<uint16_t*>(ws);
   ws += align256(n * kv_size * 2);
-  int32_t* block_counts = reinterpret_cast<int32_t*>(ws);  // salient rows per 256-row block
-  ws += align256(size_t(cdiv(total_q, 256)) * 4);
+  int32_t* flags = reinterpret_cast<int32_t*>(ws);  // compaction look-back: salient rows + 1 per 256-row block
+  const int nflags = int(reduce_compact_blocks(total_q));
+  ws += align256(size_t(nflags) * 4);
   float* part = reinterpret_cast<float*>(ws);
   const bool q_pruned = cu_promptlens != nullptr;
   const int nblk = int(cdiv(max_seqlen_k, 64));
 
-  // 1. per salient row: [K/V epilogue], dV, V-cache update (attention.py:67-74, 89-96; llada.py:103-146)
-  if (num_salient > 0) {
+  // 1. per salient row: [K/V epilogue], dV, V-cache update (attention.py:67-74, 89-96; llada.py:103-146);
+  // workgroup 0 also clears the compaction's look-back flags
+  {
     StepRowsArgs ra{};
     ra.n = num_salient;
     ra.B = batch;
@@ -385,6 +388,8 @@ static int sparse_step(const dyllm_kv_epilogue* epi, const void* q, const void* 
       ra.k_seq_starts = epi->k_seq_starts;
     }
     ra.dv = dv;
+    ra.zero = flags;
+    ra.nzero = nflags;
     if (int rc = launch_step_rows(ra, s)) return rc;
   }
   // 2. row-sparse attention of the salient queries vs the full cached K/V (attention.py:76-87),
@@ -434,14 +439,12 @@ static int sparse_step(const dyllm_kv_epilogue* epi, const void* q, const void* 
   }
   if (int rc = timed_attention_step(rs, rs_rows, cs, max_seqlen_q, s)) return rc;
   // 3. statistics reduction, tau test and compaction of the next salient set (attention.py:141-173)
-  if (int rc = launch_reduce_stats(part, cosine_stats, cosine_out, total_q, num_heads, threshold, block_counts, s))
-    return rc;
-  DYLLM_REQUIRE(next_dest_rows == nullptr || dest_seq_starts != nullptr, "next_dest_rows needs dest_seq_starts");
   CompactDest dd{};
   if (next_dest_rows) dd = CompactDest{dest_seq_starts, seq_ids, cu_seqlens_k, next_dest_rows};
-  return launch_compact_blocks(cosine_out, total_q, block_counts, cu_seqlens_q, batch, cu_promptlens, next_idx64,
-                               next_idx32, q_pruned ? next_idx_k64 : nullptr, q_pruned ? next_idx_k32 : nullptr,
-                               next_cu_salientlens, next_count, host_meta_dev, s, dd);
+  return launch_reduce_compact(part, cosine_stats, cosine_out, total_q, num_heads, threshold, flags, cu_seqlens_q, batch,
+                               cu_promptlens, next_idx64, next_idx32, q_pruned ? next_idx_k64 : nullptr,
+                               q_pruned ? next_idx_k32 : nullptr, next_cu_salientlens, next_count, host_meta_dev, s,
+                               dd);
 }
 
 int dyllm_sparse_attention_step(const void* q, const void* k, const int64_t* k_start, void* v_cache,

@@ -95,6 +95,14 @@ int launch_compact_blocks(const uint8_t* mask, int64_t T, const int32_t* block_c
                           const int32_t* cu_prompt, int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32,
                           int32_t* cu_sal, int32_t* count, int32_t* host_meta, hipStream_t s,
                           const CompactDest& dest = CompactDest{});
+// statistics reduction + tau test + compaction of the native step in one launch (look-back over
+// per-workgroup counts). flags: reduce_compact_blocks(T) int32 words, zero before the launch.
+constexpr int32_t kCompactLookbackFailed = -2;
+int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
+                          int32_t* flags, const int32_t* cu_q, int B, const int32_t* cu_prompt, int64_t* idx64,
+                          int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
+                          int32_t* host_meta, hipStream_t s, const CompactDest& dest);
+int64_t reduce_compact_blocks(int64_t T);
 int launch_fused_offset(const int32_t* idxs, const int32_t* num_idxs, const int32_t* cu_prompt,
                         const int32_t* cu_sal, int groups, int64_t* out, int64_t cap, hipStream_t s);
 

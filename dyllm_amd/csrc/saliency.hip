@@ -395,6 +395,162 @@ __global__ __launch_bounds__(kReduceRows) void compact_blocks_kernel(
   if (host_meta && wrote) __threadfence_system();
 }
 
+// ---- statistics reduction + tau test + compaction in one launch (native step) ---------------
+// Workgroup w reduces the statistics of rows [256w, 256w+256) exactly as reduce_stats_kernel,
+// publishes its salient count (count + 1 in flags[w]; 0 = not yet) with a device-scope atomic
+// store, then looks back: wavefront 0 reads flags[0..w) (one lane per workgroup, device-scope
+// atomic loads, each lane polling until its flag is set) and sums them into the workgroup's base;
+// then it places its own rows as compact_blocks_kernel does. Only counts cross workgroups, inside
+// the atomics themselves, so no fence orders any other data. Workgroups are dispatched in index
+// order, so every flag a workgroup waits for belongs to a workgroup that is running or done; the
+// poll is still bounded (kLookbackPolls per flag): a workgroup that exhausts it writes nothing, and
+// the last one then reports kCompactLookbackFailed as the count.
+constexpr int kLookbackPolls = 1 << 20;
+
+__global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
+    const float* __restrict__ part, float* __restrict__ stats, uint8_t* __restrict__ mask, int64_t T, int H,
+    float tau, int32_t* __restrict__ flags, const int32_t* __restrict__ cu_q, int B,
+    const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64, int32_t* __restrict__ idx32,
+    int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32, int32_t* __restrict__ cu_sal,
+    int32_t* __restrict__ count, int32_t* __restrict__ host_meta, CompactDest dd) {
+  constexpr int NWV = kReduceRows / 64;
+  __shared__ float red[4][3][kReduceRows];
+  __shared__ int wtot[NWV];
+  __shared__ int pre[kReduceRows + 1];
+  __shared__ int base_sh, fail_sh;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tl = tid % kReduceRows, hq = tid / kReduceRows;
+  const int nblk = gridDim.x, blk = blockIdx.x;
+  const int64_t t = int64_t(blk) * kReduceRows + tl;
+  // 1. statistics of the block's rows: four quarters of the heads, summed in quarter order
+  const int hpq = (H + 3) / 4;
+  const int h0 = hq * hpq, h1 = (h0 + hpq < H) ? h0 + hpq : H;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+  if (t < T) {
+#pragma unroll 4
+    for (int h = h0; h < h1; ++h) {
+      s0 += part[(int64_t(h) * 3 + 0) * T + t];
+      s1 += part[(int64_t(h) * 3 + 1) * T + t];
+      s2 += part[(int64_t(h) * 3 + 2) * T + t];
+    }
+  }
+  red[hq][0][tl] = s0;
+  red[hq][1][tl] = s1;
+  red[hq][2][tl] = s2;
+  __syncthreads();
+  bool sal = false;
+  if (hq == 0 && t < T) {
+    s0 = ((red[0][0][tl] + red[1][0][tl]) + red[2][0][tl]) + red[3][0][tl];
+    s1 = ((red[0][1][tl] + red[1][1][tl]) + red[2][1][tl]) + red[3][1][tl];
+    s2 = ((red[0][2][tl] + red[1][2][tl]) + red[2][2][tl]) + red[3][2][tl];
+    stats[3 * t] = s0;
+    stats[3 * t + 1] = s1;
+    stats[3 * t + 2] = s2;
+    sal = tau_cos(s0, s1, s2) < tau;
+    mask[t] = sal;
+  }
+  const unsigned long long bal = __ballot(sal);
+  const int before = __popcll(bal & ((1ull << lane) - 1));
+  if (hq == 0 && lane == 0) wtot[wid] = __popcll(bal);
+  __syncthreads();
+  int woff = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < NWV; ++w) {
+    woff += (w < wid) ? wtot[w] : 0;
+    total += wtot[w];
+  }
+  // 2. publish, 3. look back
+  if (tid == 0) __hip_atomic_store(&flags[blk], total + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (wid == 0) {
+    int base = 0;
+    bool ok = true;
+    for (int i0 = 0; i0 < blk; i0 += 64) {
+      const int i = i0 + lane;
+      int v = 1;   // lanes past the last earlier workgroup add 0
+      if (i < blk) {
+        v = __hip_atomic_load(&flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int p = 0; v == 0 && p < kLookbackPolls; ++p) {
+          __builtin_amdgcn_s_sleep(2);
+          v = __hip_atomic_load(&flags[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      ok = ok && __ballot(v == 0) == 0;
+      int c = v > 0 ? v - 1 : 0;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+      base += c;
+    }
+    if (lane == 0) {
+      base_sh = base;
+      fail_sh = ok ? 0 : 1;
+    }
+  }
+  if (hq == 0) pre[tl] = woff + before;
+  if (tid == 0) pre[kReduceRows] = total;
+  __syncthreads();
+  const int base = base_sh;
+  if (fail_sh) {
+    if (blk == nblk - 1 && tid == 0) {
+      count[0] = kCompactLookbackFailed;
+      if (host_meta) {
+        host_meta[0] = kCompactLookbackFailed;
+        __threadfence_system();
+      }
+    }
+    return;
+  }
+  // 4. placement of the block's salient rows (compact_blocks_kernel)
+  if (sal) {
+    const int pos = base + woff + before;
+    idx64[pos] = t;
+    if (idx32) idx32[pos] = int32_t(t);
+    if (idx_k || dd.dest) {
+      const int seg = find_segment(cu_q, B + 1, t);
+      const int64_t kk = idx_k ? t + cu_prompt[seg + 1] : t;   // K-space row (refresh: Q space == K space)
+      if (idx_k) {
+        idx_k[pos] = kk;
+        if (idx_k32) idx_k32[pos] = int32_t(kk);
+      }
+      if (dd.dest) dd.dest[pos] = dd.dest_starts[dd.seq_ids[seg]] + (kk - dd.cu_k[seg]);
+    }
+  }
+  bool wrote = false;
+  const int64_t lo = int64_t(blk) * kReduceRows;
+  for (int b = tid; b <= B; b += kCompactThreads) {
+    const int64_t p = cu_q[b];
+    const int owner = (p >= T) ? nblk - 1 : int(p / kReduceRows);
+    if (owner != blk) continue;
+    const int64_t local = p - lo;
+    const int v = base + (local >= kReduceRows ? total : pre[local]);
+    cu_sal[b] = v;
+    if (host_meta) host_meta[1 + b] = v;
+    wrote = true;
+  }
+  if (blk == nblk - 1 && tid == 0) {
+    count[0] = base + total;
+    if (host_meta) host_meta[0] = base + total;
+    wrote = true;
+  }
+  if (host_meta && wrote) __threadfence_system();
+}
+
+int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
+                          int32_t* flags, const int32_t* cu_q, int B, const int32_t* cu_prompt, int64_t* idx64,
+                          int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
+                          int32_t* host_meta, hipStream_t s, const CompactDest& dest) {
+  DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
+  DYLLM_REQUIRE(T >= 1 && T < (int64_t(1) << 31), "row count out of range");
+  DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
+  DYLLM_REQUIRE(dest.dest == nullptr || (dest.dest_starts && dest.seq_ids && dest.cu_k),
+                "cache rows need the cache's sequence starts, the sequence ids and cu_seqlens_k");
+  reduce_compact_kernel<<<unsigned(cdiv(T, kReduceRows)), kCompactThreads, 0, s>>>(
+      part, stats, mask, T, H, tau, flags, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count, host_meta,
+      dest);
+  return check_launch("reduce_compact_kernel");
+}
+
+int64_t reduce_compact_blocks(int64_t T) { return cdiv(T, kReduceRows); }
+
 int launch_compact_blocks(const uint8_t* mask, int64_t T, const int32_t* block_counts, const int32_t* cu_q, int B,
                           const int32_t* cu_prompt, int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32,
                           int32_t* cu_sal, int32_t* count, int32_t* host_meta, hipStream_t s,

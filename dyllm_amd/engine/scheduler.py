@@ -9,6 +9,7 @@ from __future__ import annotations
 from collections import deque
 from typing import Deque, List, Tuple
 
+import numpy as np
 import torch
 
 from ..config import Config
@@ -26,6 +27,8 @@ class Scheduler:
         self.full: Deque[Sequence] = deque()
         self.sparse: Deque[Sequence] = deque()
         self.finished: List[int] = []
+        self._host_buf = None   # host staging of the sampler output (postprocess)
+        self._host_dev = None
 
     def is_finished(self) -> bool:
         return not self.full and not self.sparse
@@ -87,32 +90,51 @@ class Scheduler:
         if seq in queue:
             queue.remove(seq)
 
+    def _to_host(self, counts: torch.Tensor, tokens: torch.Tensor, positions: torch.Tensor):
+        """The sampler's [B] counts and [B, W] tokens / positions as numpy arrays, through one
+        reusable host staging buffer: three asynchronous copies into it, then a single wait
+        (pinned when the inputs live on the GPU)."""
+        B = counts.numel()
+        W = tokens.shape[-1] if tokens.dim() == 2 else 0
+        need = B * (1 + 2 * W)
+        dev = tokens.device
+        buf = self._host_buf
+        if buf is None or buf.numel() < need or self._host_dev != dev:
+            buf = torch.empty(max(need, 64), dtype=torch.int64, pin_memory=dev.type == "cuda")
+            self._host_buf, self._host_dev = buf, dev
+        views = (buf[:B], buf[B: B + B * W].view(B, W), buf[B + B * W: need].view(B, W))
+        for dst, src in zip(views, (counts.reshape(B), tokens.reshape(B, W), positions.reshape(B, W))):
+            dst.copy_(src, non_blocking=True)
+        if dev.type == "cuda":
+            torch.cuda.current_stream(dev).synchronize()
+        return tuple(v.numpy() for v in views)
+
+    def _spent(self, seq: Sequence) -> bool:
+        """Step budget used up (fixed-count unmasking) or every answer token generated."""
+        if seq.confidence_threshold is None and seq.processed_steps == seq.num_steps:
+            return True
+        return seq.num_completion_tokens >= seq.max_new_tokens
+
     def postprocess(self, seqs: List[Sequence], selected_positions: torch.Tensor, selected_tokens: torch.Tensor,
                     selected_counts: torch.Tensor) -> List[int]:
-        """Write the sampled tokens back and retire finished sequences (scheduler.py:89-145).
-        One device->host copy carries counts, tokens and positions."""
+        """Commit one step's sampled tokens and retire finished sequences (the contract of
+        scheduler.py:89-145). A sequence finishes when it samples EOS with no mask token before
+        it (unless it ignores EOS), when its step budget is spent, or when its answer is complete.
+        With device-built sparse steps the same tokens are also committed on the device
+        (unmask_step_kernel); this host copy keeps the mirrors that finish detection and the next
+        step's launch sizes read."""
+        counts, toks, poss = self._to_host(selected_counts, selected_tokens, selected_positions)
         finished: List[int] = []
-        B = selected_counts.size(0)
-        L = selected_tokens.size(1) if selected_tokens.dim() == 2 else 0
-        packed = torch.cat([selected_counts.reshape(-1).long(), selected_tokens.reshape(-1).long(),
-                            selected_positions.reshape(-1).long()]).cpu().tolist()
-        counts = packed[:B]
-        toks = packed[B: B + B * L]
-        poss = packed[B + B * L:]
-        for b, seq in enumerate(seqs):
-            n = counts[b]
+        for seq, n, tok_row, pos_row in zip(seqs, counts.tolist(), toks, poss):
             if n > 0:
-                tok = toks[b * L: b * L + n]
-                pos = poss[b * L: b * L + n]
+                tok, pos = tok_row[:n], pos_row[:n]
                 seq.update_token(pos, tok)
                 seq.update_block_idx()
-                if self.eos in tok:
-                    eos_pos = pos[tok.index(self.eos)]
-                    if self.eos_and_done(seq, eos_pos) and not seq.ignore_eos:
-                        self._finish(seq, finished)
-                        continue
-            steps_done = seq.confidence_threshold is None and seq.processed_steps == seq.num_steps
-            if steps_done or seq.num_completion_tokens >= seq.max_new_tokens:
+                eos_at = np.flatnonzero(tok == self.eos)
+                if eos_at.size and not seq.ignore_eos and self.eos_and_done(seq, int(pos[eos_at[0]])):
+                    self._finish(seq, finished)
+                    continue
+            if self._spent(seq):
                 self._finish(seq, finished)
         get_metadata().finished_seqs = finished
         self.finished.extend(finished)

@@ -204,6 +204,16 @@ def saliency_stats(c_new, c_old, threshold):
 
 
 _HOST_META_TIMEOUT_S = 60.0
+# count written by the step's compaction when its bounded look-back over the earlier workgroups'
+# counts ran out (kCompactLookbackFailed in the library)
+_COMPACT_LOOKBACK_FAILED = -2
+
+
+def _check_count(n):
+    if n == _COMPACT_LOOKBACK_FAILED:
+        raise RuntimeError("salient compaction failed: a workgroup's look-back over the earlier counts did not "
+                           "complete (the next salient set was not written)")
+    return n
 
 
 class Compacted:
@@ -228,7 +238,7 @@ class Compacted:
             deadline = None
             while True:
                 h = hm.tolist()
-                if min(h) >= 0:
+                if min(h) >= 0 or h[0] == _COMPACT_LOOKBACK_FAILED:
                     break
                 now = time.monotonic()
                 if deadline is None:
@@ -240,10 +250,11 @@ class Compacted:
                     raise RuntimeError("salient count was not written by the compaction kernel")
         else:
             h = torch.cat([self.count, self.cu_salientlens]).cpu().tolist()
+        _check_count(h[0])
         return h[0], h[1:]
 
     def n(self) -> int:
-        return int(self.count.item())
+        return _check_count(int(self.count.item()))
 
     def trimmed(self):
         n = self.n()

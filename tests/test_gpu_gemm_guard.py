@@ -1,0 +1,67 @@
+"""GPU checks of two details of the gathered GEMM (csrc/gemm.hip) through the C ABI:
+
+* negative gather ids are padding: the A row is not read (row 0 stands in) and the output row is
+  not written, in the direct epilogue and in the split-K reduction (gemm_tile_rows, the store
+  epilogue and gemm_partial_reduce_kernel); every other row equals the fp32 oracle within the bf16
+  bound (max abs 2e-2, mean rel 1e-3);
+* the SwiGLU epilogue's SiLU (hardware reciprocal instead of an IEEE division) stays within one
+  bf16 ulp of bf16(g / (1 + exp(-g))) in fp32 over a sweep of g across the tails and around 0
+  (activations.py:11-14 computes silu(g) * u in fp32 and rounds once)."""
+import numpy as np
+import pytest
+import torch
+
+from tests._tol import assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+@pytest.mark.parametrize("M,N,K", [(40, 256, 512), (300, 1024, 12288)])
+def test_negative_gather_ids_are_padding(dev, M, N, K):
+    from dyllm_amd import _lib, ops
+
+    print(f"[gemm guard] M={M} N={N} K={K}", flush=True)
+    g = torch.Generator().manual_seed(M)
+    src_rows = 2 * M
+    x = torch.randn(src_rows, K, generator=g).to(BF)
+    w = (torch.randn(N, K, generator=g) * K ** -0.5).to(BF)
+    ids = torch.randint(0, src_rows, (M,), generator=g, dtype=torch.int32)
+    neg = torch.arange(M) % 7 == 3
+    ids[neg] = -1 - torch.arange(int(neg.sum()), dtype=torch.int32)   # -1, -2, ...
+    sentinel = torch.full((M, N), 7.0).to(BF)
+    out = sentinel.to(dev)
+    xd, wd, idd = x.to(dev), w.to(dev), ids.to(dev)
+    lib = _lib.load()
+    ws_bytes = lib.dyllm_linear_workspace_bytes(M, 0, N, K)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    _lib.call("dyllm_linear", xd.data_ptr(), xd.stride(0), idd.data_ptr(), M, None, 0, wd.data_ptr(), N, K, None,
+              out.data_ptr(), ws.data_ptr(), ws_bytes, ops._stream())
+    got = out.cpu()
+    assert torch.equal(got[neg], sentinel[neg]), "a padding row was written"
+    keep = ~neg
+    want = (x[ids[keep].long()].float() @ w.float().t()).to(BF)
+    assert_bf16_close(got[keep], want, what="gathered GEMM rows")
+
+
+def test_swiglu_silu_within_one_ulp(dev):
+    from dyllm_amd import ops
+
+    hidden, inter = 256, 512
+    M = hidden
+    # bf16 gate values: the tails (|g| up to 90, where exp(-g) over/underflows) and a dense
+    # neighbourhood of 0, M * inter of them
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([np.linspace(-90, 90, 40_000), np.linspace(-4, 4, 60_000), rng.normal(0, 3, 31_072)])
+    g = torch.from_numpy(vals[: M * inter].astype(np.float32)).to(BF).view(inter, M)
+    # A row m = e_m, so gate[m, n] = w_gate[n, m] and up[m, n] = w_up[n, m] = 1 exactly
+    w = torch.cat([g, torch.ones(inter, M, dtype=BF)], dim=0).contiguous()
+    x = torch.eye(M, dtype=torch.float32).to(BF)
+    h = ops.ffn_gate_up(x.to(dev), w.to(dev)).cpu().float()
+    gf = g.t().float()
+    want = (gf / (1.0 + torch.exp(-gf))).to(BF).float()
+    # one bf16 ulp of the reference value (2^(e - 7) for |v| in [2^e, 2^(e+1)))
+    ulp = torch.ldexp(torch.ones_like(want), torch.frexp(want.abs().clamp_min(2.0 ** -126))[1] - 8)
+    diff = (h - want).abs()
+    bad = diff > ulp
+    assert not bad.any(), f"{int(bad.sum())} values differ by more than one bf16 ulp, e.g. g={gf[bad][:5].tolist()}"

@@ -136,6 +136,10 @@ def test_pinned_salient_count_poll(monkeypatch):
     stale = ops.Compacted(None, None, None, None, None, host_meta=torch.tensor([5, 0, -1, 5], dtype=torch.int32))
     with pytest.raises(RuntimeError, match="not written"):
         stale.host()
+    # the compaction's bounded look-back ran out: its count is the failure code, reported at once
+    failed = ops.Compacted(None, None, None, None, None, host_meta=torch.tensor([-2, 0, -1, -1], dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="look-back"):
+        failed.host()
 
 
 def test_kv_epilogue_struct_matches_header():
