@@ -35,6 +35,41 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 }
 __device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
+// one head's rotation pairs (d, d + 64) for d = d0 .. d0 + 7 of k (x1 = k[d], x2 = k[d + 64]) ->
+// optional per-head RMSNorm (the head's sum of squares reduced over its 8 threads) -> neox
+// rotation -> 16-byte stores at crow[d0] and crow[d0 + 64]
+__device__ __forceinline__ void rope_k_values(float (&x1)[8], float (&x2)[8], const float (&c)[8], const float (&s)[8],
+                                              const uint16_t* __restrict__ k_norm, float eps, int d0,
+                                              uint16_t* __restrict__ crow) {
+  constexpr int D = 128, HALF = 64;
+  if (k_norm) {
+    float w1[8], w2[8];
+    unpack8(*reinterpret_cast<const uint4*>(k_norm + d0), w1);
+    unpack8(*reinterpret_cast<const uint4*>(k_norm + d0 + HALF), w2);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    ss += __shfl_xor(ss, 4, 64);
+    const float r = rsqrtf(ss / float(D) + eps);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x1[i] = bf16_round(__fmul_rn(bf16_round(x1[i] * r), w1[i]));
+      x2[i] = bf16_round(__fmul_rn(bf16_round(x2[i] * r), w2[i]));
+    }
+  }
+  float y1[8], y2[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    // rounded products, then the sum (no contraction): the eager fp32 formula
+    y1[i] = mul_sub_mul_rn(x1[i], c[i], x2[i], s[i]);
+    y2[i] = mul_add_mul_rn(x2[i], c[i], x1[i], s[i]);
+  }
+  *reinterpret_cast<uint4*>(crow + d0) = pack8(y1);
+  *reinterpret_cast<uint4*>(crow + d0 + HALF) = pack8(y2);
+}
+
 // k of one row (Hkv heads of 128) -> optional per-head RMSNorm -> neox rotation at pos -> crow.
 // Thread t of the 256-thread workgroup takes head t / 8 (heads beyond 32 loop) and the rotation
 // pairs (d, d + 64), d = 8 (t % 8) .. 8 (t % 8) + 7.
@@ -50,38 +85,11 @@ __device__ __forceinline__ void rope_k_row(const uint16_t* __restrict__ krow, ui
   *reinterpret_cast<float4*>(c + 4) = *reinterpret_cast<const float4*>(cos_t + pos * HALF + d0 + 4);
   *reinterpret_cast<float4*>(s) = *reinterpret_cast<const float4*>(sin_t + pos * HALF + d0);
   *reinterpret_cast<float4*>(s + 4) = *reinterpret_cast<const float4*>(sin_t + pos * HALF + d0 + 4);
-  float w1[8], w2[8];
-  if (k_norm) {
-    unpack8(*reinterpret_cast<const uint4*>(k_norm + d0), w1);
-    unpack8(*reinterpret_cast<const uint4*>(k_norm + d0 + HALF), w2);
-  }
   for (int h = t >> 3; h < Hkv; h += 32) {
     float x1[8], x2[8];
     unpack8(*reinterpret_cast<const uint4*>(krow + h * D + d0), x1);
     unpack8(*reinterpret_cast<const uint4*>(krow + h * D + d0 + HALF), x2);
-    if (k_norm) {
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss += x1[i] * x1[i] + x2[i] * x2[i];
-      ss += __shfl_xor(ss, 1, 64);
-      ss += __shfl_xor(ss, 2, 64);
-      ss += __shfl_xor(ss, 4, 64);
-      const float r = rsqrtf(ss / float(D) + eps);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        x1[i] = bf16_round(__fmul_rn(bf16_round(x1[i] * r), w1[i]));
-        x2[i] = bf16_round(__fmul_rn(bf16_round(x2[i] * r), w2[i]));
-      }
-    }
-    float y1[8], y2[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      // rounded products, then the sum (no contraction): the eager fp32 formula
-      y1[i] = mul_sub_mul_rn(x1[i], c[i], x2[i], s[i]);
-      y2[i] = mul_add_mul_rn(x2[i], c[i], x1[i], s[i]);
-    }
-    *reinterpret_cast<uint4*>(crow + h * D + d0) = pack8(y1);
-    *reinterpret_cast<uint4*>(crow + h * D + d0 + HALF) = pack8(y2);
+    rope_k_values(x1, x2, c, s, k_norm, eps, d0, crow + h * D);
   }
 }
 
@@ -116,12 +124,36 @@ __global__ __launch_bounds__(256) void kv_rope_scatter_kernel(KvRopeArgs a) {
 // One 256-thread workgroup per salient list entry j (StepRowsArgs). Every wavefront derives the
 // entry's sequence and its key's rank among the sequence's salient keys itself (ballot counts over
 // the sequence's list segment, a few hundred entries at most), so no workgroup waits on another.
+// The loads that depend on j alone (the new v row, the k row, its position and rotary table rows)
+// are issued before that index chain, so its round trips overlap them.
 __global__ __launch_bounds__(256) void step_rows_kernel(StepRowsArgs a) {
+  constexpr int D = 128, HALF = 64;
   const int j = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63;
   if (j == 0)
     for (int i = t; i < a.nzero; i += 256) a.zero[i] = 0;
   if (j >= a.n) return;
+  const uint16_t* src = a.kv ? a.kv + (a.kv_rows ? int64_t(a.kv_rows[j]) : int64_t(j)) * a.ld_kv : nullptr;
+  const uint4* nr = reinterpret_cast<const uint4*>(src ? src + a.kv_size : a.v_new + int64_t(j) * a.kv_size);
+  const int64_t n16 = a.kv_size / 8;
+  // the first two 16-byte pieces of this thread's part of the new v row (the rest, if any, later)
+  uint4 nv0 = make_uint4(0, 0, 0, 0), nv1 = make_uint4(0, 0, 0, 0);
+  if (t < n16) nv0 = nr[t];
+  if (t + 256 < n16) nv1 = nr[t + 256];
+  // k of head t / 8 (one head per thread group when Hkv <= 32, the common case)
+  const bool k_fast = src && a.Hkv <= 32;
+  const int h = t >> 3, d0 = (t & 7) * 8;
+  float x1[8], x2[8], c[8], sn[8];
+  if (k_fast && h < a.Hkv) {
+    const int64_t pos = clamp_pos(a.positions[a.pos_idx ? int64_t(a.pos_idx[j]) : int64_t(j)], a.max_position);
+    unpack8(*reinterpret_cast<const uint4*>(src + h * D + d0), x1);
+    unpack8(*reinterpret_cast<const uint4*>(src + h * D + d0 + HALF), x2);
+    *reinterpret_cast<float4*>(c) = *reinterpret_cast<const float4*>(a.cos + pos * HALF + d0);
+    *reinterpret_cast<float4*>(c + 4) = *reinterpret_cast<const float4*>(a.cos + pos * HALF + d0 + 4);
+    *reinterpret_cast<float4*>(sn) = *reinterpret_cast<const float4*>(a.sin + pos * HALF + d0);
+    *reinterpret_cast<float4*>(sn + 4) = *reinterpret_cast<const float4*>(a.sin + pos * HALF + d0 + 4);
+  }
+  // the sequence of entry j, its key, and the key's rank among the sequence's salient keys
   const int b = find_segment_wave(a.cu_sal, a.B + 1, j);
   const int64_t s0 = a.cu_sal[b], s1 = a.cu_sal[b + 1];
   const int64_t kbeg = a.cu_k[b], Lk = a.cu_k[b + 1] - kbeg;
@@ -139,29 +171,34 @@ __global__ __launch_bounds__(256) void step_rows_kernel(StepRowsArgs a) {
     rank += __popcll(__ballot(lt));
   }
   const int64_t sid = a.seq_ids[b];
-  const uint16_t* src = a.kv ? a.kv + (a.kv_rows ? int64_t(a.kv_rows[j]) : int64_t(j)) * a.ld_kv : nullptr;
-  const uint4* nr = reinterpret_cast<const uint4*>(src ? src + a.kv_size : a.v_new + int64_t(j) * a.kv_size);
   uint4* cr = reinterpret_cast<uint4*>(a.v_cache + (a.v_seq_starts[sid] + off) * a.kv_size);
   uint4* dr = reinterpret_cast<uint4*>(a.dv + (s0 + rank) * a.kv_size);
-  const int64_t n16 = a.kv_size / 8;
-  int64_t i = t;
-  for (; i + 256 < n16; i += 512) {   // both loads of a pair in flight before the stores
-    const uint4 o0 = cr[i], n0 = nr[i], o1 = cr[i + 256], n1 = nr[i + 256];
-    dr[i] = bf16x8_sub(n0, o0);
-    dr[i + 256] = bf16x8_sub(n1, o1);
-    cr[i] = n0;
-    cr[i + 256] = n1;
+  {
+    const uint4 o0 = t < n16 ? cr[t] : make_uint4(0, 0, 0, 0);
+    const uint4 o1 = t + 256 < n16 ? cr[t + 256] : make_uint4(0, 0, 0, 0);
+    if (t < n16) {
+      dr[t] = bf16x8_sub(nv0, o0);
+      cr[t] = nv0;
+    }
+    if (t + 256 < n16) {
+      dr[t + 256] = bf16x8_sub(nv1, o1);
+      cr[t + 256] = nv1;
+    }
   }
-  for (; i < n16; i += 256) {
+  for (int64_t i = t + 512; i < n16; i += 256) {   // v rows past 512 pieces (more than 32 kv heads)
     const uint4 o = cr[i], nw = nr[i];
     dr[i] = bf16x8_sub(nw, o);
     cr[i] = nw;
   }
-  if (src) {
+  if (!src) return;
+  uint16_t* crow = a.k_cache + (a.k_seq_starts[sid] + off) * a.kv_size;
+  if (!k_fast) {
     const int64_t pos = clamp_pos(a.positions[a.pos_idx ? int64_t(a.pos_idx[j]) : int64_t(j)], a.max_position);
-    rope_k_row(src, a.k_cache + (a.k_seq_starts[sid] + off) * a.kv_size, a.Hkv, pos, a.cos, a.sin, a.k_norm,
-               a.eps);
+    rope_k_row(src, crow, a.Hkv, pos, a.cos, a.sin, a.k_norm, a.eps);
+    return;
   }
+  if (h >= a.Hkv) return;
+  rope_k_values(x1, x2, c, sn, a.k_norm, a.eps, d0, crow + h * D);
 }
 
 int launch_step_rows(const StepRowsArgs& a, hipStream_t s) {
