@@ -1077,7 +1077,6 @@ int dyllm_fused_experts(const void* x, const int32_t* rows_idx, int64_t tokens, 
   DYLLM_NONNULL(topk_weights);
   DYLLM_NONNULL(topk_ids);
   DYLLM_NONNULL(out);
-  DYLLM_REQUIRE(rows_idx == nullptr, "fused_experts takes compacted tokens (gather them first)");
   DYLLM_REQUIRE(hidden % 64 == 0 && intermediate % 64 == 0, "hidden and intermediate must be multiples of 64");
   if (tokens <= 0) return 0;
   const size_t need = dyllm_fused_experts_workspace_bytes(tokens, top_k, num_experts, hidden, intermediate);
@@ -1101,9 +1100,10 @@ int dyllm_fused_experts(const void* x, const int32_t* rows_idx, int64_t tokens, 
   GemmArgs g{};
   g.A = static_cast<const uint16_t*>(x);
   g.lda = hidden;
-  g.a_rows = tokens;
+  g.a_rows = rows_idx ? 0 : tokens;   // a gathered source's row count is not known here
   g.a_ids = sorted;
   g.a_div = top_k;
+  g.a_map = rows_idx;                 // token t reads x row rows_idx[t]
   g.id_limit = S;
   g.W = static_cast<const uint16_t*>(w1);
   g.ldw = hidden;

@@ -94,6 +94,7 @@ __device__ __forceinline__ void gemm_tile_rows(const GemmArgs& g, int64_t M, int
       if (g.a_ids) {
         const int64_t id = g.a_ids[m];
         row = (id >= 0 && id < g.id_limit) ? id / g.a_div : 0;
+        if (g.a_map) row = g.a_map[row];
       }
     }
     rows[i] = row;

@@ -229,6 +229,7 @@ struct GemmArgs {
   int64_t a_rows;             // rows A holds, when known (0: unknown); A spans < 4 GiB either way
   const int32_t* a_ids;
   int a_div;
+  const int32_t* a_map;       // optional: A row of id = a_map[id / a_div] (else id / a_div)
   int64_t id_limit;
   const uint16_t* W;
   int64_t ldw;

@@ -28,23 +28,24 @@ class LLaDAMoESparseBlock(nn.Module):
         self.down_proj = _param(E, H, I, device=device, gen=gen)
         self.cache_update = MLPcache(H, device=device)
 
-    def experts(self, x, out=None, out_rows=None):
-        w, ids = ops.moe_gate(x, self.gate, self.top_k, renormalize=self.renormalize)
-        return ops.fused_experts(x, self.gate_up_proj, self.down_proj, w, ids, out=out, out_rows=out_rows)
+    def experts(self, x, out=None, out_rows=None, rows_idx=None):
+        w, ids = ops.moe_gate(x, self.gate, self.top_k, renormalize=self.renormalize, rows_idx=rows_idx)
+        return ops.fused_experts(x, self.gate_up_proj, self.down_proj, w, ids, out=out, out_rows=out_rows,
+                                 rows_idx=rows_idx)
 
     def forward(self, x):
         """Reference interface: x = gathered salient rows (sparse) or all rows (full)."""
         return self.cache_update(self.experts(x.contiguous()))
 
     def forward_salient(self, h_all, timing=None, lazy=False):
-        """Sparse step: route the salient rows of ``h_all`` and write the expert outputs
+        """Sparse step: route the salient rows of ``h_all`` (read in place by the router and the
+        first grouped GEMM, util.py:19-36's gather fused away) and write the expert outputs
         straight into the FFN cache rows."""
         ctx = get_context()
         md = get_metadata()
         cm = self.cache_update.cache_manager
-        x = ops.gather_rows_2D(h_all.contiguous(), ctx.idx_salient_row)
         dest = self.cache_update.dest_rows()
-        self.experts(x, out=cm._slab, out_rows=dest)
+        self.experts(h_all.contiguous(), out=cm._slab, out_rows=dest, rows_idx=ctx.idx_salient_row_i32)
         cm.finish(md.finished_seqs)
         return self.cache_update.gather_all(lazy)
 

@@ -755,15 +755,19 @@ def swiglu_ffn(x, w_gate_up, w_down, rows_idx=None, out=None, out_rows=None):
     return ffn_down(h, w_down, out, out_rows)
 
 
-def moe_gate(hidden_states, router_weight, top_k, renormalize=False):
-    """fp32 softmax top-k routing (fused_moe.py:375-408 without the DiffusionGemma extras)."""
+def moe_gate(hidden_states, router_weight, top_k, renormalize=False, rows_idx=None):
+    """fp32 softmax top-k routing (fused_moe.py:375-408 without the DiffusionGemma extras); with
+    ``rows_idx`` the tokens are rows rows_idx[t] of ``hidden_states``."""
     _check(hidden_states, "hidden_states", torch.bfloat16, 2)
+    if hidden_states.stride(1) != 1 or hidden_states.stride(0) != hidden_states.shape[1]:
+        raise RuntimeError("hidden_states must be contiguous")
     rw = router_weight.to(torch.bfloat16).contiguous()
-    T = hidden_states.shape[0]
+    ri = _i32(rows_idx) if rows_idx is not None else None
+    T = ri.numel() if ri is not None else hidden_states.shape[0]
     w = torch.empty((T, top_k), dtype=torch.bfloat16, device=hidden_states.device)
     ids = torch.empty((T, top_k), dtype=torch.int32, device=hidden_states.device)
     if T:
-        _lib.call("dyllm_moe_gate", _ptr(hidden_states), None, T, hidden_states.shape[1], _ptr(rw), rw.shape[0],
+        _lib.call("dyllm_moe_gate", _ptr(hidden_states), _ptr(ri), T, hidden_states.shape[1], _ptr(rw), rw.shape[0],
                   int(top_k), int(bool(renormalize)), _ptr(w), _ptr(ids), _stream())
     return w, ids
 
@@ -782,15 +786,25 @@ def moe_align_block_size(topk_ids, block_size, num_experts):
     return sorted_ids, tile_e, npp
 
 
-def fused_experts(hidden_states, w1, w2, topk_weights, topk_ids, activation="silu", out=None, out_rows=None):
-    """fused_experts (fused_moe.py:269-335) with SiLU gating."""
+def fused_experts(hidden_states, w1, w2, topk_weights, topk_ids, activation="silu", out=None, out_rows=None,
+                  rows_idx=None):
+    """fused_experts (fused_moe.py:269-335) with SiLU gating. With ``rows_idx`` token t is row
+    rows_idx[t] of ``hidden_states`` (the salient rows, gathered inside the first grouped GEMM)."""
     if activation != "silu":
         raise RuntimeError("only the silu activation (LLaDA-MoE) is implemented")
     x = hidden_states
     _check(x, "hidden_states", torch.bfloat16, 2)
     _check(w1, "w1", torch.bfloat16, 3)
     _check(w2, "w2", torch.bfloat16, 3)
-    T, hidden = x.shape
+    ri = None
+    if rows_idx is not None:
+        _gemm_source(x)
+        ri = _i32(rows_idx)
+        if ri.numel() != topk_ids.shape[0]:
+            raise RuntimeError("rows_idx must have one entry per routed token")
+        if x.stride(1) != 1 or x.stride(0) != x.shape[1]:
+            raise RuntimeError("hidden_states must be contiguous when rows are gathered")
+    T, hidden = (topk_ids.shape[0], x.shape[1]) if ri is not None else x.shape
     E, two_i, _ = w1.shape
     inter = two_i // 2
     top_k = topk_ids.shape[1]
@@ -805,6 +819,6 @@ def fused_experts(hidden_states, w1, w2, topk_weights, topk_ids, activation="sil
         return out
     ws_bytes = _lib.load().dyllm_fused_experts_workspace_bytes(T, top_k, E, hidden, inter)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
-    _lib.call("dyllm_fused_experts", _ptr(x), None, T, hidden, _ptr(w1), _ptr(w2), E, inter, _ptr(tw), _ptr(ti),
+    _lib.call("dyllm_fused_experts", _ptr(x), _ptr(ri), T, hidden, _ptr(w1), _ptr(w2), E, inter, _ptr(tw), _ptr(ti),
               top_k, _ptr(out), _ptr(orow), _ptr(ws), ws_bytes, _stream())
     return out

@@ -403,7 +403,9 @@ size_t dyllm_fused_experts_workspace_bytes(int64_t tokens, int top_k, int num_ex
                                            int intermediate);
 
 /* fused_experts with SiLU gating: w1 [E, 2*I, hidden], w2 [E, hidden, I]; routing from
- * dyllm_moe_gate. out[out_rows ? out_rows[t] : t] = sum_k w_k * FFN_{e_k}(x_t), bf16. */
+ * dyllm_moe_gate. out[out_rows ? out_rows[t] : t] = sum_k w_k * FFN_{e_k}(x_t), bf16, where token t
+ * is x row rows_idx[t] (rows_idx NULL: row t; the gather of the salient rows, util.py:19-36,
+ * happens inside the first grouped GEMM). */
 int dyllm_fused_experts(const void* x, const int32_t* rows_idx, int64_t tokens, int hidden, const void* w1,
                         const void* w2, int num_experts, int intermediate, const void* topk_weights,
                         const int32_t* topk_ids, int top_k, void* out, const int64_t* out_rows, void* workspace,

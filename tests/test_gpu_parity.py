@@ -361,6 +361,30 @@ def test_moe_gate_align_experts(dev):
     assert_bf16_close(out, want.to(BF), what="fused experts")
 
 
+def test_moe_gathered_rows_match_compacted(dev):
+    """Router and experts reading the salient rows in place (rows_idx) give bit-identical routing
+    and outputs to the same calls on the gathered rows (gather_rows_2D, util.py:19-36), and write
+    only the destination rows."""
+    ops = _ops()
+    g = _gen(22)
+    T_all, hidden, E, top_k, inter = 500, 256, 64, 8, 128
+    x_all = _randn(g, T_all, hidden).to(dev)
+    rows = torch.randperm(T_all, generator=g)[:173].to(torch.int32).to(dev)
+    wr = _randn(g, E, hidden, scale=0.1).to(dev)
+    w1 = _randn(g, E, 2 * inter, hidden, scale=0.05).to(dev)
+    w2 = _randn(g, E, hidden, inter, scale=0.05).to(dev)
+    x = x_all[rows.long()].contiguous()
+    w, ids = ops.moe_gate(x, wr, top_k)
+    wg, idg = ops.moe_gate(x_all, wr, top_k, rows_idx=rows)
+    assert torch.equal(ids, idg) and torch.equal(w, wg)
+    dest = torch.randperm(T_all + 50, generator=g)[:173].to(dev)
+    want = torch.zeros(T_all + 50, hidden, dtype=BF, device=dev)
+    ops.fused_experts(x, w1, w2, w, ids, out=want, out_rows=dest)
+    got = torch.zeros_like(want)
+    ops.fused_experts(x_all, w1, w2, w, ids, out=got, out_rows=dest, rows_idx=rows)
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("T,hidden,E,top_k,renorm", [(1, 48, 8, 2, False), (33, 48, 8, 2, True), (70, 272, 13, 4, False),
                                                      (257, 2048, 64, 8, True)])
 def test_moe_gate_shapes(dev, T, hidden, E, top_k, renorm):
