@@ -395,46 +395,88 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
 
 // Persistent launch: one workgroup per CU loops over the output tiles. The number of tiles can
 // come from device memory (num_m_dev: the salient count written by the compaction kernel), so
-// the GEMM is enqueued without the host knowing M. Tiles are split into 8 contiguous ranges,
-// one per XCD (workgroup b runs on XCD b % 8), ordered split-K slice > N tile > M tile, so the
-// M tiles that share a weight slice run together on one XCD and read it from HBM once.
+// the GEMM is enqueued without the host knowing M. Workgroup b runs on XCD b % 8; the columns
+// (split-K slice, N tile) are split into 8 contiguous ranges, one per XCD, and the M tiles that
+// share a weight slice run together on one XCD, so they read it from HBM once:
+//   * grouped (SwiGLU GEMM, when the M tiles of one column fit the XCD's workgroups and this
+//     takes no more rounds): the XCD's workgroups form groups of as many as there are M tiles; member i of a
+//     group always computes M tile i, and a group walks its share of the XCD's columns. The M
+//     tiles of a column start together and stream its weight slice in step (one HBM read of it,
+//     the others hitting L2), and a workgroup's gathered A rows never change;
+//   * otherwise the XCD's tiles in order (M fastest, then N tile, then split-K slice), one per
+//     workgroup per round.
+struct TileWalk {
+  bool grouped;
+  int mtr, n_tiles;
+  int64_t t, t_end, stride;   // linear walk: tiles t, t + stride, ... < t_end
+  int member;                 // grouped walk: fixed M tile, columns t, t + stride, ... < t_end
+  __device__ __forceinline__ bool valid() const { return t < t_end; }
+  __device__ __forceinline__ int mt(int64_t u) const { return grouped ? member : int(u % mtr); }
+  __device__ __forceinline__ int64_t col(int64_t u) const { return grouped ? u : u / mtr; }
+};
+
+__device__ __forceinline__ TileWalk tile_walk(int64_t mtr, int n_tiles, int ksplit, int P, bool allow_grouped) {
+  TileWalk w{};
+  w.mtr = int(mtr);
+  w.n_tiles = n_tiles;
+  const int64_t ncols = int64_t(n_tiles) * ksplit;
+  const int64_t total = mtr * ncols;
+  if ((P & 7) != 0) {
+    w.t = blockIdx.x;
+    w.t_end = total;
+    w.stride = P;
+    return w;
+  }
+  const int x = blockIdx.x & 7, local = blockIdx.x >> 3, nloc = P >> 3;
+  const int64_t c_lo = ncols * x / 8, c_hi = ncols * (x + 1) / 8;
+  const int64_t groups = mtr > 0 ? nloc / mtr : 0;
+  // rounds of the XCD's busiest range either way
+  const int64_t cols_max = cdiv(ncols, 8);
+  if (allow_grouped && groups > 0 && cdiv(cols_max, groups) <= cdiv(cols_max * mtr, nloc)) {
+    w.grouped = true;
+    const int64_t grp = local / mtr;
+    w.member = int(local % mtr);
+    w.t = grp < groups ? c_lo + grp : c_hi;
+    w.t_end = c_hi;
+    w.stride = groups;
+  } else {
+    w.t = c_lo * mtr + local;
+    w.t_end = c_hi * mtr;
+    w.stride = nloc;
+  }
+  return w;
+}
+
 template <int BM, int BN, int WGN, GemmEpi EPI>
 __global__ __launch_bounds__(128 * WGN) __attribute__((amdgpu_waves_per_eu(WGN == 2 ? 1 : 2, WGN == 2 ? 1 : 2)))
 void gemm_kernel(GemmArgs g) {
   const int64_t M = g.num_m_dev ? min(int64_t(g.num_m_dev[0]), g.M) : g.M;   // never past the host capacity
   const int n_tiles = (EPI == GemmEpi::SwiGLU) ? (g.half_n / (BN / 2)) : int(cdiv(g.N, BN));
-  const int mtr = int(cdiv(M, BM));
-  const int64_t total = int64_t(mtr) * n_tiles * g.ksplit;
-  const int P = gridDim.x;
-  int64_t t, t_end, stride;
-  if ((P & 7) == 0) {
-    const int x = blockIdx.x & 7, local = blockIdx.x >> 3;
-    const int64_t lo = total * x / 8, hi = total * (x + 1) / 8;
-    t = lo + local;
-    t_end = hi;
-    stride = P >> 3;
-  } else {
-    t = blockIdx.x;
-    t_end = total;
-    stride = P;
-  }
+  // grouped walks for the SwiGLU GEMM only: measured on the Store GEMMs (down projection with
+  // split-K, K/V projection) they were 1-3 % slower, while the gate_up GEMM keeps its time and
+  // fetches 5 % less from HBM
+  const TileWalk tw = tile_walk(cdiv(M, BM), n_tiles, g.ksplit, gridDim.x, EPI == GemmEpi::SwiGLU);
   constexpr int CA = BM / (16 * WGN);
   int64_t rows[CA], rows_next[CA];
   if constexpr (EPI == GemmEpi::SwiGLU) {
-    if (t < t_end)
-      gemm_tile_rows<BM, WGN>(g, M, int(t % mtr), __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6),
+    if (tw.valid())
+      gemm_tile_rows<BM, WGN>(g, M, tw.mt(tw.t), __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6),
                               (threadIdx.x & 63) >> 3, rows);
   }
-  for (; t < t_end; t += stride) {
-    const int mt = int(t % mtr);
-    const int64_t rest = t / mtr;
-    const int nt = int(rest % n_tiles);
-    const int kz = int(rest / n_tiles);
-    const int mt_next = (EPI == GemmEpi::SwiGLU && t + stride < t_end) ? int((t + stride) % mtr) : -1;
+  for (int64_t u = tw.t; u < tw.t_end; u += tw.stride) {
+    const int mt = tw.mt(u);
+    const int64_t c = tw.col(u);
+    const int nt = int(c % n_tiles);
+    const int kz = int(c / n_tiles);
+    // the SwiGLU tile looks the next tile's source rows up during its K loop (grouped walks keep
+    // one M tile, whose rows are already in place)
+    const int mt_next = (EPI == GemmEpi::SwiGLU && !tw.grouped && u + tw.stride < tw.t_end) ? tw.mt(u + tw.stride) : -1;
     gemm_tile<BM, BN, WGN, EPI>(g, M, mt, nt, kz, rows, mt_next, rows_next);
     if constexpr (EPI == GemmEpi::SwiGLU) {
+      if (mt_next >= 0) {
 #pragma unroll
-      for (int i = 0; i < CA; ++i) rows[i] = rows_next[i];
+        for (int i = 0; i < CA; ++i) rows[i] = rows_next[i];
+      }
     }
   }
 }
