@@ -56,9 +56,9 @@ EVENT_STRIDE = 8
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch of the gate_up GEMM at this workload, from rocprofv3 FETCH_SIZE / WRITE_SIZE
 # calibrated against a 256 MiB copy (profiles/pmc_gemm_gate_up_config1.md).
-GATE_UP_TRAFFIC_BYTES = 361.7e6
+GATE_UP_TRAFFIC_BYTES = 345.0e6
 # HBM bytes per launch of the fused attention kernel, same method (profiles/pmc_attention_step_config1.md)
-ATTN_TRAFFIC_BYTES = 420.4e6
+ATTN_TRAFFIC_BYTES = 418.9e6
 
 
 def build_workload(cfg, layers, device, seed=0):
@@ -427,9 +427,30 @@ def profile_gate_up(cfg, reps=3):
     for _ in range(reps):
         ops.ffn_gate_up(x, w, rows)
         b.copy_(a)  # calibration: 256 MiB read + 256 MiB written
-    torch.cuda.synchronize()
-    print(f"[bench] profiled gate_up: {reps} launches of M={M}, plus {reps} calibration copies of 256 MiB",
-          file=sys.stderr)
+    # the gather's and the scatter's share: the same products on contiguous rows, in this order
+    # (dispatches in the counter file follow it): gate_up gathered, gate_up contiguous, down with
+    # the FFN-cache scatter (random cache rows), down contiguous
+    xc = x[rows.long()].contiguous()
+    wd = torch.empty(hid, inter, device=dev).normal_(0, 0.02, generator=g).to(torch.bfloat16)
+    cache = torch.empty(cfg["batch"] * (cfg["prompt"] + cfg["response"]), hid, dtype=torch.bfloat16, device=dev)
+    dest = torch.randperm(cache.shape[0], device=dev, generator=g)[:M]
+    h = ops.ffn_gate_up(xc, w)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(4)]
+    cases = [lambda: ops.ffn_gate_up(x, w, rows), lambda: ops.ffn_gate_up(xc, w),
+             lambda: ops.ffn_down(h, wd, out=cache, out_rows=dest), lambda: ops.ffn_down(h, wd)]
+    ms = [0.0] * 4
+    for i, fn in enumerate(cases):
+        for _ in range(2):   # warm
+            fn()
+        for _ in range(reps):
+            ev[i][0].record()
+            fn()
+            ev[i][1].record()
+            torch.cuda.synchronize()
+            ms[i] += ev[i][0].elapsed_time(ev[i][1]) / reps
+    print(f"[bench] profiled gate_up: {reps} launches of M={M}, plus {reps} calibration copies of 256 MiB; then "
+          f"{reps} each of gate_up gathered / contiguous and down scattered / contiguous: "
+          + ", ".join(f"{v * 1e3:.1f} us" for v in ms), file=sys.stderr)
 
 
 def profile_attention(cfg, reps=5):
@@ -571,6 +592,34 @@ def time_moe(reps=6, copies=4):
             "router_us": round(router_us, 2)}
 
 
+def probe_issue(iters=4096):
+    """dyllm_issue_probe at one wavefront per SIMD (256 workgroups of 256 threads): mean cycles per
+    loop iteration of 4 MFMA 32x32x16, of 64 FMA, of 64 exp + 64 mul, and of the MFMA loop fused
+    with each VALU loop in one wavefront (compiler-scheduled and pinned 1 MFMA : 16 VALU). The
+    overlap of MFMA and VALU work = (MFMA + VALU - both) / min(MFMA, VALU)."""
+    import torch
+
+    from dyllm_amd import _lib
+
+    wgs = 256
+    sink = torch.empty(wgs * 256, dtype=torch.float32, device="cuda")
+    cyc = torch.empty(wgs, dtype=torch.int64, device="cuda")
+    names = ["mfma", "fma", "exp", "mfma+fma", "mfma+fma pinned", "mfma+exp", "mfma+exp pinned"]
+    res = {}
+    for mode, name in enumerate(names):
+        for _ in range(2):   # the second launch is timed
+            _lib.call("dyllm_issue_probe", mode, wgs, iters, sink.data_ptr(), cyc.data_ptr(),
+                      torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        res[name] = round(float(cyc.double().mean()) / iters, 1)
+    ov = {}
+    for both, valu in (("mfma+fma", "fma"), ("mfma+fma pinned", "fma"), ("mfma+exp", "exp"),
+                       ("mfma+exp pinned", "exp")):
+        ov[both] = round((res["mfma"] + res[valu] - res[both]) / min(res["mfma"], res[valu]), 3)
+    print(json.dumps({"probe": "MFMA/VALU issue of one wavefront per SIMD", "cycles_per_iteration": res,
+                      "overlap_fraction": ov, "iters": iters, "workgroups": wgs}))
+
+
 def _attn_flops(T, L, HD, n, n_seq_sal):
     """Algorithmic MFMA work of the fused attention kernel: row-sparse tiles 4 Lk H D per salient
     query row; column-sparse tiles QK^T 2 Lk H D per other row plus PV over the salient keys of
@@ -694,6 +743,9 @@ def main():
     ap.add_argument("--perturb", type=float, default=None,
                     help="config 1's perturbed fraction of the response rows (default 0.15); the PMC traffic "
                          "figures apply to the default only")
+    ap.add_argument("--probe-issue", action="store_true",
+                    help="MFMA / VALU issue probe of one SIMD (dyllm_issue_probe): cycles per loop iteration of "
+                         "each kind alone and both in one wavefront; prints one JSON line")
     ap.add_argument("--profile-hbm", action="store_true",
                     help="run only the standalone HBM-bound kernels at the config-1 shape and print their GB/s")
     args = ap.parse_args()
@@ -722,6 +774,9 @@ def main():
         return
     if args.profile_attention:
         profile_attention(cfg)
+        return
+    if args.probe_issue:
+        probe_issue()
         return
     layers = args.layers or cfg["layers"]
     dev = "cuda:0"

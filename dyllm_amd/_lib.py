@@ -44,6 +44,7 @@ SIGNATURES = {
     "dyllm_unmask_step": [_P, _P, _I, _P, _P, _P, _L, _P, _P, _P, _P, _L, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                           _P, _I, _P],
     "dyllm_attention_timer_read": [_P, _P],
+    "dyllm_issue_probe": [_I, _I, _I, _P, _P, _P],
     "dyllm_attention_sparse_workspace_bytes": [_I, _I, _L, _I],
     "dyllm_attention_sparse_varlen": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, _L, _I, _P, _P, _P,
                                       _P, _P, c_float, _P, c_size_t, _P],

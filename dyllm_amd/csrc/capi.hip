@@ -109,6 +109,14 @@ int dyllm_attention_timer_read(float* total_ms, int* launches) {
 }
 int dyllm_abi_version(void) { return 4; }
 
+int dyllm_issue_probe(int mode, int workgroups, int iters, void* sink, void* cycles, void* stream) {
+  DYLLM_NONNULL(sink);
+  DYLLM_NONNULL(cycles);
+  DYLLM_REQUIRE(workgroups >= 1 && iters >= 1, "workgroups and iters must be positive");
+  return launch_issue_probe(mode, workgroups, iters, static_cast<float*>(sink),
+                            static_cast<unsigned long long*>(cycles), DYLLM_STREAM(stream));
+}
+
 // ---------------------------------------------------------------------------------------
 size_t dyllm_attention_sparse_workspace_bytes(int batch, int num_heads, int64_t total_q, int max_seqlen_k) {
   const int64_t nblk = cdiv(max_seqlen_k > 0 ? max_seqlen_k : 1, 64);

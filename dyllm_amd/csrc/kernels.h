@@ -268,4 +268,7 @@ int launch_moe_align(const int32_t* ids, int64_t S, int E, int bm, int32_t* sort
 int launch_moe_combine(const uint16_t* y, int64_t T, int Hd, int top_k, uint16_t* out, const int64_t* dst_rows,
                        hipStream_t s);
 
+// issue-rate probe (probe.hip): per-wavefront cycles of MFMA / VALU loops alone and together
+int launch_issue_probe(int mode, int wgs, int iters, float* sink, unsigned long long* cyc, hipStream_t s);
+
 }  // namespace dyllm

@@ -87,6 +87,13 @@ int dyllm_attention_kernel_info(int dim, int mask_v_rows, int64_t* out);
 int dyllm_attention_timer(int enable);
 int dyllm_attention_timer_read(float* total_ms, int* launches);
 
+/* Issue-rate probe of one SIMD (no counterpart in the reference; for benchmarks): `workgroups`
+ * 256-thread workgroups each run `iters` iterations of a loop chosen by mode -- 0: 4 MFMA
+ * 32x32x16 bf16, 1: 64 v_fma_f32, 2: 64 v_exp_f32 + 64 v_mul_f32, 3: 0 and 1 in one wavefront,
+ * 4: the same pinned as 1 MFMA / 16 VALU groups, 5: 0 and 2, 6: 5 pinned. cycles[w] receives the
+ * s_memtime cycles of workgroup w's loop; sink (workgroups * 256 floats) keeps the results live. */
+int dyllm_issue_probe(int mode, int workgroups, int iters, void* sink, void* cycles, void* stream);
+
 /* ---- attention ------------------------------------------------------------------------ */
 
 /* Workspace for dyllm_attention_sparse_varlen. */
