@@ -264,16 +264,28 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
         }
       }
     };
-    auto fetch_k = [&](int kb) {
+    // K rows of one 64-key block into registers: a full block (block-uniform branch) loads without
+    // per-row guards or zero fills, the ragged last block guards each row
+    auto load_k_block = [&](uint4 (&dst)[KCH], int kb) {
       const int key0 = kb * kBK;
+      if (key0 + kBK <= Lk) {
+        const uint16_t* kp = Kb + int64_t(key0) * ldkv;
+#pragma unroll
+        for (int it = 0; it < KCH; ++it) {
+          const int c = tid + NT * it;
+          dst[it] = *reinterpret_cast<const uint4*>(kp + int64_t(c >> 4) * ldkv + (c & 15) * 8);
+        }
+        return;
+      }
 #pragma unroll
       for (int it = 0; it < KCH; ++it) {
         const int c = tid + NT * it;
         const int key = c >> 4, dc = c & 15;
-        kreg[it] = (key0 + key < Lk) ? *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8)
-                                     : make_uint4(0, 0, 0, 0);
+        dst[it] = (key0 + key < Lk) ? *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8)
+                                    : make_uint4(0, 0, 0, 0);
       }
     };
+    auto fetch_k = [&](int kb) { load_k_block(kreg, kb); };
     auto stage_k = [&](uint16_t* kt) {
 #pragma unroll
       for (int it = 0; it < KCH; ++it) {
@@ -474,16 +486,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       float* const mt_par = sp.m + pg * (kMaxBlk2 * 32) + ql;
       float pm[2] = {-FLT_MAX, -FLT_MAX}, pl[2] = {0.f, 0.f};   // [own group, partner group]
       uint4 kreg1[KCH];
-      auto fetch_k1 = [&](int kb) {
-        const int key0 = kb * kBK;
-#pragma unroll
-        for (int it = 0; it < KCH; ++it) {
-          const int c = tid + NT * it;
-          const int key = c >> 4, dc = c & 15;
-          kreg1[it] = (key0 + key < Lk) ? *reinterpret_cast<const uint4*>(Kb + int64_t(key0 + key) * ldkv + dc * 8)
-                                        : make_uint4(0, 0, 0, 0);
-        }
-      };
+      auto fetch_k1 = [&](int kb) { load_k_block(kreg1, kb); };
       auto stage_k1 = [&]() {
 #pragma unroll
         for (int it = 0; it < KCH; ++it) {
