@@ -79,10 +79,6 @@ int launch_saliency_reduce(const float* part, float* stats, uint8_t* mask, int64
 int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
                    int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
                    hipStream_t s, int32_t* host_meta = nullptr);
-// statistics reduction + tau test of the native step; block_counts (optional) receives the
-// salient rows of every 256-row block for launch_compact_blocks
-int launch_reduce_stats(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
-                        int32_t* block_counts, hipStream_t s);
 // dest (optional): the row of every salient row in a per-layer cache addressed by dest_starts
 // (scatter_update addressing of its K-space row; cu_k = the batch's key prefix)
 struct CompactDest {
@@ -91,10 +87,6 @@ struct CompactDest {
   const int32_t* cu_k;
   int64_t* dest;
 };
-int launch_compact_blocks(const uint8_t* mask, int64_t T, const int32_t* block_counts, const int32_t* cu_q, int B,
-                          const int32_t* cu_prompt, int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32,
-                          int32_t* cu_sal, int32_t* count, int32_t* host_meta, hipStream_t s,
-                          const CompactDest& dest = CompactDest{});
 // statistics reduction + tau test + compaction of the native step in one launch (look-back over
 // per-workgroup counts). flags: reduce_compact_blocks(T) int32 words, zero before the launch.
 constexpr int32_t kCompactLookbackFailed = -2;

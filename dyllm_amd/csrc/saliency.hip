@@ -9,10 +9,12 @@
 //   * compaction-- torch.nonzero (ascending) + searchsorted(idxs, cu_seqlens_q) +
 //                  fused_offset (attention.py:147-166, attention_aux_kernels.cu:112-128).
 //
-// MI355X design: the stats of the column-sparse attention epilogue are written per
-// (head, row) without atomics and reduced here in a fixed order, so the salient set is
-// run-to-run deterministic; compaction is one workgroup of 16 wavefronts that scans the
-// byte mask with ballot/popcount prefix sums and never returns to the host.
+// MI355X design: the stats of the column-sparse attention epilogue are written per (head, row)
+// without atomics and reduced here in a fixed order, so the salient set is run-to-run
+// deterministic. The sparse step reduces, tests and compacts in one multi-workgroup launch
+// (reduce_compact_kernel, a look-back over per-workgroup counts); the standalone compaction is one
+// workgroup of 16 wavefronts that scans the byte mask with ballot / popcount prefix sums. Neither
+// returns to the host.
 #include "kernels.h"
 
 namespace dyllm {
@@ -252,159 +254,21 @@ __global__ __launch_bounds__(kCompactThreads) void compact_kernel(
   write_host_meta(host_meta, cu_sal, count, B);
 }
 
-// ---- statistics reduction of the native step ------------------------------------------
-// Every workgroup reduces the per-head partial statistics of 256 rows: its four 256-thread
-// quarters sum contiguous quarters of the heads (ascending), and the quarter sums are added in
-// quarter order (a fixed order: deterministic); it writes the statistics and the tau decision.
-// (A variant that let the last workgroup compact the mask in the same launch measured slower:
-// the device-scope fences it needs cost more than the second launch.)
-constexpr int kReduceRows = kCompactThreads / 4;
-
-__device__ __forceinline__ void reduce_rows(const float* __restrict__ part, float* __restrict__ stats,
-                                            uint8_t* __restrict__ mask, int64_t T, int H, float tau,
-                                            int32_t* __restrict__ block_counts) {
-  __shared__ float red[4][3][kReduceRows];
-  const int tl = threadIdx.x % kReduceRows, hq = threadIdx.x / kReduceRows;
-  const int64_t t = int64_t(blockIdx.x) * kReduceRows + tl;
-  const int hpq = (H + 3) / 4;
-  const int h0 = hq * hpq, h1 = (h0 + hpq < H) ? h0 + hpq : H;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f;
-  if (t < T) {
-#pragma unroll 4
-    for (int h = h0; h < h1; ++h) {
-      s0 += part[(int64_t(h) * 3 + 0) * T + t];
-      s1 += part[(int64_t(h) * 3 + 1) * T + t];
-      s2 += part[(int64_t(h) * 3 + 2) * T + t];
-    }
-  }
-  red[hq][0][tl] = s0;
-  red[hq][1][tl] = s1;
-  red[hq][2][tl] = s2;
-  __syncthreads();
-  bool sal = false;
-  if (hq == 0 && t < T) {
-    s0 = ((red[0][0][tl] + red[1][0][tl]) + red[2][0][tl]) + red[3][0][tl];
-    s1 = ((red[0][1][tl] + red[1][1][tl]) + red[2][1][tl]) + red[3][1][tl];
-    s2 = ((red[0][2][tl] + red[1][2][tl]) + red[2][2][tl]) + red[3][2][tl];
-    stats[3 * t] = s0;
-    stats[3 * t + 1] = s1;
-    stats[3 * t + 2] = s2;
-    sal = tau_cos(s0, s1, s2) < tau;
-    mask[t] = sal;
-  }
-  if (block_counts) {
-    // salient rows of this block, for the multi-workgroup compaction (waves of the first
-    // quarter hold the rows)
-    __shared__ int wcnt[kReduceRows / 64];
-    const unsigned long long bal = __ballot(sal);
-    if (hq == 0 && (threadIdx.x & 63) == 0) wcnt[threadIdx.x >> 6] = __popcll(bal);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      int c = 0;
-      for (int w = 0; w < kReduceRows / 64; ++w) c += wcnt[w];
-      block_counts[blockIdx.x] = c;
-    }
-  }
-}
-
-__global__ __launch_bounds__(kCompactThreads) void reduce_stats_kernel(const float* __restrict__ part,
-                                                                       float* __restrict__ stats,
-                                                                       uint8_t* __restrict__ mask, int64_t T, int H,
-                                                                       float tau, int32_t* __restrict__ block_counts) {
-  reduce_rows(part, stats, mask, T, H, tau, block_counts);
-}
-
-int launch_reduce_stats(const float* part, float* stats, uint8_t* mask, int64_t T, int H, float tau,
-                        int32_t* block_counts, hipStream_t s) {
-  if (T <= 0) return 0;
-  reduce_stats_kernel<<<unsigned(cdiv(T, kReduceRows)), kCompactThreads, 0, s>>>(part, stats, mask, T, H, tau,
-                                                                                   block_counts);
-  return check_launch("reduce_stats_kernel");
-}
-
-// ---- multi-workgroup compaction (native step) ----------------------------------------
-// Workgroup w owns mask rows [256w, 256w+256); its base is the sum of the salient counts of the
-// workgroups before it (written by reduce_stats_kernel). Rows are emitted in ascending order,
-// cu_salientlens[b] by the workgroup that owns row cu_q[b] (the last one for cu_q[B] = T), the
-// count by the last workgroup; the same values go to pinned host memory when given.
-__global__ __launch_bounds__(kReduceRows) void compact_blocks_kernel(
-    const uint8_t* __restrict__ mask, int64_t T, const int32_t* __restrict__ block_counts,
-    const int32_t* __restrict__ cu_q, int B, const int32_t* __restrict__ cu_prompt, int64_t* __restrict__ idx64,
-    int32_t* __restrict__ idx32, int64_t* __restrict__ idx_k, int32_t* __restrict__ idx_k32,
-    int32_t* __restrict__ cu_sal, int32_t* __restrict__ count, int32_t* __restrict__ host_meta, CompactDest dd) {
-  constexpr int NWV = kReduceRows / 64;
-  __shared__ int wtot[NWV];
-  __shared__ int part_sh[NWV];
-  __shared__ int pre[kReduceRows + 1];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int nblk = gridDim.x, blk = blockIdx.x;
-  const int64_t t = int64_t(blk) * kReduceRows + tid;
-  // base = sum of the earlier blocks' counts
-  int acc = 0;
-  for (int w = tid; w < blk; w += kReduceRows) acc += block_counts[w];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-  if (lane == 0) part_sh[wid] = acc;
-  const bool sal = t < T && mask[t];
-  const unsigned long long bal = __ballot(sal);
-  const int before = __popcll(bal & ((1ull << lane) - 1));
-  if (lane == 0) wtot[wid] = __popcll(bal);
-  __syncthreads();
-  int base = 0, woff = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < NWV; ++w) {
-    base += part_sh[w];
-    woff += (w < wid) ? wtot[w] : 0;
-    total += wtot[w];
-  }
-  pre[tid] = woff + before;
-  if (tid == 0) pre[kReduceRows] = total;
-  const int pos = base + woff + before;
-  if (sal) {
-    idx64[pos] = t;
-    if (idx32) idx32[pos] = int32_t(t);
-    if (idx_k || dd.dest) {
-      const int seg = find_segment(cu_q, B + 1, t);
-      const int64_t kk = idx_k ? t + cu_prompt[seg + 1] : t;   // K-space row (refresh: Q space == K space)
-      if (idx_k) {
-        idx_k[pos] = kk;
-        if (idx_k32) idx_k32[pos] = int32_t(kk);
-      }
-      // row of this salient row in the consumer's cache (the FFN-output scatter target)
-      if (dd.dest) dd.dest[pos] = dd.dest_starts[dd.seq_ids[seg]] + (kk - dd.cu_k[seg]);
-    }
-  }
-  __syncthreads();
-  bool wrote = false;
-  const int64_t lo = int64_t(blk) * kReduceRows;
-  for (int b = tid; b <= B; b += kReduceRows) {
-    const int64_t p = cu_q[b];
-    const int owner = (p >= T) ? nblk - 1 : int(p / kReduceRows);
-    if (owner != blk) continue;
-    const int64_t local = p - lo;
-    const int v = base + (local >= kReduceRows ? total : pre[local]);
-    cu_sal[b] = v;
-    if (host_meta) host_meta[1 + b] = v;
-    wrote = true;
-  }
-  if (blk == nblk - 1 && tid == 0) {
-    count[0] = base + total;
-    if (host_meta) host_meta[0] = base + total;
-    wrote = true;
-  }
-  if (host_meta && wrote) __threadfence_system();
-}
-
 // ---- statistics reduction + tau test + compaction in one launch (native step) ---------------
-// Workgroup w reduces the statistics of rows [256w, 256w+256) exactly as reduce_stats_kernel,
-// publishes its salient count (count + 1 in flags[w]; 0 = not yet) with a device-scope atomic
+// Workgroup w reduces the per-head partial statistics of rows [256w, 256w+256): its four
+// 256-thread quarters sum contiguous quarters of the heads (ascending) and the quarter sums are
+// added in quarter order (a fixed order: deterministic, where the reference's atomicAdd across head
+// blocks is not); it writes the statistics and the tau decision, publishes its salient count (count + 1 in flags[w]; 0 = not yet) with a device-scope atomic
 // store, then looks back: wavefront 0 reads flags[0..w) (one lane per workgroup, device-scope
 // atomic loads, each lane polling until its flag is set) and sums them into the workgroup's base;
-// then it places its own rows as compact_blocks_kernel does. Only counts cross workgroups, inside
+// then it places its own rows in ascending order (cu_salientlens[b] by the workgroup that owns row
+// cu_q[b], the count by the last workgroup; the same values go to pinned host memory when given).
+// Only counts cross workgroups, inside
 // the atomics themselves, so no fence orders any other data. Workgroups are dispatched in index
 // order, so every flag a workgroup waits for belongs to a workgroup that is running or done; the
 // poll is still bounded (kLookbackPolls per flag): a workgroup that exhausts it writes nothing, and
 // the last one then reports kCompactLookbackFailed as the count.
+constexpr int kReduceRows = kCompactThreads / 4;
 constexpr int kLookbackPolls = 1 << 20;
 
 __global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
@@ -550,21 +414,6 @@ int launch_reduce_compact(const float* part, float* stats, uint8_t* mask, int64_
 }
 
 int64_t reduce_compact_blocks(int64_t T) { return cdiv(T, kReduceRows); }
-
-int launch_compact_blocks(const uint8_t* mask, int64_t T, const int32_t* block_counts, const int32_t* cu_q, int B,
-                          const int32_t* cu_prompt, int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32,
-                          int32_t* cu_sal, int32_t* count, int32_t* host_meta, hipStream_t s,
-                          const CompactDest& dest) {
-  DYLLM_REQUIRE(B >= 1, "batch must hold at least one sequence");
-  DYLLM_REQUIRE(T >= 1 && T < (int64_t(1) << 31), "row count out of range");
-  DYLLM_REQUIRE(idx_k == nullptr || cu_prompt != nullptr, "cu_promptlens is required for K-space indices");
-  DYLLM_REQUIRE(dest.dest == nullptr || (dest.dest_starts && dest.seq_ids && dest.cu_k),
-                "cache rows need the cache's sequence starts, the sequence ids and cu_seqlens_k");
-  compact_blocks_kernel<<<unsigned(cdiv(T, kReduceRows)), kReduceRows, 0, s>>>(
-      mask, T, block_counts, cu_q, B, cu_prompt, idx64, idx32, idx_k, idx_k32, cu_sal, count, host_meta, dest);
-  return check_launch("compact_blocks_kernel");
-}
-
 
 int launch_compact(const uint8_t* mask, int64_t T, const int32_t* cu_q, int B, const int32_t* cu_prompt,
                    int64_t* idx64, int32_t* idx32, int64_t* idx_k, int32_t* idx_k32, int32_t* cu_sal, int32_t* count,
