@@ -335,6 +335,17 @@ class ModelRunner:
         rows only (RowLogits)."""
         return RowLogits(self.model(input_ids, positions), self.model.compute_logits)
 
+    def _host_candidates(self, seqs: List[Sequence], pruned: bool, width: int) -> int:
+        """Candidates of the step from the host mirrors (the masked positions of the current block,
+        at most `width` per sequence): the count unmask_step_kernel writes to cand_n, summed."""
+        mask = self.config.mask_id
+        total = 0
+        for seq in seqs:
+            limit = min(len(seq), seq.block_size * (seq.block_idx + 1) + seq.num_prompt_tokens)
+            off = seq.answer_start if pruned else 0
+            total += min(width, int(np.count_nonzero(seq.token_arr[off:limit] == mask)) if limit > off else 0)
+        return total
+
     def _run_device_step(self, db: _DeviceBatch, seqs: List[Sequence], pruned: bool):
         """A sparse step of the same batch as the previous one, built on the device."""
         from .. import _lib
@@ -365,7 +376,8 @@ class ModelRunner:
         logits = self.run_model(input_ids, positions, False)
         with torch.inference_mode():
             pos, tok, cnt = self.sampler(input_logits=logits, ctx=get_context(),
-                                         input_indices=DenseCandidates(db.cand_rel, db.cand_n, offsets),
+                                         input_indices=DenseCandidates(db.cand_rel, db.cand_n, offsets,
+                                                                       self._host_candidates(seqs, pruned, db.W)),
                                          temperatures=db.temps, num_transfer=db.transfers, top_k=db.top_ks,
                                          top_p=db.top_ps, block_size=db.W, confidence_thresholds=db.thrs)
         db.record(pos, tok, cnt)

@@ -74,8 +74,11 @@ class DenseCandidates:
     offset of candidate j from sequence b's first queried row, valid for j < count[b], in ascending
     position order; offsets[b] turns an offset into the absolute position."""
 
-    def __init__(self, rel: torch.Tensor, count: torch.Tensor, offsets: torch.Tensor):
+    def __init__(self, rel: torch.Tensor, count: torch.Tensor, offsets: torch.Tensor, n_valid: Optional[int] = None):
         self.rel, self.count, self.offsets = rel, count, offsets
+        # total of count[] when the host knows it (its token mirrors): the sampler then runs the
+        # LM head, softmax and sampling on the valid candidates only, in the host path's order
+        self.n_valid = n_valid
 
 
 class BaseSampler(nn.Module):
@@ -148,16 +151,31 @@ class BaseSampler(nn.Module):
         B, W = cands.rel.shape
         valid = torch.arange(W, device=dev).unsqueeze(0) < cands.count.long().unsqueeze(1)
         rows = (ctx.cu_seqlens_q[:-1].long().unsqueeze(1) + cands.rel).masked_fill(~valid, 0).reshape(-1)
-        cand = logits.index_select(0, rows)
         rep = lambda t: t.reshape(-1).repeat_interleave(W, output_size=B * W)
+        # the valid slots first (ascending (b, j): the host path's candidate order), sized by the
+        # host's count so nothing waits on the device; a padding slot (-1) lands in a spare slot
+        # B * W that is dropped. Without the host count every slot runs (empty ones masked).
+        if cands.n_valid is not None:
+            sel = torch.nonzero_static(valid.reshape(-1), size=int(cands.n_valid), fill_value=-1).reshape(-1)
+            dst = torch.where(sel >= 0, sel, torch.full_like(sel, B * W))
+            pick = lambda t: t.index_select(0, sel.clamp_min(0))
+        else:
+            dst = None
+            pick = lambda t: t
+        cand = logits.index_select(0, pick(rows))
         if temperatures is not None:
-            cand = cand / rep(temperatures).unsqueeze(-1)
-        cand = top_k_logits(cand, rep(top_k) if top_k is not None else None)
-        cand = top_p_logits(cand, rep(top_p) if top_p is not None else None)
+            cand = cand / pick(rep(temperatures)).unsqueeze(-1)
+        cand = top_k_logits(cand, pick(rep(top_k)) if top_k is not None else None)
+        cand = top_p_logits(cand, pick(rep(top_p)) if top_p is not None else None)
         probs = F.softmax(cand, dim=-1)
         top_probs, top_tokens = probs.max(dim=-1)
         scores = self.compute_scores(probs, top_probs)
-        tokens = self.sample_token(probs, top_tokens, rep(temperatures) if temperatures is not None else None)
+        tokens = self.sample_token(probs, top_tokens, pick(rep(temperatures)) if temperatures is not None else None)
+        if dst is not None:
+            full_s = torch.full((B * W + 1,), float("-inf"), dtype=scores.dtype, device=dev)
+            full_t = torch.zeros((B * W + 1,), dtype=tokens.dtype, device=dev)
+            scores = full_s.index_copy_(0, dst, scores)[: B * W]
+            tokens = full_t.index_copy_(0, dst, tokens)[: B * W]
         d_scores = scores.view(B, W).masked_fill(~valid, float("-inf"))
         d_tokens = tokens.view(B, W).masked_fill(~valid, 0)
         d_pos = (cands.rel + cands.offsets.long().unsqueeze(1)).masked_fill(~valid, 0)

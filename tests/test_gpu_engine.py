@@ -127,3 +127,23 @@ def test_device_bookkeeping_same_tokens(dev, model):
         dev_steps.append(eng.model_runner.device_steps)
     assert dev_steps[0] == 0 and dev_steps[1] > 10
     assert outs[0] == outs[1]
+
+
+def test_device_bookkeeping_same_tokens_sampled(dev):
+    """With a temperature (Dream samples categorically), device-built steps draw from the random
+    generator exactly as host-built ones do: the sampler runs on the valid candidates only, in
+    the host path's order, so both give the same tokens from the same seed."""
+    from dyllm_amd import SamplingParams, dLLM
+
+    outs, dev_steps = [], []
+    for on in (False, True):
+        eng = dLLM("tiny-dream", threshold=0.99, max_num_seqs=3)
+        eng.model_runner.device_bookkeeping = on
+        sp = SamplingParams(max_new_tokens=48, steps=12, num_full_steps=2, block_size=16, temperature=0.8)
+        torch.manual_seed(1234)
+        out = eng.generate([[3, 14, 15, 92, 65], [2, 71, 82, 81], [1] * 9], sp)
+        torch.cuda.synchronize()
+        outs.append([o["token_ids"] for o in out])
+        dev_steps.append(eng.model_runner.device_steps)
+    assert dev_steps[0] == 0 and dev_steps[1] > 5
+    assert outs[0] == outs[1]
