@@ -425,10 +425,14 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
             const float m_g = m_tab[blkl * 32];
             if (blk != blk_prev) {
               const float f = __builtin_amdgcn_exp2f((m_prev - m_g) * c2);
+              // skipped when no row's running maximum moved since the previous group's block (f is
+              // exactly 1 on every lane) or nothing is accumulated yet: the same values either way
+              if (blk_prev >= 0 && __ballot(f != 1.0f) != 0) {
 #pragma unroll
-              for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) o_acc[i][r] *= f;
+                  for (int r = 0; r < 16; ++r) o_acc[i][r] *= f;
+              }
               m_prev = m_g;
               blk_prev = blk;
             }
@@ -647,10 +651,12 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     // the blocks after the last salient one rescale the accumulator to the final max
     {
       const float f = __builtin_amdgcn_exp2f((m_prev - m_run) * c2);
+      if (blk_prev >= 0 && __ballot(f != 1.0f) != 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o_acc[i][r] *= f;
+          for (int r = 0; r < 16; ++r) o_acc[i][r] *= f;
+      }
     }
   }
   if (!two_pass) {
@@ -716,10 +722,14 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
         pf[t][u] = p.v;
       }
     l_run = l_run * rescale + psum;
+    // the accumulator rescale is skipped when no row's maximum moved in this block (rescale is
+    // exactly 1 on every lane) and before the first block's products (all zero): the same values
+    if (kb > 0 && __ballot(rescale != 1.0f) != 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o_acc[i][r] *= rescale;
+        for (int r = 0; r < 16; ++r) o_acc[i][r] *= rescale;
+    }
 
     // ---- O^T += V^T P^T on the 16-key groups that carry salient rows -----------------
     if (bmask != 0) {
