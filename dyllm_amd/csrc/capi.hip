@@ -283,12 +283,12 @@ static int timed_attention_step(const AttnArgs& rs, int rs_rows, const AttnArgs&
   return 0;
 }
 
-// Body of dyllm_sparse_attention_step(_kv): three launches and the compaction pair.
+// Body of dyllm_sparse_attention_step(_kv): three launches.
 //   1. step_rows_kernel: per salient row, [K/V epilogue], dV (at the key's rank within its
 //      sequence) and the V-cache update;
 //   2. attention_step_kernel: row-sparse tiles of the salient queries + column-sparse tiles of
 //      the others (their salient maps built in LDS from the lists);
-//   3. reduce_stats_kernel + compact_blocks_kernel: tau test and the next salient set.
+//   3. reduce_compact_kernel: head sums, tau test and the next salient set in one pass.
 static int sparse_step(const dyllm_kv_epilogue* epi, const void* q, const void* k, const int64_t* k_start,
                        void* v_cache, const int64_t* v_seq_starts, const void* v_new, void* c_cache,
                        const int64_t* c_seq_starts, const int64_t* seq_ids, int batch, int num_heads, int num_kv_heads,

@@ -363,7 +363,7 @@ __global__ __launch_bounds__(kCompactThreads) void reduce_compact_kernel(
     }
     return;
   }
-  // 4. placement of the block's salient rows (compact_blocks_kernel)
+  // 4. placement of the block's salient rows
   if (sal) {
     const int pos = base + woff + before;
     idx64[pos] = t;
