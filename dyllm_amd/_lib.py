@@ -78,6 +78,7 @@ SIGNATURES = {
     "dyllm_gather_rows": [_P, _L, _P, _L, _P, _L, _P],
     "dyllm_swiglu_ffn_workspace_bytes": [_L, _I],
     "dyllm_swiglu_ffn": [_P, _L, _P, _L, _P, _P, _I, _I, _P, c_size_t, _P, _P, _P],
+    "dyllm_silu_and_mul": [_P, _L, _L, _I, _P, _L, _P],
     "dyllm_ffn_tile_rows": [_L, _I, _I, _I],
     "dyllm_ffn_gate_up": [_P, _L, _P, _L, _P, _L, _P, _I, _I, _P, _P],
     "dyllm_ffn_down": [_P, _L, _P, _L, _P, _I, _I, _P, _P, _P, c_size_t, _P],

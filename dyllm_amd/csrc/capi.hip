@@ -107,7 +107,7 @@ int dyllm_attention_timer_read(float* total_ms, int* launches) {
   tm.used = 0;
   return 0;
 }
-int dyllm_abi_version(void) { return 4; }
+int dyllm_abi_version(void) { return 5; }
 
 int dyllm_issue_probe(int mode, int workgroups, int iters, void* sink, void* cycles, void* stream) {
   DYLLM_NONNULL(sink);
@@ -1038,6 +1038,15 @@ int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64
     return rc;
   return dyllm_ffn_down(workspace, rows, nullptr, 0, w_down, hidden, intermediate, out, out_rows,
                         static_cast<char*>(workspace) + hb, db, stream);
+}
+
+int dyllm_silu_and_mul(const void* gate_up, int64_t ld_in, int64_t rows, int intermediate, void* out, int64_t ld_out,
+                       void* stream) {
+  if (rows <= 0) return 0;
+  DYLLM_NONNULL(gate_up);
+  DYLLM_NONNULL(out);
+  return launch_silu_and_mul(static_cast<const uint16_t*>(gate_up), ld_in, rows, intermediate,
+                             static_cast<uint16_t*>(out), ld_out, DYLLM_STREAM(stream));
 }
 
 // ---------------------------------------------------------------------------------------

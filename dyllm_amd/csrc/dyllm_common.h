@@ -116,6 +116,18 @@ __device__ __forceinline__ uint4 bf16x8_sub(uint4 nw, uint4 o) {
   return make_uint4(d[0], d[1], d[2], d[3]);
 }
 
+// x * sigmoid(x) with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE division:
+// within 2-3 ulp of fp32 x / (1 + exp(-x)) before the bf16 rounding of the product. v_rcp_f32
+// flushes a denormal result, which 1 / (1 + exp(-x)) is for x in (-88.7, -87.3) while
+// x / (1 + exp(-x)) is still a normal number there; the reciprocal is therefore taken of the
+// denominator scaled by 2^-64 and the product scaled back (both scalings are exact), which leaves
+// every other value unchanged and saturates to -0 / x at the tails like the division. Shared by
+// the SwiGLU GEMM epilogue and the standalone SiLU-and-mul kernel, so both give the same bits.
+__device__ __forceinline__ float silu_f(float x) {
+  const float r = __builtin_amdgcn_rcpf((1.0f + __expf(-x)) * 0x1p-64f);
+  return (x * r) * 0x1p-64f;
+}
+
 __host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---- host-side error plumbing -------------------------------------------------------

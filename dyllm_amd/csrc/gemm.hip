@@ -48,16 +48,6 @@ namespace dyllm {
 constexpr int kGemmBK = 64;
 constexpr int kGemmBN = 256;
 
-// x * sigmoid(x) with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE division:
-// within 2-3 ulp of fp32 x / (1 + exp(-x)) before the bf16 rounding of the product. v_rcp_f32
-// flushes a denormal result, which 1 / (1 + exp(-x)) is for x in (-88.7, -87.3) while
-// x / (1 + exp(-x)) is still a normal number there; the reciprocal is therefore taken of the
-// denominator scaled by 2^-64 and the product scaled back (both scalings are exact), which leaves
-// every other value unchanged and saturates to -0 / x at the tails like the division.
-__device__ __forceinline__ float silu_f(float x) {
-  const float r = __builtin_amdgcn_rcpf((1.0f + __expf(-x)) * 0x1p-64f);
-  return (x * r) * 0x1p-64f;
-}
 __device__ __forceinline__ float bf16_rt(float x) { return __uint_as_float(uint32_t(f32_to_bf16(x)) << 16); }
 __device__ __forceinline__ void bf16x4_to_f32(uint2 v, float* f) {
   f[0] = __uint_as_float(v.x << 16);

@@ -245,6 +245,9 @@ struct GemmArgs {
 // tile_m: 128 / 192 / 256, or 0 to choose from M and the grid size. ksplit > 1 needs
 // g.partial with gemm_partial_bytes() bytes and is followed by the reduction kernel.
 int launch_gemm(GemmEpi epi, const GemmArgs& g, int64_t m_bound, int tile_m, int ksplit, hipStream_t s);
+// out[r] = bf16(silu(g) * u) for gu rows [g (inter) | u (inter)] (act.hip)
+int launch_silu_and_mul(const uint16_t* gu, int64_t ld_in, int64_t rows, int inter, uint16_t* out, int64_t ld_out,
+                        hipStream_t s);
 size_t gemm_partial_bytes(int64_t m_bound, int N, int tile_m, int ksplit);
 struct GemmPlan {
   int tile_m;   // 128 / 192 / 256

@@ -744,13 +744,44 @@ def _rms_norm_cache_rows(x, weight, eps, residual, out, residual_out):
     return out if residual is None else (out, residual_out)
 
 
+# Row count from which the dense FFN of all rows (the full step) runs the library GEMMs around
+# dyllm_silu_and_mul instead of the fused gate_up / down kernels: measured faster from 2048 rows on
+# (LLaDA-8B shapes), where the fused GEMMs' gather and scatter epilogues have nothing to save.
+DENSE_FFN_LIBRARY_ROWS = 2048
+
+
+def silu_and_mul(gate_up, out=None):
+    """SiluAndMul (activations.py:11-14) of a merged gate_up product [rows, 2I] (gate columns
+    first): bf16(silu(g) * u) computed in fp32 with one rounding (dyllm_silu_and_mul)."""
+    _check(gate_up, "gate_up", torch.bfloat16, 2)
+    if gate_up.stride(1) != 1 or gate_up.shape[1] % 2:
+        raise RuntimeError("gate_up must be [rows, 2I] with contiguous rows")
+    rows, inter = gate_up.shape[0], gate_up.shape[1] // 2
+    if out is None:
+        out = torch.empty((rows, inter), dtype=gate_up.dtype, device=gate_up.device)
+    else:
+        _check(out, "out", torch.bfloat16, 2)
+        if out.shape[0] < rows or out.shape[1] < inter or out.stride(1) != 1:
+            raise RuntimeError("out must hold [rows, I] with contiguous rows")
+    if rows:
+        _lib.call("dyllm_silu_and_mul", _ptr(gate_up), gate_up.stride(0), rows, inter, _ptr(out), out.stride(0),
+                  _stream())
+    return out
+
+
 def swiglu_ffn(x, w_gate_up, w_down, rows_idx=None, out=None, out_rows=None):
     """down(silu(a Wg^T) * (a Wu^T)) for a = x[rows_idx] (or all rows of x). With
     ``out``/``out_rows`` the result rows are written to out[out_rows[m]] (in-place scatter
-    into a cache); otherwise a new [M, hidden] tensor is returned."""
+    into a cache); otherwise a new [M, hidden] tensor is returned. A dense product of at least
+    DENSE_FFN_LIBRARY_ROWS rows runs gate_up and down as library GEMMs around silu_and_mul (the
+    same rounding points: g and u in bf16, silu(g) * u in fp32, h in bf16)."""
     _check(w_down, "w_down", torch.bfloat16, 2)
     if tuple(w_down.shape) != (x.shape[1], w_gate_up.shape[0] // 2):
         raise RuntimeError("weights must be w_gate_up [2I, hidden] and w_down [hidden, I]")
+    if rows_idx is None and out is None and x.shape[0] >= DENSE_FFN_LIBRARY_ROWS:
+        _check(x, "x", torch.bfloat16, 2)
+        _check(w_gate_up, "w_gate_up", torch.bfloat16, 2)
+        return torch.nn.functional.linear(silu_and_mul(torch.nn.functional.linear(x, w_gate_up)), w_down)
     h = ffn_gate_up(x, w_gate_up, rows_idx)
     return ffn_down(h, w_down, out, out_rows)
 

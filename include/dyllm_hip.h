@@ -25,6 +25,7 @@
  *   dyllm_gather_rows              <- gather_rows_2D, dyllm/utils/util.py:19-36
  *   dyllm_swiglu_ffn               <- LLaDAMLP.forward, dyllm/model_executor/models/llada.py:38-43
  *                                     (+ MLPcache.scatter_update, mlp_cache_manage.py:24-40)
+ *   dyllm_silu_and_mul             <- SiluAndMul.forward, dyllm/model_executor/layers/activations.py:11-14
  *   dyllm_moe_gate                 <- moe_gate, dyllm/model_executor/layers/fused_moe.py:375-408
  *   dyllm_moe_align_block_size     <- moe_align_block_size, fused_moe.py:37-85
  *   dyllm_fused_experts            <- fused_experts, fused_moe.py:269-335
@@ -321,6 +322,14 @@ size_t dyllm_ffn_down_workspace_bytes(int64_t rows, int64_t rows_hint, int hidde
 int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64_t rows, const void* w_gate_up,
                      const void* w_down, int hidden, int intermediate, void* workspace, size_t workspace_bytes,
                      void* out, const int64_t* out_rows, void* stream);
+
+/* SiLU-and-mul of a merged gate_up product (SiluAndMul, activations.py:11-14): for m < rows,
+ * out[m][j] = bf16(silu(g) * u) in fp32 with g = gate_up[m][j], u = gate_up[m][intermediate + j]
+ * (bf16; row strides ld_in >= 2*intermediate and ld_out >= intermediate, multiples of 8; both
+ * buffers 16-byte aligned). The same arithmetic as the SwiGLU epilogue of dyllm_ffn_gate_up, for
+ * a gate_up product computed by another GEMM (the dense full step runs the library GEMM). */
+int dyllm_silu_and_mul(const void* gate_up, int64_t ld_in, int64_t rows, int intermediate, void* out, int64_t ld_out,
+                       void* stream);
 
 /* The two stages of dyllm_swiglu_ffn: h_out [rows, intermediate] = silu(a W_g^T) * (a W_u^T)
  * with a = x[rows_idx[m] or m]; then out[out_rows[m] or m] = h[m] W_d^T. `rows` is the capacity

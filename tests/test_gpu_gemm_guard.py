@@ -6,7 +6,8 @@
   bound (max abs 2e-2, mean rel 1e-3);
 * the SwiGLU epilogue's SiLU (hardware reciprocal instead of an IEEE division) stays within one
   bf16 ulp of bf16(g / (1 + exp(-g))) in fp32 over a sweep of g across the tails and around 0
-  (activations.py:11-14 computes silu(g) * u in fp32 and rounds once)."""
+  (activations.py:11-14 computes silu(g) * u in fp32 and rounds once), and the standalone
+  dyllm_silu_and_mul gives the same bits on the same g and u."""
 import numpy as np
 import pytest
 import torch
@@ -65,3 +66,13 @@ def test_swiglu_silu_within_one_ulp(dev):
     diff = (h - want).abs()
     bad = diff > ulp
     assert not bad.any(), f"{int(bad.sum())} values differ by more than one bf16 ulp, e.g. g={gf[bad][:5].tolist()}"
+    # the standalone SiLU-and-mul (dyllm_silu_and_mul, after a library gate_up GEMM) on the same g
+    # and u: bit-identical to the fused epilogue, with u != 1 as well
+    gu = torch.cat([g.t(), torch.ones(M, inter, dtype=BF)], dim=1).contiguous().to(dev)
+    assert torch.equal(ops.silu_and_mul(gu).cpu().float(), h)
+    u = (torch.randn(M, inter, generator=torch.Generator().manual_seed(3)) * 2).to(BF)
+    h2 = ops.silu_and_mul(torch.cat([g.t(), u], dim=1).contiguous().to(dev)).cpu().float()
+    want2 = (gf / (1.0 + torch.exp(-gf)) * u.float()).to(BF).float()
+    ulp2 = torch.ldexp(torch.ones_like(want2), torch.frexp(want2.abs().clamp_min(2.0 ** -126))[1] - 8)
+    bad2 = (h2 - want2).abs() > ulp2
+    assert not bad2.any(), f"silu_and_mul: {int(bad2.sum())} values off by more than one bf16 ulp"

@@ -339,6 +339,25 @@ def test_swiglu_ffn_gathered(dev, M, hidden, inter):
     assert (cache.cpu()[untouched] == 0).all()
 
 
+@pytest.mark.parametrize("M,hidden,inter", [(2048, 512, 1024), (2500, 1024, 2048)])
+def test_swiglu_ffn_dense_library_path(dev, M, hidden, inter):
+    """A dense FFN of at least DENSE_FFN_LIBRARY_ROWS rows (the full step) runs the library GEMMs
+    around dyllm_silu_and_mul: the same oracle bar as the fused kernels, and within the bf16 bound
+    of the fused kernels' result on the same rows."""
+    ops = _ops()
+    assert M >= ops.DENSE_FFN_LIBRARY_ROWS
+    print(f"[ffn dense] M={M} hidden={hidden} inter={inter}", flush=True)
+    g = _gen(M + 1)
+    x = _randn(g, M, hidden)
+    wgu = _randn(g, 2 * inter, hidden, scale=hidden ** -0.5)
+    wd = _randn(g, hidden, inter, scale=inter ** -0.5)
+    xd, wgud, wdd = x.to(dev), wgu.to(dev), wd.to(dev)
+    y = ops.swiglu_ffn(xd, wgud, wdd)
+    assert_bf16_close(y, ref.swiglu_ffn(x, wgu, wd).to(BF), what="dense SwiGLU FFN (library GEMMs)")
+    fused = ops.ffn_down(ops.ffn_gate_up(xd, wgud), wdd)
+    assert_bf16_close(y, fused, what="library vs fused FFN")
+
+
 def test_moe_gate_align_experts(dev):
     ops = _ops()
     g = _gen(21)

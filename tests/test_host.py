@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     assert len(names) >= 25
     for n in names:
         assert hasattr(lib, n), f"{n} declared in include/dyllm_hip.h but not exported"
-    assert lib.dyllm_abi_version() == 4
+    assert lib.dyllm_abi_version() == 5
 
 
 def _ctype_of(param):
