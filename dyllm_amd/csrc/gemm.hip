@@ -396,14 +396,34 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
 //   * otherwise the XCD's tiles in order (M fastest, then N tile, then split-K slice), one per
 //     workgroup per round.
 struct TileWalk {
-  bool grouped;
+  bool grouped, msplit;
   int mtr, n_tiles;
   int64_t t, t_end, stride;   // linear walk: tiles t, t + stride, ... < t_end
   int member;                 // grouped walk: fixed M tile, columns t, t + stride, ... < t_end
+  int64_t m_lo, ncols;        // M-split walk: the XCD's M tiles from m_lo, columns fastest
   __device__ __forceinline__ bool valid() const { return t < t_end; }
-  __device__ __forceinline__ int mt(int64_t u) const { return grouped ? member : int(u % mtr); }
-  __device__ __forceinline__ int64_t col(int64_t u) const { return grouped ? u : u / mtr; }
+  __device__ __forceinline__ int mt(int64_t u) const {
+    return msplit ? int(m_lo + u / ncols) : (grouped ? member : int(u % mtr));
+  }
+  __device__ __forceinline__ int64_t col(int64_t u) const { return msplit ? u % ncols : (grouped ? u : u / mtr); }
 };
+
+// Expert-grouped GEMMs: each XCD takes a contiguous eighth of the M tiles (consecutive experts'
+// buckets) with all their columns, columns fastest, so an M tile's gathered rows are read into
+// that XCD's L2 once for all its N tiles and each expert's weights are read by one or two XCDs.
+__device__ __forceinline__ TileWalk tile_walk_msplit(int64_t mtr, int n_tiles, int ksplit, int P) {
+  TileWalk w{};
+  w.msplit = true;
+  w.mtr = int(mtr);
+  w.n_tiles = n_tiles;
+  w.ncols = int64_t(n_tiles) * ksplit;
+  const int x = blockIdx.x & 7, local = blockIdx.x >> 3, nloc = P >> 3;
+  w.m_lo = mtr * x / 8;
+  w.t = local;
+  w.t_end = (mtr * (x + 1) / 8 - w.m_lo) * w.ncols;
+  w.stride = nloc;
+  return w;
+}
 
 __device__ __forceinline__ TileWalk tile_walk(int64_t mtr, int n_tiles, int ksplit, int P, bool allow_grouped) {
   TileWalk w{};
@@ -445,7 +465,9 @@ void gemm_kernel(GemmArgs g) {
   // grouped walks for the SwiGLU GEMM only: measured on the Store GEMMs (down projection with
   // split-K, K/V projection) they were 1-3 % slower, while the gate_up GEMM keeps its time and
   // fetches 5 % less from HBM
-  const TileWalk tw = tile_walk(cdiv(M, BM), n_tiles, g.ksplit, gridDim.x, EPI == GemmEpi::SwiGLU);
+  const TileWalk tw = (g.tile_expert && (gridDim.x & 7) == 0)
+                          ? tile_walk_msplit(cdiv(M, BM), n_tiles, g.ksplit, gridDim.x)
+                          : tile_walk(cdiv(M, BM), n_tiles, g.ksplit, gridDim.x, EPI == GemmEpi::SwiGLU);
   constexpr int CA = BM / (16 * WGN);
   int64_t rows[CA], rows_next[CA];
   if constexpr (EPI == GemmEpi::SwiGLU) {
