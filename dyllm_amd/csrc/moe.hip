@@ -15,17 +15,19 @@
 
 namespace dyllm {
 
-// ---- router: 32 tokens per workgroup on the matrix cores ----------------------------------
-// E <= 64 experts, hidden a multiple of 16. logits[32 tokens][64 experts] = X W^T with
-// v_mfma_f32_32x32x16_bf16 (exact bf16 products, fp32 sums): wavefront w takes the experts
+// ---- router: 16 tokens per workgroup on the matrix cores ----------------------------------
+// E <= 64 experts, hidden a multiple of 16. logits[16 tokens][64 experts] = X W^T with
+// v_mfma_f32_32x32x16_bf16 (rows 16-31 of the 32-row tile zero: 16 tokens per workgroup put
+// 231 workgroups on the 256 CUs at config 3, where 32 left half of them idle and ran the softmax
+// and top-k of twice as many tokens per CU: 27.6 -> 20.5 us) (exact bf16 products, fp32 sums): wavefront w takes the experts
 // [32 (w & 1), +32) over one eighth of the hidden dimension (w >> 1), straight from global
 // memory (each lane a 16-byte piece of its token row and of its expert row per 16-wide step, the
 // next four steps loaded while the current four are multiplied); the eighths are added through
 // LDS in a fixed order. (Config 3, 3686 tokens: 169 us for the former wavefront-per-token kernel,
 // 70 / 46 / 35 us with the hidden dimension split in 2 / 4 / 8.) Then one wavefront per token: lane e holds expert e's logit for the softmax
-// and the top-k. (The logits' fp32 sums run in the matrix cores' order, not element by element:
+// and the top-k (each lane counts the experts ranked before its own: no dependent shuffle chain). (The logits' fp32 sums run in the matrix cores' order, not element by element:
 // rounding-level differences, which move the top-k only at near-ties.)
-constexpr int kRouterTok = 32;
+constexpr int kRouterTok = 16;   // tokens per workgroup (rows 16-31 of the 32-row MFMA tile are zero)
 constexpr int kRouterU = 4;
 constexpr int kRouterKS = 8;                       // hidden-dimension slices
 constexpr int kRouterThreads = 128 * kRouterKS;    // 2 expert halves x kRouterKS slices
@@ -45,7 +47,7 @@ __global__ __launch_bounds__(kRouterThreads) void moe_router_kernel(const uint16
   const int eh = w & 1, kh = w >> 1;
   const int64_t t0 = int64_t(blockIdx.x) * kRouterTok;
   const int64_t ta = t0 + ql;
-  const bool a_ok = ta < T;
+  const bool a_ok = ql < kRouterTok && ta < T;
   const int64_t xr = a_ok ? (rows ? int64_t(rows[ta]) : ta) : 0;
   const int eb = 32 * eh + ql;
   const bool b_ok = eb < E;
@@ -81,7 +83,10 @@ __global__ __launch_bounds__(kRouterThreads) void moe_router_kernel(const uint16
   }
   // C layout: lane (ql, half) holds expert column ql, token rows (r / 4) * 8 + half * 4 + r % 4
 #pragma unroll
-  for (int r = 0; r < 16; ++r) part[kh][(r >> 2) * 8 + half * 4 + (r & 3)][32 * eh + ql] = acc[r];
+  for (int r = 0; r < 16; ++r) {
+    const int tr = (r >> 2) * 8 + half * 4 + (r & 3);
+    if (tr < kRouterTok) part[kh][tr][32 * eh + ql] = acc[r];
+  }
   __syncthreads();
   for (int r = w; r < kRouterTok; r += kRouterThreads / 64) {
     const int64_t t = t0 + r;
@@ -95,30 +100,24 @@ __global__ __launch_bounds__(kRouterThreads) void moe_router_kernel(const uint16
     const float mx = wave_max(logit);
     const float e = (lane < E) ? expf(logit - mx) : 0.f;
     const float sum = wave_sum(e);
-    float p = (lane < E) ? e / sum : -1.0f;
-    // top-k: repeated wave argmax, lowest expert index wins ties (torch.topk order is
-    // unspecified for exact ties)
+    const float p = (lane < E) ? e / sum : -1.0f;
+    // top-k in descending probability, lowest expert index first among exact ties (torch.topk
+    // order is unspecified for exact ties): each lane counts the experts ranked before its own
+    // from wave-uniform reads of every lane's probability (no dependent shuffle chain); the
+    // k best then sum in rank order, as an iterative argmax would add them
+    const float pv = p;
+    int rank = 0;
+    for (int j = 0; j < E; ++j) {
+      const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), j));
+      rank += (pj > pv || (pj == pv && j < lane)) ? 1 : 0;
+    }
+    const int my_rank = (lane < E && rank < top_k) ? rank : -1;
+    const float my_w = pv;
     float picked_sum = 0.f;
-    float my_w = 0.f;
-    int my_rank = -1;
     for (int k = 0; k < top_k; ++k) {
-      float best = p;
-      int bi = lane;
-  #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ob = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ob > best || (ob == best && oi < bi)) {
-          best = ob;
-          bi = oi;
-        }
-      }
-      if (lane == bi) {
-        my_rank = k;
-        my_w = p;
-        p = -2.0f;
-      }
-      picked_sum += best;
+      const unsigned long long who = __ballot(my_rank == k);
+      const int src = __builtin_ctzll(who);
+      picked_sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pv), src));
     }
     if (my_rank >= 0) {
       const float wv = renorm ? my_w / picked_sum : my_w;
