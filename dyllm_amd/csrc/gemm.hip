@@ -133,7 +133,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   // address arithmetic. Offsets are 32-bit: every operand spans less than 4 GiB (checked on the
   // host where the extent is known).
   uint32_t a_vo[CA];
-  if constexpr (EPI == GemmEpi::SwiGLU) {
+  if (EPI == GemmEpi::SwiGLU || g.tile_expert) {   // rows looked up by the caller (during the previous tile)
 #pragma unroll
     for (int i = 0; i < CA; ++i) a_vo[i] = uint32_t((rows[i] * g.lda + lane_chunk) * 2);
   } else {
@@ -257,9 +257,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
   __builtin_amdgcn_s_barrier();
   // the next tile's source rows: issued before every load of the K loop, so the loop's vmcnt
   // waits complete them as well
-  if constexpr (EPI == GemmEpi::SwiGLU) {
-    if (mt_next >= 0) gemm_tile_rows<BM, WGN>(g, M, mt_next, w, lrow, rows_next);
-  }
+  if (mt_next >= 0) gemm_tile_rows<BM, WGN>(g, M, mt_next, w, lrow, rows_next);
   int wcur = 0;   // kt % 3
   // The last K substep of each slice is carried across the slice's barrier: its fragments are
   // read before the barrier and its MFMAs issued after it, while the first fragment reads of the
@@ -470,7 +468,10 @@ void gemm_kernel(GemmArgs g) {
                           : tile_walk(cdiv(M, BM), n_tiles, g.ksplit, gridDim.x, EPI == GemmEpi::SwiGLU);
   constexpr int CA = BM / (16 * WGN);
   int64_t rows[CA], rows_next[CA];
-  if constexpr (EPI == GemmEpi::SwiGLU) {
+  // the SwiGLU and the expert-grouped GEMMs look each tile's source rows up during the previous
+  // tile's K loop (the dense Store GEMMs measured 2-5 % slower with it and look them up per tile)
+  const bool row_ahead = EPI == GemmEpi::SwiGLU || g.tile_expert != nullptr;
+  if (row_ahead) {
     if (tw.valid())
       gemm_tile_rows<BM, WGN>(g, M, tw.mt(tw.t), __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6),
                               (threadIdx.x & 63) >> 3, rows);
@@ -482,13 +483,11 @@ void gemm_kernel(GemmArgs g) {
     const int kz = int(c / n_tiles);
     // the SwiGLU tile looks the next tile's source rows up during its K loop (grouped walks keep
     // one M tile, whose rows are already in place)
-    const int mt_next = (EPI == GemmEpi::SwiGLU && !tw.grouped && u + tw.stride < tw.t_end) ? tw.mt(u + tw.stride) : -1;
+    const int mt_next = (row_ahead && !tw.grouped && u + tw.stride < tw.t_end) ? tw.mt(u + tw.stride) : -1;
     gemm_tile<BM, BN, WGN, EPI>(g, M, mt, nt, kz, rows, mt_next, rows_next);
-    if constexpr (EPI == GemmEpi::SwiGLU) {
-      if (mt_next >= 0) {
+    if (mt_next >= 0) {
 #pragma unroll
-        for (int i = 0; i < CA; ++i) rows[i] = rows_next[i];
-      }
+      for (int i = 0; i < CA; ++i) rows[i] = rows_next[i];
     }
   }
 }
