@@ -76,3 +76,25 @@ def test_swiglu_silu_within_one_ulp(dev):
     ulp2 = torch.ldexp(torch.ones_like(want2), torch.frexp(want2.abs().clamp_min(2.0 ** -126))[1] - 8)
     bad2 = (h2 - want2).abs() > ulp2
     assert not bad2.any(), f"silu_and_mul: {int(bad2.sum())} values off by more than one bf16 ulp"
+
+
+def test_silu_and_mul_strided_rows(dev):
+    """dyllm_silu_and_mul through the C ABI on padded row strides (ld_in > 2I, ld_out > I) and an
+    odd row count: every output element equals bf16(silu(g) * u) within one bf16 ulp of the fp32
+    reference, and the padding columns of the output rows are left untouched."""
+    from dyllm_amd import _lib, ops
+
+    rows, inter, pad_in, pad_out = 37, 136, 16, 24
+    g = torch.Generator().manual_seed(11)
+    gu = (torch.randn(rows, 2 * inter + pad_in, generator=g) * 3).to(BF)
+    sentinel = torch.full((rows, inter + pad_out), 5.0).to(BF)
+    out = sentinel.to(dev)
+    gud = gu.to(dev)
+    _lib.call("dyllm_silu_and_mul", gud.data_ptr(), gu.shape[1], rows, inter, out.data_ptr(), out.shape[1], ops._stream())
+    got = out.cpu()
+    assert torch.equal(got[:, inter:], sentinel[:, inter:]), "padding columns were written"
+    gf, uf = gu[:, :inter].float(), gu[:, inter:2 * inter].float()
+    want = (gf / (1.0 + torch.exp(-gf)) * uf).to(BF).float()
+    ulp = torch.ldexp(torch.ones_like(want), torch.frexp(want.abs().clamp_min(2.0 ** -126))[1] - 8)
+    bad = (got[:, :inter].float() - want).abs() > ulp
+    assert not bad.any(), f"{int(bad.sum())} values off by more than one bf16 ulp"
