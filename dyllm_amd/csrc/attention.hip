@@ -39,8 +39,8 @@ constexpr int kVStride = kBK + 12;   // V^T tile row stride (elements): 152 B, c
 constexpr int kMaxBlk2 = 64;
 struct ColSparseLds {
   float* m;          // [NW][kMaxBlk2][32] running max of each query row after each key block
-  int16_t* keys;     // [kMaxBlk2 * kBK] salient keys in 16-slot groups, -1 = padding
-  uint8_t* gblk;     // [4 * kMaxBlk2] key block of each group
+  int16_t* keys;     // [kMaxBlk2 * kBK] salient keys in groups of kGroupSlots<CHUNKED>, -1 = padding
+  uint8_t* gblk;     // [8 * kMaxBlk2] key block of each group
   int* ngrp;         // number of groups
   float* xch;        // [NW][96] pass-1 partials exchanged between the waves of a pair (64 sums, 32 maxima)
   // maps built from the compact salient lists (AttnArgs::sal_k):
@@ -48,6 +48,15 @@ struct ColSparseLds {
   int* sblk;                  // [kMaxBlk2] dV row of group slot sl in block kb = cu_sal[b] + sblk[kb] + sl
   uint32_t* rowflag;          // [NW] salient bits of the tile's query rows (32 per wavefront)
 };
+
+// Key slots per pass-2 group: 16 (v_mfma_f32_32x32x16_bf16 for PV) for rows that fit the LDS max
+// table, 8 (v_mfma_f32_32x32x8_bf16, half the keys per product) for the chunked long rows, whose
+// sparse blocks hold a few salient keys each (config 4: about 3 per 64-key block), so half-size
+// groups halve pass 2's padding: its score recomputation, staging and exponentials.
+template <bool CHUNKED>
+constexpr int kGroupSlots = CHUNKED ? 8 : 16;
+
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4_t;
 
 union Pack8 {
   bf16x8_t v;
@@ -88,6 +97,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
   const int64_t kv0 = a.k_seq_starts ? a.k_seq_starts[sid] : (a.kv_start ? a.kv_start[b] : int64_t(k_beg));
   // salient lists of this sequence (fused step: the column-sparse maps are built from them)
   constexpr bool lists = MODE == AttnMode::ColSparse && LISTS;
+  constexpr int GS = kGroupSlots<CHUNKED>;   // pass-2 key slots per group
   const int s_beg = lists ? a.cu_sal[b] : 0, s_end = lists ? a.cu_sal[b + 1] : 0;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -334,7 +344,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       if (lane < nkc) {
         word = lists ? sp.kbits[lane] : a.kmask[int64_t(b) * a.nblk + kb0 + lane];
         if (kb0 + lane == nkb - 1 && (Lk & (kBK - 1))) word &= (1ull << (Lk & (kBK - 1))) - 1;   // keys < Lk only
-        grp = (__popcll(word) + 15) >> 4;
+        grp = (__popcll(word) + GS - 1) / GS;
       }
       int inc = grp;
       int pinc = __popcll(word);
@@ -350,14 +360,14 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
       const int g0 = inc - grp;
       if (lane == 63) *sp.ngrp = inc;
       // dV row of group slot sl of this block: the key's rank among the sequence's salient keys
-      if (lists && lane < nkc) sp.sblk[lane] = keys_before + (pinc - __popcll(word)) - 16 * g0;
+      if (lists && lane < nkc) sp.sblk[lane] = keys_before + (pinc - __popcll(word)) - GS * g0;
       int n = 0;
       while (word) {
-        sp.keys[g0 * 16 + n] = int16_t(lane * kBK + __builtin_ctzll(word));
+        sp.keys[g0 * GS + n] = int16_t(lane * kBK + __builtin_ctzll(word));
         word &= word - 1;
         ++n;
       }
-      for (; n < grp * 16; ++n) sp.keys[g0 * 16 + n] = -1;
+      for (; n < grp * GS; ++n) sp.keys[g0 * GS + n] = -1;
       for (int j = 0; j < grp; ++j) sp.gblk[g0 + j] = uint8_t(lane);
     };
     // pass 2's accumulator state, carried from chunk to chunk
@@ -366,10 +376,11 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
     auto pass2 = [&](int kb0, int ngrp) {
       // ---- pass 2 ---- over the groups of blocks kb0 .. (ngrp groups, read before the barrier
       // that precedes this call)
-      const int npb = (ngrp + 3) >> 2;
+      constexpr int GPB = kBK / GS;   // groups per 64-slot pass block
+      const int npb = (ngrp + GPB - 1) / GPB;
       // slots past the last group (the tail of the last 64-slot block) were never written
       auto slot_key = [&](int sl) -> int {
-        const int kr = sl < ngrp * 16 ? int(sp.keys[sl]) : -1;
+        const int kr = sl < ngrp * GS ? int(sp.keys[sl]) : -1;
         return kr < 0 ? -1 : kb0 * kBK + kr;
       };
       auto load_meta2 = [&](int pb) {
@@ -381,7 +392,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
           for (int j = 0; j < 4; ++j) {
             const int sl = pb * kBK + 4 * kq + j;
             const int key = slot_key(sl);
-            meta_slot[it][j] = key < 0 ? -1 : (lists ? s_beg + sp.sblk[sp.gblk[sl >> 4]] + sl : (ks_b ? ks_b[key] : key));
+            meta_slot[it][j] = key < 0 ? -1 : (lists ? s_beg + sp.sblk[sp.gblk[sl / GS]] + sl : (ks_b ? ks_b[key] : key));
           }
         }
       };
@@ -417,8 +428,8 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int g = pb * 4 + t * 2 + u;
+          for (int u = 0; u < 32 / GS; ++u) {
+            const int g = pb * GPB + t * (32 / GS) + u;
             if (g >= ngrp) continue;
             const int blkl = __builtin_amdgcn_readfirstlane(int(sp.gblk[g]));
             const int blk = kb0 + blkl;
@@ -437,6 +448,26 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
               blk_prev = blk;
             }
             const float m2 = m_g * c2;
+            if constexpr (GS == 8) {
+              // the group's 8 keys are rows 8u .. 8u+7 of the 32-key score half: this lane holds
+              // keys 8u + 4*half + 0..3 in registers 4u .. 4u+3, the layout of the 32x32x8 B operand
+              Pack4 p;
+#pragma unroll
+              for (int j = 0; j < 2; ++j) {
+                const float e0 = __builtin_amdgcn_exp2f(fmaf(sa[t][4 * u + 2 * j], c2, -m2));
+                const float e1 = __builtin_amdgcn_exp2f(fmaf(sa[t][4 * u + 2 * j + 1], c2, -m2));
+                p.u[j] = pack_bf16x2(e0, e1);
+              }
+              const int kofs8 = t * 32 + u * 8 + half * 4;
+#pragma unroll
+              for (int dt = 0; dt < 4; ++dt) {
+                Pack4 va;
+                va.d = *reinterpret_cast<const uint2*>(&vt_lds[(dt * 32 + ql) * kVStride + kofs8]);
+                o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(__builtin_bit_cast(s16x4_t, va.d),
+                                                                      __builtin_bit_cast(s16x4_t, p.d), o_acc[dt], 0, 0, 0);
+              }
+              continue;
+            } else {
             Pack8 p;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -457,6 +488,7 @@ __device__ __forceinline__ void attention_tile(const AttnArgs& a, int wg, uint16
               va.u[2] = hi.u[0];
               va.u[3] = hi.u[1];
               o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va.v, p.v, o_acc[dt], 0, 0, 0);
+            }
             }
           }
         }
@@ -884,7 +916,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   if constexpr (MODE == AttnMode::ColSparse) {
     __shared__ float m_lds[NW * kMaxBlk2 * 32];
     __shared__ int16_t key_lds[kMaxBlk2 * kBK];
-    __shared__ uint8_t gblk_lds[4 * kMaxBlk2];
+    __shared__ uint8_t gblk_lds[8 * kMaxBlk2];
     __shared__ int ngrp_lds;
     __shared__ float xch_lds[NW * 96];
     attention_tile<MODE, NW>(a, xcd_remap(blockIdx.x, gridDim.x), k_lds, vt_lds,
@@ -905,7 +937,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[kD * kVStride];
   __shared__ float m_lds[NW * kMaxBlk2 * 32];
   __shared__ int16_t key_lds[kMaxBlk2 * kBK];
-  __shared__ uint8_t gblk_lds[4 * kMaxBlk2];
+  __shared__ uint8_t gblk_lds[8 * kMaxBlk2];
   __shared__ int ngrp_lds;
   __shared__ float xch_lds[NW * 96];
   __shared__ unsigned long long kbits_lds[kMaxBlk2];
