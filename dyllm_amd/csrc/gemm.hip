@@ -463,13 +463,13 @@ void gemm_kernel(GemmArgs g) {
   // grouped walks for the SwiGLU GEMM only: measured on the Store GEMMs (down projection with
   // split-K, K/V projection) they were 1-3 % slower, while the gate_up GEMM keeps its time and
   // fetches 5 % less from HBM
-  // the Store GEMMs take the M-split walk too when it leaves the busiest XCD fewer tiles than
+  // the dense GEMMs take the M-split walk too when it leaves the busiest XCD fewer tiles than
   // the column ranges do (e.g. 14 columns over 8 XCDs: ranges of 2 columns x all M tiles
   // overflow 28 workgroups per XCD into a second round, eighths of the M tiles do not)
   const int64_t m_tiles = cdiv(M, BM), cols = int64_t(n_tiles) * g.ksplit;
   const bool msplit = (gridDim.x & 7) == 0 &&
                       (g.tile_expert != nullptr ||
-                       (EPI == GemmEpi::Store && cdiv(m_tiles, 8) * cols < cdiv(cols, 8) * m_tiles));
+                       (cdiv(m_tiles, 8) * cols < cdiv(cols, 8) * m_tiles));
   const TileWalk tw = msplit
                           ? tile_walk_msplit(m_tiles, n_tiles, g.ksplit, gridDim.x)
                           : tile_walk(m_tiles, n_tiles, g.ksplit, gridDim.x, EPI == GemmEpi::SwiGLU);
