@@ -391,6 +391,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int64_t M, int mt, 
 //     group always computes M tile i, and a group walks its share of the XCD's columns. The M
 //     tiles of a column start together and stream its weight slice in step (one HBM read of it,
 //     the others hitting L2), and a workgroup's gathered A rows never change;
+//   * M-split (the expert-grouped GEMMs always; the dense ones when it leaves the busiest XCD
+//     fewer tiles): each XCD takes a contiguous eighth of the M tiles with all their columns,
+//     columns fastest;
 //   * otherwise the XCD's tiles in order (M fastest, then N tile, then split-K slice), one per
 //     workgroup per round.
 struct TileWalk {
