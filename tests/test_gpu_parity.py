@@ -314,9 +314,10 @@ def test_attention_sparse_varlen_shapes(dev, lens, sal_frac, H, Hkv):
 # FFN / MoE
 # ---------------------------------------------------------------------------------------
 # (400, 3584, 512): Dream's hidden size, whose 14 down-projection column tiles leave tile counts
-# below the CU count that are not a multiple of 8
+# below the CU count that are not a multiple of 8; (600, 256, 11008) and (1600, 1024, 1536): the
+# down projection (both) and the gate_up GEMM (the latter) take the M-split tile walk
 @pytest.mark.parametrize("M,hidden,inter", [(77, 256, 512), (300, 512, 384), (600, 256, 11008), (920, 4096, 1024),
-                                            (1500, 1024, 2048), (400, 3584, 512)])
+                                            (1500, 1024, 2048), (400, 3584, 512), (1600, 1024, 1536)])
 def test_swiglu_ffn_gathered(dev, M, hidden, inter):
     ops = _ops()
     g = _gen(M)
