@@ -326,8 +326,9 @@ int dyllm_swiglu_ffn(const void* x, int64_t ld_x, const int32_t* rows_idx, int64
 /* SiLU-and-mul of a merged gate_up product (SiluAndMul, activations.py:11-14): for m < rows,
  * out[m][j] = bf16(silu(g) * u) in fp32 with g = gate_up[m][j], u = gate_up[m][intermediate + j]
  * (bf16; row strides ld_in >= 2*intermediate and ld_out >= intermediate, multiples of 8; both
- * buffers 16-byte aligned). The same arithmetic as the SwiGLU epilogue of dyllm_ffn_gate_up, for
- * a gate_up product computed by another GEMM (the dense full step runs the library GEMM). */
+ * buffers 16-byte aligned; out must not overlap gate_up). The same arithmetic as the SwiGLU
+ * epilogue of dyllm_ffn_gate_up, for a gate_up product computed by another GEMM (the dense full
+ * step runs the library GEMM). */
 int dyllm_silu_and_mul(const void* gate_up, int64_t ld_in, int64_t rows, int intermediate, void* out, int64_t ld_out,
                        void* stream);
 
